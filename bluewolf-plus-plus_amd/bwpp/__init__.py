@@ -1,0 +1,19 @@
+"""bwpp -- Python host side of libbwpp_hip, the MI355X backend of BW++.
+
+The compute path is the C library libbwpp_hip.so and its gfx950 code
+objects (lib/); this package only binds them.  There is no CPU fallback:
+if the library or a code object is missing, HipBackend() raises.
+"""
+from . import _lib, synth
+from ._lib import (AttentionParams, DType, Epilogue, LibraryMissing,
+                   MatmulParams, ReduceParams, RmsnormParams, SoftmaxParams,
+                   Status)
+from .backend import BwppError, HipBackend
+
+__all__ = ["HipBackend", "BwppError", "LibraryMissing", "Status", "DType",
+           "Epilogue", "MatmulParams", "SoftmaxParams", "RmsnormParams",
+           "AttentionParams", "ReduceParams", "synth", "load_library"]
+
+
+def load_library():
+    return _lib.load()

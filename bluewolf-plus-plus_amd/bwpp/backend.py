@@ -1,0 +1,122 @@
+"""Python host mirror of libbwpp_hip's operator interface.
+
+`HipBackend.dispatch_*` keep the argument order of the reference's Metal
+dispatch functions (runtime/metal/dispatch_stub.h:42-74): buffers first, then
+the params struct.  The Metal device/queue pair becomes the backend handle and
+the MSL source argument disappears (kernels are prebuilt code objects).
+Buffers are torch tensors on the GPU or raw device addresses (int); None is
+NULL.  Every call raises BwppError on a non-OK status instead of returning
+silently as the Metal stub does (dispatch_stub.m:66-79).
+"""
+from __future__ import annotations
+
+import ctypes
+
+from . import _lib
+from ._lib import (AttentionParams, MatmulParams, ReduceParams, RmsnormParams,
+                   SoftmaxParams, Status)
+
+
+class BwppError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        self.status = Status(status) if status in Status._value2member_map_ else status
+        super().__init__(f"{self.status!s}: {message}")
+
+
+def _ptr(buf) -> int | None:
+    if buf is None:
+        return None
+    if isinstance(buf, int):
+        return buf
+    if hasattr(buf, "data_ptr"):
+        if not buf.is_cuda:
+            raise ValueError("libbwpp_hip operators take device buffers")
+        return buf.data_ptr()
+    raise TypeError(f"cannot pass {type(buf)!r} as a device buffer")
+
+
+class HipBackend:
+    """One libbwpp_hip handle (device, loaded code objects, stream)."""
+
+    def __init__(self, device: int = 0, code_object_dir: str | None = None,
+                 stream=None):
+        self.lib = _lib.load()
+        h = ctypes.c_void_p()
+        st = self.lib.bwpp_hip_create(
+            ctypes.byref(h), device,
+            code_object_dir.encode() if code_object_dir else None)
+        if st != 0:
+            raise BwppError(st, self.lib.bwpp_hip_last_error(None).decode())
+        self._h = h
+        self.device = device
+        if stream is not None:
+            self.set_stream(stream)
+
+    # ------------------------------------------------------------ handle
+    def close(self):
+        if getattr(self, "_h", None):
+            self.lib.bwpp_hip_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, st: int):
+        if st != 0:
+            raise BwppError(st, self.lib.bwpp_hip_last_error(self._h).decode())
+
+    def set_stream(self, stream):
+        """stream: torch.cuda.Stream, a raw hipStream_t (int) or None."""
+        raw = getattr(stream, "cuda_stream", stream)
+        self._check(self.lib.bwpp_hip_set_stream(self._h, raw or None))
+
+    def stream(self) -> int:
+        return self.lib.bwpp_hip_get_stream(self._h) or 0
+
+    def sync(self):
+        self._check(self.lib.bwpp_hip_sync(self._h))
+
+    @property
+    def cus(self) -> int:
+        return self.lib.bwpp_hip_device_cus(self._h)
+
+    # --------------------------------------------------------- operators
+    def dispatch_matmul(self, a, b, c, bias, params: MatmulParams):
+        self._check(self.lib.bwpp_hip_dispatch_matmul(
+            self._h, _ptr(a), _ptr(b), _ptr(c), _ptr(bias), params))
+
+    def dispatch_softmax(self, x, y, params: SoftmaxParams):
+        self._check(self.lib.bwpp_hip_dispatch_softmax(
+            self._h, _ptr(x), _ptr(y), params))
+
+    def dispatch_rmsnorm(self, x, gamma, beta, y, params: RmsnormParams):
+        self._check(self.lib.bwpp_hip_dispatch_rmsnorm(
+            self._h, _ptr(x), _ptr(gamma), _ptr(beta), _ptr(y), params))
+
+    def dispatch_layernorm(self, x, gamma, beta, y, params: RmsnormParams):
+        self._check(self.lib.bwpp_hip_dispatch_layernorm(
+            self._h, _ptr(x), _ptr(gamma), _ptr(beta), _ptr(y), params))
+
+    def dispatch_attention(self, q, k, v, o, params: AttentionParams):
+        self._check(self.lib.bwpp_hip_dispatch_attention(
+            self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(o), params))
+
+    def dispatch_reduce_max(self, x, maxv, argmax, params: ReduceParams):
+        self._check(self.lib.bwpp_hip_dispatch_reduce_max(
+            self._h, _ptr(x), _ptr(maxv), _ptr(argmax), params))
+
+    def dispatch_reduce_max_mask(self, x, mask, params: ReduceParams):
+        self._check(self.lib.bwpp_hip_dispatch_reduce_max_mask(
+            self._h, _ptr(x), _ptr(mask), params))
+
+    def dispatch_reduce_max_grad(self, mask, dy, dx, params: ReduceParams):
+        self._check(self.lib.bwpp_hip_dispatch_reduce_max_grad(
+            self._h, _ptr(mask), _ptr(dy), _ptr(dx), params))
+
+    def dispatch_reduce_max_grad_argmax(self, x, argmax, dy, dx,
+                                        params: ReduceParams):
+        self._check(self.lib.bwpp_hip_dispatch_reduce_max_grad_argmax(
+            self._h, _ptr(x), _ptr(argmax), _ptr(dy), _ptr(dx), params))

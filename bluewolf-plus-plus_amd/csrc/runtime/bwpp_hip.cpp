@@ -1,0 +1,510 @@
+// libbwpp_hip host runtime: code-object loading, the kernel handle cache,
+// argument validation, launch geometry and the device arena.
+//
+// Replaces runtime/metal/dispatch_stub.m.  Where the Metal stub compiles MSL
+// at first dispatch and keeps one function-static PSO per op
+// (dispatch_stub.m:6-56, 81), this layer loads prebuilt gfx950 code objects
+// once per handle with hipModuleLoad and resolves every kernel symbol up
+// front, so a missing kernel is an error at bwpp_hip_create() and never a
+// silent no-op at dispatch time (dispatch_stub.m:94-98).
+#include "bwpp_hip.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <dlfcn.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../kargs.h"
+
+namespace {
+
+thread_local std::string g_create_error;
+
+// Code objects built by the package Makefile, all required.
+const char *const kModules[] = {"bwpp_rowops.hsaco"};
+
+// Row-op kernels: bwpp_row_<op>_v<VPT>_w<WPR>_<f|p>, see rowops.hip.
+enum RowOpId { ROW_SOFTMAX, ROW_RMSNORM, ROW_LAYERNORM, ROW_MAX, ROW_MAXGRAD, ROW_MASK, ROW_NOPS };
+const char *const kRowOpNames[ROW_NOPS] = {"softmax", "rmsnorm", "layernorm", "max", "maxgrad", "mask"};
+// (float4 chunks per thread, waves per row); same list as BWPP_ROW_ALL_CFG.
+struct RowCfg {
+  int vpt;
+  int wpr;
+};
+constexpr int kRowNCfg = 17;
+const RowCfg kRowCfgs[kRowNCfg] = {{1, 1}, {2, 1}, {4, 1}, {8, 1}, {16, 1}, {2, 2}, {4, 2}, {8, 2}, {1, 4},
+                                   {2, 4}, {4, 4}, {8, 4}, {16, 4}, {2, 8}, {4, 8}, {8, 8}, {16, 8}};
+inline uint32_t row_capacity(const RowCfg &c) { return 256u * (uint32_t)c.wpr * (uint32_t)c.vpt; }
+inline uint32_t row_block(const RowCfg &c) { return c.wpr >= 4 ? 64u * (uint32_t)c.wpr : 256u; }
+inline uint32_t row_rows_per_block(const RowCfg &c) { return row_block(c) / (64u * (uint32_t)c.wpr); }
+int find_cfg(int vpt, int wpr) {
+  for (int i = 0; i < kRowNCfg; ++i)
+    if (kRowCfgs[i].vpt == vpt && kRowCfgs[i].wpr == wpr) return i;
+  return -1;
+}
+
+}  // namespace
+
+struct BwppHip {
+  int device = 0;
+  int cus = 0;
+  hipStream_t stream = nullptr;
+  std::vector<hipModule_t> modules;
+  std::string err;
+  int row_cfg_override = -1;  // BWPP_ROW_CFG: index into kRowCfgs (tuning)
+  uint32_t row_grid_cap = 0;  // BWPP_ROW_GRID: max blocks per row launch (0 = per-op default)
+
+  hipFunction_t row_reg[ROW_NOPS][kRowNCfg][2] = {};
+  hipFunction_t row_gen[ROW_NOPS] = {};
+  hipFunction_t row_maxgrad_idx = nullptr;
+  hipFunction_t row_maxgrad_idx_v4 = nullptr;
+  hipFunction_t row_maskgrad = nullptr;
+  hipFunction_t col_maskgrad = nullptr;
+  hipFunction_t col_max = nullptr;
+  hipFunction_t col_maxgrad = nullptr;
+  hipFunction_t col_mask = nullptr;
+};
+
+namespace {
+
+BwppHipStatus fail(BwppHip *h, BwppHipStatus s, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (h)
+    h->err = buf;
+  else
+    g_create_error = buf;
+  return s;
+}
+
+BwppHipStatus resolve(BwppHip *h, const std::string &name, hipFunction_t *out) {
+  for (hipModule_t m : h->modules) {
+    hipFunction_t f = nullptr;
+    if (hipModuleGetFunction(&f, m, name.c_str()) == hipSuccess && f) {
+      *out = f;
+      return BWPP_HIP_OK;
+    }
+  }
+  (void)hipGetLastError();  // clear the lookup misses
+  return fail(h, BWPP_HIP_ERR_NO_KERNEL, "kernel %s not found in any loaded code object", name.c_str());
+}
+
+BwppHipStatus resolve_all(BwppHip *h) {
+  BwppHipStatus s;
+  for (int op = 0; op < ROW_NOPS; ++op) {
+    for (int c = 0; c < kRowNCfg; ++c) {
+      for (int full = 0; full < 2; ++full) {
+        std::string n = std::string("bwpp_row_") + kRowOpNames[op] + "_v" + std::to_string(kRowCfgs[c].vpt) +
+                        "_w" + std::to_string(kRowCfgs[c].wpr) + (full ? "_f" : "_p");
+        if ((s = resolve(h, n, &h->row_reg[op][c][full])) != BWPP_HIP_OK) return s;
+      }
+    }
+    if ((s = resolve(h, std::string("bwpp_row_") + kRowOpNames[op] + "_gen", &h->row_gen[op])) != BWPP_HIP_OK)
+      return s;
+  }
+  struct {
+    const char *name;
+    hipFunction_t *slot;
+  } singles[] = {
+      {"bwpp_row_maxgrad_idx", &h->row_maxgrad_idx}, {"bwpp_row_maxgrad_idx_v4", &h->row_maxgrad_idx_v4},
+      {"bwpp_row_maskgrad", &h->row_maskgrad},       {"bwpp_col_maskgrad", &h->col_maskgrad},
+      {"bwpp_col_max", &h->col_max},                 {"bwpp_col_maxgrad", &h->col_maxgrad},
+      {"bwpp_col_mask", &h->col_mask},
+  };
+  for (auto &e : singles)
+    if ((s = resolve(h, e.name, e.slot)) != BWPP_HIP_OK) return s;
+  return BWPP_HIP_OK;
+}
+
+std::string library_dir() {
+  Dl_info info;
+  if (dladdr((void *)&bwpp_hip_create, &info) && info.dli_fname) {
+    std::string p(info.dli_fname);
+    size_t slash = p.rfind('/');
+    if (slash != std::string::npos) return p.substr(0, slash);
+  }
+  return ".";
+}
+
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+BwppHipStatus enter(BwppHip *h) {
+  if (!h) return BWPP_HIP_ERR_INVALID_ARG;
+  h->err.clear();
+  hipError_t e = hipSetDevice(h->device);
+  if (e != hipSuccess) return fail(h, BWPP_HIP_ERR_HIP, "hipSetDevice(%d): %s", h->device, hipGetErrorString(e));
+  return BWPP_HIP_OK;
+}
+
+template <class Args>
+BwppHipStatus launch(BwppHip *h, hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx,
+                     const Args &args, uint32_t shmem = 0) {
+  if (gx == 0 || gy == 0 || gz == 0) return BWPP_HIP_OK;
+  void *params[] = {const_cast<Args *>(&args)};
+  hipError_t e = hipModuleLaunchKernel(f, gx, gy, gz, bx, 1, 1, shmem, h->stream, params, nullptr);
+  if (e != hipSuccess) return fail(h, BWPP_HIP_ERR_HIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
+  return BWPP_HIP_OK;
+}
+
+inline uint32_t eff_ld(uint32_t ld, uint32_t cols) { return ld ? ld : cols; }
+
+// Picks the register-resident configuration for one operator on rows of
+// `cols` floats, or -1 for the multi-pass fallback.  Rows up to 512 get one
+// wave each; longer rows get a block of 4 waves (8 for softmax from 4096
+// columns, and for every operator above 16384), with the float4 chunks per
+// thread doubled until the row fits (<= 16, i.e. 32768 columns).  These are
+// the fastest layouts measured on MI355X at 4096 columns.
+int pick_row_cfg(const BwppHip *h, RowOpId op, uint32_t cols, bool vec_ok) {
+  if (!vec_ok) return -1;
+  if (h->row_cfg_override >= 0 && h->row_cfg_override < kRowNCfg &&
+      row_capacity(kRowCfgs[h->row_cfg_override]) >= cols)
+    return h->row_cfg_override;
+  if (cols <= 256) return find_cfg(1, 1);
+  if (cols <= 512) return find_cfg(2, 1);
+  if (cols > 32768) return -1;
+  const int wpr = (cols > 16384 || (op == ROW_SOFTMAX && cols >= 4096)) ? 8 : 4;
+  int vpt = 1;
+  while (row_capacity(RowCfg{vpt, wpr}) < cols) vpt *= 2;
+  return find_cfg(vpt, wpr);
+}
+
+// Launches one row-wise (axis = last) operator.  The norms run a persistent
+// grid of 4 blocks per CU so each block reuses its gamma/beta registers over
+// several rows; the others launch one block per row group.
+BwppHipStatus row_dispatch(BwppHip *h, RowOpId op, const BwppRowArgs &a, bool vec_ok) {
+  const int c = pick_row_cfg(h, op, a.cols, vec_ok);
+  if (c < 0) return launch(h, h->row_gen[op], a.rows, 1, 1, 256, a);
+  const RowCfg &cfg = kRowCfgs[c];
+  const int full = (a.cols == row_capacity(cfg)) ? 1 : 0;
+  const uint32_t rpb = row_rows_per_block(cfg);
+  uint32_t grid = (a.rows + rpb - 1) / rpb;
+  uint32_t cap = h->row_grid_cap;
+  if (cap == 0 && (op == ROW_RMSNORM || op == ROW_LAYERNORM) && h->cus > 0) cap = 4u * (uint32_t)h->cus;
+  if (cap && grid > cap) grid = cap;
+  return launch(h, h->row_reg[op][c][full], grid, 1, 1, row_block(cfg), a);
+}
+
+inline uint32_t stream_grid(uint32_t rows) { return rows < (1u << 20) ? rows : (1u << 20); }
+
+BwppHipStatus check_rows(BwppHip *h, uint32_t rows, uint32_t cols, uint32_t ld) {
+  if (ld < cols) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "ld (%u) < cols (%u)", ld, cols);
+  (void)rows;
+  return BWPP_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *bwpp_hip_status_string(BwppHipStatus s) {
+  switch (s) {
+    case BWPP_HIP_OK: return "ok";
+    case BWPP_HIP_ERR: return "error";
+    case BWPP_HIP_ERR_INVALID_ARG: return "invalid argument";
+    case BWPP_HIP_ERR_HIP: return "HIP runtime error";
+    case BWPP_HIP_ERR_NO_KERNEL: return "kernel or code object missing";
+    case BWPP_HIP_ERR_ALIAS: return "output aliases an input";
+    case BWPP_HIP_ERR_OUT_OF_MEMORY: return "out of device memory";
+    case BWPP_HIP_ERR_UNSUPPORTED: return "unsupported";
+    case BWPP_HIP_ERR_NO_DEVICE: return "no HIP device";
+  }
+  return "unknown status";
+}
+
+BwppHipStatus bwpp_hip_create(BwppHip **out, int device, const char *code_object_dir) {
+  g_create_error.clear();
+  if (!out) return fail(nullptr, BWPP_HIP_ERR_INVALID_ARG, "out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0)
+    return fail(nullptr, BWPP_HIP_ERR_NO_DEVICE, "no HIP device (%s)", e == hipSuccess ? "count 0" : hipGetErrorString(e));
+  if (device < 0 || device >= n)
+    return fail(nullptr, BWPP_HIP_ERR_NO_DEVICE, "device %d out of range (%d devices)", device, n);
+  if ((e = hipSetDevice(device)) != hipSuccess)
+    return fail(nullptr, BWPP_HIP_ERR_HIP, "hipSetDevice(%d): %s", device, hipGetErrorString(e));
+
+  BwppHip *h = new BwppHip();
+  h->device = device;
+  (void)hipDeviceGetAttribute(&h->cus, hipDeviceAttributeMultiprocessorCount, device);
+  if (const char *cfg = getenv("BWPP_ROW_CFG")) h->row_cfg_override = atoi(cfg);
+  if (const char *gc = getenv("BWPP_ROW_GRID")) h->row_grid_cap = (uint32_t)strtoul(gc, nullptr, 10);
+
+  const std::string dir = code_object_dir ? std::string(code_object_dir) : library_dir();
+  for (const char *mod : kModules) {
+    const std::string path = dir + "/" + mod;
+    hipModule_t m = nullptr;
+    e = hipModuleLoad(&m, path.c_str());
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      bwpp_hip_destroy(h);
+      return fail(nullptr, BWPP_HIP_ERR_NO_KERNEL, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
+    }
+    h->modules.push_back(m);
+  }
+  BwppHipStatus s = resolve_all(h);
+  if (s != BWPP_HIP_OK) {
+    g_create_error = h->err;
+    bwpp_hip_destroy(h);
+    return s;
+  }
+  *out = h;
+  return BWPP_HIP_OK;
+}
+
+void bwpp_hip_destroy(BwppHip *h) {
+  if (!h) return;
+  for (hipModule_t m : h->modules) (void)hipModuleUnload(m);
+  delete h;
+}
+
+BwppHipStatus bwpp_hip_set_stream(BwppHip *h, void *hip_stream) {
+  if (!h) return BWPP_HIP_ERR_INVALID_ARG;
+  h->stream = (hipStream_t)hip_stream;
+  return BWPP_HIP_OK;
+}
+
+void *bwpp_hip_get_stream(const BwppHip *h) { return h ? (void *)h->stream : nullptr; }
+
+BwppHipStatus bwpp_hip_sync(BwppHip *h) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  hipError_t e = hipStreamSynchronize(h->stream);
+  if (e != hipSuccess) return fail(h, BWPP_HIP_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+  return BWPP_HIP_OK;
+}
+
+const char *bwpp_hip_last_error(const BwppHip *h) { return h ? h->err.c_str() : g_create_error.c_str(); }
+
+int bwpp_hip_device_cus(const BwppHip *h) { return h ? h->cus : 0; }
+
+// ---------------------------------------------------------------- memory
+
+BwppHipStatus bwpp_hip_arena_init(BwppHip *h, BwppHipArena *arena, size_t capacity) {
+  if (!arena) return BWPP_HIP_ERR_INVALID_ARG;
+  arena->buffer = nullptr;
+  arena->capacity = 0;
+  arena->offset = 0;
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, capacity ? capacity : 1);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(h, BWPP_HIP_ERR_OUT_OF_MEMORY, "hipMalloc(%zu): %s", capacity, hipGetErrorString(e));
+  }
+  arena->buffer = (unsigned char *)p;
+  arena->capacity = capacity;
+  arena->offset = 0;
+  arena->device = h->device;
+  return BWPP_HIP_OK;
+}
+
+void bwpp_hip_arena_reset(BwppHipArena *arena) {
+  if (arena) arena->offset = 0;
+}
+
+void *bwpp_hip_arena_alloc(BwppHipArena *arena, size_t size, size_t align) {
+  if (!arena || !arena->buffer) return nullptr;
+  if (align == 0) align = 1;
+  if (align & (align - 1)) return nullptr;  // power of two only
+  const size_t mask = align - 1;
+  const uintptr_t base = (uintptr_t)arena->buffer;
+  const size_t start = ((base + arena->offset + mask) & ~(uintptr_t)mask) - base;
+  if (start > arena->capacity || size > arena->capacity - start) return nullptr;
+  arena->offset = start + size;
+  return arena->buffer + start;
+}
+
+void bwpp_hip_arena_destroy(BwppHipArena *arena) {
+  if (!arena) return;
+  if (arena->buffer) {
+    (void)hipSetDevice(arena->device);
+    (void)hipFree(arena->buffer);
+  }
+  arena->buffer = nullptr;
+  arena->capacity = 0;
+  arena->offset = 0;
+}
+
+static BwppHipStatus copy(BwppHip *h, void *dst, const void *src, size_t bytes, hipMemcpyKind kind) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (bytes == 0) return BWPP_HIP_OK;
+  if (!dst || !src) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "NULL copy pointer");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, h->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+  if (e != hipSuccess) return fail(h, BWPP_HIP_ERR_HIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
+  return BWPP_HIP_OK;
+}
+
+BwppHipStatus bwpp_hip_copy_to_device(BwppHip *h, void *dst, const void *src, size_t bytes) {
+  return copy(h, dst, src, bytes, hipMemcpyHostToDevice);
+}
+
+BwppHipStatus bwpp_hip_copy_to_host(BwppHip *h, void *dst, const void *src, size_t bytes) {
+  return copy(h, dst, src, bytes, hipMemcpyDeviceToHost);
+}
+
+// ------------------------------------------------------------- row ops
+
+BwppHipStatus bwpp_hip_dispatch_softmax(BwppHip *h, const float *x, float *y, BwppSoftmaxParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!x || !y) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "softmax: NULL x or y");
+  const uint32_t ld = eff_ld(p.ld, p.cols);
+  if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
+  if (p.rows == 0 || p.cols == 0) return BWPP_HIP_OK;
+  BwppRowArgs a = {};
+  a.x = x;
+  a.y = y;
+  a.rows = p.rows;
+  a.cols = p.cols;
+  a.ld = ld;
+  const bool vec = aligned16(x) && aligned16(y) && (ld % 4 == 0);
+  return row_dispatch(h, ROW_SOFTMAX, a, vec);
+}
+
+static BwppHipStatus norm_dispatch(BwppHip *h, RowOpId op, const float *x, const float *gamma, const float *beta,
+                                   float *y, BwppRmsnormParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!x || !y) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "%s: NULL x or y", kRowOpNames[op]);
+  const uint32_t ld = eff_ld(p.ld, p.cols);
+  if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
+  if (p.rows == 0 || p.cols == 0) return BWPP_HIP_OK;
+  BwppRowArgs a = {};
+  a.x = x;
+  a.y = y;
+  a.gamma = gamma;
+  a.beta = beta;
+  a.rows = p.rows;
+  a.cols = p.cols;
+  a.ld = ld;
+  a.eps = p.eps;
+  const bool vec = aligned16(x) && aligned16(y) && (ld % 4 == 0) && (!gamma || aligned16(gamma)) &&
+                   (!beta || aligned16(beta));
+  return row_dispatch(h, op, a, vec);
+}
+
+BwppHipStatus bwpp_hip_dispatch_rmsnorm(BwppHip *h, const float *x, const float *gamma, const float *beta,
+                                        float *y, BwppRmsnormParams p) {
+  return norm_dispatch(h, ROW_RMSNORM, x, gamma, beta, y, p);
+}
+
+BwppHipStatus bwpp_hip_dispatch_layernorm(BwppHip *h, const float *x, const float *gamma, const float *beta,
+                                          float *y, BwppRmsnormParams p) {
+  return norm_dispatch(h, ROW_LAYERNORM, x, gamma, beta, y, p);
+}
+
+BwppHipStatus bwpp_hip_dispatch_reduce_max(BwppHip *h, const float *x, float *maxv, int32_t *argmax,
+                                           BwppReduceParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!x || (!maxv && !argmax)) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "reduce_max: NULL x or both outputs NULL");
+  const uint32_t ld = eff_ld(p.ld, p.cols);
+  if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
+  BwppRowArgs a = {};
+  a.x = x;
+  a.maxv = maxv;
+  a.argmax = argmax;
+  a.rows = p.rows;
+  a.cols = p.cols;
+  a.ld = ld;
+  if (p.axis == 0) {
+    if (p.cols == 0) return BWPP_HIP_OK;
+    return launch(h, h->col_max, (p.cols + 255) / 256, 1, 1, 256, a);
+  }
+  if (p.rows == 0) return BWPP_HIP_OK;
+  if (p.cols == 0) return launch(h, h->row_gen[ROW_MAX], p.rows, 1, 1, 256, a);
+  return row_dispatch(h, ROW_MAX, a, aligned16(x) && (ld % 4 == 0));
+}
+
+BwppHipStatus bwpp_hip_dispatch_reduce_max_mask(BwppHip *h, const float *x, float *mask, BwppReduceParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!x || !mask) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "reduce_max_mask: NULL x or mask");
+  const uint32_t ld = eff_ld(p.ld, p.cols);
+  if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
+  if (p.rows == 0 || p.cols == 0) return BWPP_HIP_OK;
+  BwppRowArgs a = {};
+  a.x = x;
+  a.y = mask;
+  a.rows = p.rows;
+  a.cols = p.cols;
+  a.ld = ld;
+  if (p.axis == 0) return launch(h, h->col_mask, (p.cols + 255) / 256, 1, 1, 256, a);
+  return row_dispatch(h, ROW_MASK, a, aligned16(x) && aligned16(mask) && (ld % 4 == 0));
+}
+
+BwppHipStatus bwpp_hip_dispatch_reduce_max_grad(BwppHip *h, const float *mask, const float *dy, float *dx,
+                                                BwppReduceParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!mask || !dy || !dx) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "reduce_max_grad: NULL mask, dy or dx");
+  const uint32_t ld = eff_ld(p.ld, p.cols);
+  if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
+  if (p.rows == 0 || p.cols == 0) return BWPP_HIP_OK;
+  BwppRowArgs a = {};
+  a.x = mask;
+  a.dy = dy;
+  a.y = dx;
+  a.rows = p.rows;
+  a.cols = p.cols;
+  a.ld = ld;
+  return launch(h, p.axis == 0 ? h->col_maskgrad : h->row_maskgrad, stream_grid(p.rows), 1, 1, 256, a);
+}
+
+BwppHipStatus bwpp_hip_dispatch_reduce_max_grad_argmax(BwppHip *h, const float *x, const int32_t *argmax,
+                                                       const float *dy, float *dx, BwppReduceParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if ((!x && !argmax) || !dy || !dx)
+    return fail(h, BWPP_HIP_ERR_INVALID_ARG, "reduce_max_grad_argmax: need x or argmax, and dy, dx");
+  const uint32_t ld = eff_ld(p.ld, p.cols);
+  if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
+  if (p.rows == 0 || p.cols == 0) return BWPP_HIP_OK;
+  BwppRowArgs a = {};
+  a.x = x;
+  a.idx_in = argmax;
+  a.dy = dy;
+  a.y = dx;
+  a.rows = p.rows;
+  a.cols = p.cols;
+  a.ld = ld;
+  if (p.axis == 0) return launch(h, h->col_maxgrad, (p.cols + 255) / 256, 1, 1, 256, a);
+  if (argmax) {
+    const bool vec = aligned16(dx) && (ld % 4 == 0);
+    return launch(h, vec ? h->row_maxgrad_idx_v4 : h->row_maxgrad_idx, stream_grid(p.rows), 1, 1, 256, a);
+  }
+  return row_dispatch(h, ROW_MAXGRAD, a, aligned16(x) && aligned16(dx) && (ld % 4 == 0));
+}
+
+}  // extern "C"
+
+// ------------------------------------------------- contractions (pending)
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, const void *b, void *c,
+                                                  const void *bias, BwppMatmulParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  (void)a; (void)b; (void)c; (void)bias; (void)p;
+  return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "matmul kernels not built yet");
+}
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, const void *k, const void *v,
+                                                     void *o, BwppAttentionParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  (void)q; (void)k; (void)v; (void)o; (void)p;
+  return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention kernels not built yet");
+}

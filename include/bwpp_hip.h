@@ -1,0 +1,265 @@
+/*
+ * bwpp_hip.h -- C ABI of libbwpp_hip, the MI355X (gfx950) execution backend
+ * for BW++'s hot ops.
+ *
+ * It replaces the reference's Metal operator seam
+ * (runtime/metal/dispatch_stub.h:42-74, implemented in dispatch_stub.m) and
+ * gives runtime/core's arena (runtime/core/arena.h:6-15) a device-memory
+ * twin.  Kernels are hand-written gfx950 HIP, prebuilt into code objects
+ * (*.hsaco) that bwpp_hip_create() loads with hipModuleLoad; every operator
+ * launches with hipModuleLaunchKernel on the handle's stream.
+ *
+ * Conventions (kept from the reference):
+ *  - the caller owns every buffer; pointers are device pointers unless a
+ *    function says otherwise;
+ *  - row-major with explicit leading dimensions (in elements); softmax and
+ *    the norms run along the last axis;
+ *  - a NULL gamma / beta / bias means 1 / 0 / 0 (dispatch_stub.m:103-110,
+ *    215-234);
+ *  - the params structs keep the reference's type names and leading fields,
+ *    in the reference's order (dispatch_stub.h:9-40); fields added after them
+ *    take their documented default when zero, so a reference-style
+ *    initialiser `{M, N, K, lda, ldb, ldc}` keeps its meaning.
+ * Differences:
+ *  - every call returns a status instead of returning silently on bad
+ *    arguments (dispatch_stub.m:66-79); a failed call launches nothing;
+ *  - launches are asynchronous on the handle's stream; bwpp_hip_sync() waits
+ *    (the reference waits inside every dispatch, dispatch_stub.m:139-140);
+ *  - the function cache is filled once in bwpp_hip_create() and read-only
+ *    afterwards, so one handle may be used from several threads as long as
+ *    they do not race on the stream setting (the reference's function-static
+ *    PSO caches are not thread-safe, dispatch_stub.m:81).
+ */
+#ifndef BWPP_HIP_H
+#define BWPP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* 0 and 1 coincide with the reference's BwppStatus {BWPP_OK, BWPP_ERR}
+ * (compiler/include/bwpp.h:8-11); the rest refine BWPP_ERR. */
+typedef enum {
+  BWPP_HIP_OK = 0,
+  BWPP_HIP_ERR = 1,
+  BWPP_HIP_ERR_INVALID_ARG = 2,   /* NULL pointer, bad size, ld < cols, ... */
+  BWPP_HIP_ERR_HIP = 3,           /* a HIP runtime call failed */
+  BWPP_HIP_ERR_NO_KERNEL = 4,     /* code object or kernel symbol missing */
+  BWPP_HIP_ERR_ALIAS = 5,         /* GEMM/attention output overlaps an input */
+  BWPP_HIP_ERR_OUT_OF_MEMORY = 6, /* device allocation or arena exhausted */
+  BWPP_HIP_ERR_UNSUPPORTED = 7,   /* valid request this build does not run */
+  BWPP_HIP_ERR_NO_DEVICE = 8      /* no usable HIP device */
+} BwppHipStatus;
+
+typedef enum { BWPP_HIP_F32 = 0, BWPP_HIP_BF16 = 1 } BwppHipDType;
+
+/* Same values as BwppTileEpilogue (compiler/include/tile_ir.h:35-40). */
+typedef enum {
+  BWPP_HIP_EPILOGUE_NONE = 0,
+  BWPP_HIP_EPILOGUE_ADD = 1,
+  BWPP_HIP_EPILOGUE_SILU = 2,
+  BWPP_HIP_EPILOGUE_ADD_SILU = 3
+} BwppHipEpilogue;
+
+/* dispatch_stub.h:9-16 + extensions.
+ * C = op(A)·op(B) (+bias[col]) (→SiLU).  A is [M x K] (trans_a: stored
+ * [K x M]), B is [K x N] (trans_b: stored [N x K]); lda/ldb/ldc are the row
+ * strides of the stored matrices.  dtype F32: fp32 in/out on FP32 MFMA;
+ * BF16: bf16 A, B, bias and C with fp32 accumulation and epilogue, C rounded
+ * to nearest even.  bias is read only when the epilogue includes ADD. */
+typedef struct {
+  uint32_t M;
+  uint32_t N;
+  uint32_t K;
+  uint32_t lda;
+  uint32_t ldb;
+  uint32_t ldc;
+  uint32_t dtype;    /* BwppHipDType, 0 = F32 */
+  uint32_t epilogue; /* BwppHipEpilogue, 0 = none */
+  uint32_t trans_a;  /* 0 = A row-major [M x K] */
+  uint32_t trans_b;  /* 0 = B row-major [K x N] */
+} BwppMatmulParams;
+
+/* dispatch_stub.h:18-22 */
+typedef struct {
+  uint32_t rows;
+  uint32_t cols;
+  uint32_t ld;
+} BwppSoftmaxParams;
+
+/* dispatch_stub.h:24-29; also used by LayerNorm and the norm grads. */
+typedef struct {
+  uint32_t rows;
+  uint32_t cols;
+  uint32_t ld;
+  float eps;
+} BwppRmsnormParams;
+
+/* dispatch_stub.h:31-40 + extensions.  One (batch, head) slice is the
+ * reference's single-head problem: Q [M x K], K [N x K], V [N x D],
+ * O [M x D] with row strides ldq/ldk/ldv/ldo; slices are placed by the
+ * batch/head strides (elements).  O = softmax(scale * Q·K^T [masked]) · V.
+ * causal masks keys n > m + (N - M) (bottom-right aligned; rows that see no
+ * key produce zeros).  dtype BF16: bf16 Q/K/V/O, fp32 softmax and
+ * accumulation; F32: fp32 throughout. */
+typedef struct {
+  uint32_t M;
+  uint32_t N;
+  uint32_t K;
+  uint32_t D;
+  uint32_t ldq;
+  uint32_t ldk;
+  uint32_t ldv;
+  uint32_t ldo;
+  uint32_t batch; /* 0 = 1 */
+  uint32_t heads; /* 0 = 1 */
+  uint64_t q_batch_stride, q_head_stride;
+  uint64_t k_batch_stride, k_head_stride;
+  uint64_t v_batch_stride, v_head_stride;
+  uint64_t o_batch_stride, o_head_stride;
+  float scale;     /* 0 = 1.0: the reference applies no scale */
+  uint32_t causal; /* 0 = unmasked, as the reference */
+  uint32_t dtype;  /* BwppHipDType, 0 = F32 */
+} BwppAttentionParams;
+
+/* reduce_max family.  axis follows bwpp_cpu_ref.c:156,172: axis == 0 reduces
+ * over rows (one result per column), any other value reduces along each row
+ * (one result per row). */
+typedef struct {
+  uint32_t rows;
+  uint32_t cols;
+  uint32_t ld; /* row stride of x / mask / dx; 0 = cols */
+  int32_t axis;
+} BwppReduceParams;
+
+typedef struct BwppHip BwppHip;
+
+/* ---- handle ---- */
+
+/* Selects `device`, loads every code object from code_object_dir (NULL: the
+ * directory holding libbwpp_hip.so) and resolves every kernel.  Fails with
+ * NO_DEVICE / NO_KERNEL / HIP rather than returning a half-built handle.
+ * Replaces the per-op PSO cache (dispatch_stub.m:6-56). */
+BwppHipStatus bwpp_hip_create(BwppHip **out, int device,
+                              const char *code_object_dir);
+void bwpp_hip_destroy(BwppHip *h);
+/* Stream for subsequent launches (a hipStream_t); NULL = the null stream. */
+BwppHipStatus bwpp_hip_set_stream(BwppHip *h, void *hip_stream);
+void *bwpp_hip_get_stream(const BwppHip *h);
+/* Waits for all work on the handle's stream. */
+BwppHipStatus bwpp_hip_sync(BwppHip *h);
+/* Text of the last failure on this handle ("" if none). */
+const char *bwpp_hip_last_error(const BwppHip *h);
+const char *bwpp_hip_status_string(BwppHipStatus s);
+/* Number of compute units of the handle's device (for launch heuristics). */
+int bwpp_hip_device_cus(const BwppHip *h);
+
+/* ---- device memory ---- */
+
+/* Device twin of runtime/core/arena.h:6-15 / arena.c:4-38: one hipMalloc of
+ * `capacity` bytes, bump allocation with power-of-two alignment, NULL on
+ * exhaustion, reset rewinds, destroy frees. */
+typedef struct {
+  unsigned char *buffer; /* device address */
+  size_t capacity;
+  size_t offset;
+  int device;
+} BwppHipArena;
+
+BwppHipStatus bwpp_hip_arena_init(BwppHip *h, BwppHipArena *arena,
+                                  size_t capacity);
+void bwpp_hip_arena_reset(BwppHipArena *arena);
+void *bwpp_hip_arena_alloc(BwppHipArena *arena, size_t size, size_t align);
+void bwpp_hip_arena_destroy(BwppHipArena *arena);
+
+/* Stream-ordered copies, complete on return. */
+BwppHipStatus bwpp_hip_copy_to_device(BwppHip *h, void *dst, const void *src,
+                                      size_t bytes);
+BwppHipStatus bwpp_hip_copy_to_host(BwppHip *h, void *dst, const void *src,
+                                    size_t bytes);
+
+/* ---- operators (device pointers; asynchronous on the handle's stream) ---- */
+
+/* bwpp_metal_dispatch_matmul (dispatch_stub.h:42-49); CPU twin
+ * bwpp_cpu_matmul_f32 (bwpp_cpu_ref.c:8-35).  C must not overlap A, B or
+ * bias (ALIAS). */
+BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a,
+                                       const void *b, void *c,
+                                       const void *bias,
+                                       BwppMatmulParams params);
+
+/* bwpp_metal_dispatch_softmax (dispatch_stub.h:51-56); CPU twin
+ * bwpp_cpu_softmax_f32 (bwpp_cpu_ref.c:37-61).  y may equal x. */
+BwppHipStatus bwpp_hip_dispatch_softmax(BwppHip *h, const float *x, float *y,
+                                        BwppSoftmaxParams params);
+
+/* bwpp_metal_dispatch_rmsnorm (dispatch_stub.h:58-65); CPU twin
+ * bwpp_cpu_rmsnorm_f32 (bwpp_cpu_ref.c:63-90).  y may equal x. */
+BwppHipStatus bwpp_hip_dispatch_rmsnorm(BwppHip *h, const float *x,
+                                        const float *gamma, const float *beta,
+                                        float *y, BwppRmsnormParams params);
+
+/* LayerNorm: no reference kernel (ROADMAP.md:14); same argument order as
+ * rmsnorm.  y = (x-mean)/sqrt(var+eps)*gamma+beta, population variance. */
+BwppHipStatus bwpp_hip_dispatch_layernorm(BwppHip *h, const float *x,
+                                          const float *gamma,
+                                          const float *beta, float *y,
+                                          BwppRmsnormParams params);
+
+/* bwpp_metal_dispatch_attention (dispatch_stub.h:67-74); CPU twin
+ * bwpp_cpu_attention_f32 (bwpp_cpu_ref.c:92-144).  O must not overlap Q, K
+ * or V (ALIAS). */
+BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q,
+                                          const void *k, const void *v,
+                                          void *o, BwppAttentionParams params);
+
+/* reduce_max forward (graph op BWPP_GOP_REDUCE_MAX, graph_ir.h:48; no
+ * reference kernel): maxv as the reference's fold, argmax = lowest index
+ * holding it (-1 if none).  Either output may be NULL, not both. */
+BwppHipStatus bwpp_hip_dispatch_reduce_max(BwppHip *h, const float *x,
+                                           float *maxv, int32_t *argmax,
+                                           BwppReduceParams params);
+
+/* bwpp_cpu_reduce_max_mask_f32 (bwpp_cpu_ref.c:146-190): 1.0 at every
+ * element equal to its line's maximum, else 0.0. */
+BwppHipStatus bwpp_hip_dispatch_reduce_max_mask(BwppHip *h, const float *x,
+                                                float *mask,
+                                                BwppReduceParams params);
+
+/* bwpp_cpu_reduce_max_grad_f32 (bwpp_cpu_ref.c:192-219): dx = mask * dy,
+ * dy broadcast along the reduced axis. */
+BwppHipStatus bwpp_hip_dispatch_reduce_max_grad(BwppHip *h, const float *mask,
+                                                const float *dy, float *dx,
+                                                BwppReduceParams params);
+
+/* reduce_max grad routed one-hot to the lowest-index maximum: pass x (the
+ * argmax is recomputed in the same pass) or argmax (saved indices), not
+ * both NULL; dx is fully written. */
+BwppHipStatus bwpp_hip_dispatch_reduce_max_grad_argmax(
+    BwppHip *h, const float *x, const int32_t *argmax, const float *dy,
+    float *dx, BwppReduceParams params);
+
+/* ---- synthetic inputs (host memory, no device needed) ----
+ * Counter-based: element i of (seed, stream) is a pure function of
+ * (seed, stream, i), so subsets and threads agree with a full fill.
+ * SplitMix64 -> 24-bit uniform; normal by Box-Muller in double. */
+void bwpp_synth_uniform_f32(float *dst, uint64_t n, uint64_t seed,
+                            uint64_t stream, float lo, float hi);
+void bwpp_synth_normal_f32(float *dst, uint64_t n, uint64_t seed,
+                           uint64_t stream, float mean, float stddev);
+/* The reference's test fixture x[i][j] = (i*cols + j + 1) * scale
+ * (runtime/cpu/test_matmul.c:7-13). */
+void bwpp_synth_ramp_f32(float *dst, uint32_t rows, uint32_t cols,
+                         float scale);
+/* fp32 -> bf16 round to nearest even (NaN kept quiet), and back (exact). */
+void bwpp_f32_to_bf16(const float *src, uint16_t *dst, uint64_t n);
+void bwpp_bf16_to_f32(const uint16_t *src, float *dst, uint64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BWPP_HIP_H */
