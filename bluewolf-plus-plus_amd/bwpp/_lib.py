@@ -126,6 +126,13 @@ def load():
     global _lib
     if _lib is not None:
         return _lib
+    try:
+        # torch ships its own HIP runtime under the same soname; loading torch
+        # first makes libbwpp_hip bind to that one, so device pointers and
+        # streams from torch are valid in the library.
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not os.path.exists(LIB_PATH):
         raise LibraryMissing(
             f"{LIB_PATH} is not built; run `make -C {PKG_DIR}` or "

@@ -25,4 +25,23 @@ typedef struct {
   float eps;
 } BwppRowArgs;
 
+/* GEMM: C = op(A)·op(B) (+bias) (->SiLU); see gemm.hip. */
+typedef struct {
+  const void *a;
+  const void *b;
+  const void *bias; /* NULL: no bias even if the epilogue asks for one */
+  void *c;
+  uint32_t M;
+  uint32_t N;
+  uint32_t K;
+  uint32_t lda;
+  uint32_t ldb;
+  uint32_t ldc;
+  uint32_t epilogue; /* BWPP_HIP_EPILOGUE_* values */
+  uint32_t tiles_m;  /* ceil(M / BM) */
+  uint32_t tiles_n;  /* ceil(N / BN) */
+  uint32_t group_m;  /* tile-order group height (in tiles) */
+  uint32_t vec_ok;   /* 1: rows are 16-byte aligned (edge kernels only) */
+} BwppGemmArgs;
+
 #endif /* BWPP_KARGS_H */

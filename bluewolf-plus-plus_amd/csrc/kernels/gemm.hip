@@ -1,0 +1,504 @@
+// MFMA GEMMs for gfx950:  C = op(A) · op(B) (+ bias[col]) (-> SiLU).
+//
+// Semantics: runtime/cpu/bwpp_cpu_ref.c:8-35 (fp32 accumulation, bias added
+// to the accumulator, then SiLU x / (1 + e^-x)); the MSL kernel it replaces
+// is codegen_metal.c:357-434.  op(A) is A [M x K] or, with TA, the transpose
+// of a stored [K x M]; op(B) is B [K x N] or, with TB, the transpose of a
+// stored [N x K].
+//
+// Both kernels compute C^T tiles: the MFMA "A" operand is a tile of op(B)^T
+// (rows = output columns n) and the "B" operand a tile of op(A)^T (columns =
+// output rows m).  The accumulator of v_mfma_f32_32x32x{16_bf16,2f32} then
+// gives each lane one output row m and runs of 4 consecutive columns n, so
+// the epilogue stores 8-byte (bf16) or 16-byte (fp32) runs.
+//
+// bf16 kernel (v_mfma_f32_32x32x16_bf16, 8 bf16 per lane per operand):
+//   block tile BM x BN x BK = 256 x 256 x 64, 4 waves in 2 x 2, each wave
+//   128 x 128 (4 x 4 MFMA tiles of 32 x 32).  Both operands sit in LDS
+//   K-contiguous ([row][k], 128-byte rows of eight 16-byte chunks, chunk c of
+//   row r stored at c ^ (r & 7)), double-buffered: 2 x 64 KiB.  An operand
+//   whose rows are K-contiguous in memory is copied with 16-byte loads; one
+//   that is MN-contiguous (row-major B, or A with TA) is loaded as 8 x 8
+//   blocks and transposed in registers on the way to LDS.
+// fp32 kernel (v_mfma_f32_32x32x2f32, 1 float per lane per operand):
+//   128 x 128 x 32 tile, 4 waves in 2 x 2 (64 x 64 each); an operand keeps its
+//   memory orientation in LDS (MN-contiguous rows padded to R+32 floats,
+//   K-contiguous rows padded to BK+2), which makes the per-lane 4-byte MFMA
+//   operand reads bank-conflict free without any transpose.
+//
+// Tile order: workgroups are dispatched round-robin over the 8 XCDs, so
+// block b is remapped to tile (b % 8) * (T / 8) + b / 8 (when 8 | T), giving
+// each XCD a contiguous run of tiles; runs are walked group_m tile-rows at a
+// time so tiles that share A rows and B columns meet in the same L2.
+#include "common.h"
+#include "../kargs.h"
+
+using namespace bwpp;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+namespace {
+
+constexpr uint32_t kEpiAdd = 1u, kEpiSilu = 2u;
+
+__device__ __forceinline__ void tile_coords(const BwppGemmArgs &a, uint32_t &tm, uint32_t &tn) {
+  const uint32_t T = a.tiles_m * a.tiles_n;
+  uint32_t b = blockIdx.x;
+  if ((T & 7u) == 0) b = (b & 7u) * (T >> 3) + (b >> 3);
+  const uint32_t gm = a.group_m;
+  const uint32_t per_group = gm * a.tiles_n;
+  const uint32_t g = b / per_group;
+  const uint32_t first = g * gm;
+  const uint32_t rows = min(gm, a.tiles_m - first);
+  const uint32_t idx = b - g * per_group;
+  tm = first + idx % rows;
+  tn = idx / rows;
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// ---------------------------------------------------------------- bf16
+
+__device__ __forceinline__ uint32_t dword(const uint4 &v, int d) {
+  return d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
+}
+// bf16 i (0..7) of x0's row and the same of x1's row, packed as one dword.
+__device__ __forceinline__ uint32_t pair_b16(int i, const uint4 &r0, const uint4 &r1) {
+  const uint32_t x0 = dword(r0, i >> 1), x1 = dword(r1, i >> 1);
+  return (i & 1) ? ((x0 >> 16) | (x1 & 0xFFFF0000u)) : ((x0 & 0xFFFFu) | (x1 << 16));
+}
+// 8 x 8 transpose of bf16: in[r] holds row r (8 values; dword d holds
+// elements 2d and 2d+1 in its low and high halves); out[i] = column i.
+__device__ __forceinline__ void transpose8x8_b16(const uint4 (&in)[8], uint4 (&out)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    out[i] = make_uint4(pair_b16(i, in[0], in[1]), pair_b16(i, in[2], in[3]),
+                        pair_b16(i, in[4], in[5]), pair_b16(i, in[6], in[7]));
+}
+
+// Gathers up to 8 bf16 from p[0..7] (element e kept only if ok(e)) into a
+// 16-byte chunk, zero elsewhere.
+template <class Ok>
+__device__ __forceinline__ uint4 gather8_b16(const uint16_t *p, Ok ok) {
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (ok(e)) w[e >> 1] |= (uint32_t)p[e] << ((e & 1) * 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// One 16-byte chunk (8 bf16) of a K-contiguous row, guarded for edges.
+template <bool EDGE>
+__device__ __forceinline__ uint4 load_chunk_b16(const uint16_t *base, uint32_t ld, uint32_t row,
+                                               uint32_t rows, uint32_t k, uint32_t K, bool vec) {
+  if (!EDGE) return *reinterpret_cast<const uint4 *>(base + (size_t)row * ld + k);
+  if (row >= rows) return make_uint4(0, 0, 0, 0);
+  const uint16_t *p = base + (size_t)row * ld + k;
+  if (vec && k + 8 <= K) return *reinterpret_cast<const uint4 *>(p);
+  return gather8_b16(p, [&](int e) { return k + e < K; });
+}
+
+// 8 consecutive MN elements of one K row of an MN-contiguous operand.
+template <bool EDGE>
+__device__ __forceinline__ uint4 load_mnrow_b16(const uint16_t *base, uint32_t ld, uint32_t k,
+                                               uint32_t K, uint32_t mn, uint32_t MN, bool vec) {
+  if (!EDGE) return *reinterpret_cast<const uint4 *>(base + (size_t)k * ld + mn);
+  if (k >= K) return make_uint4(0, 0, 0, 0);
+  const uint16_t *p = base + (size_t)k * ld + mn;
+  if (vec && mn + 8 <= MN) return *reinterpret_cast<const uint4 *>(p);
+  return gather8_b16(p, [&](int e) { return mn + e < MN; });
+}
+
+// Staging of one operand tile (R rows of the LDS tile, BK = 64) through
+// registers.  MNC: the operand is MN-contiguous in memory (needs transpose).
+template <int R, int NT, bool MNC, bool EDGE>
+struct StageB16 {
+  static constexpr int kChunks = MNC ? (64 / 8) * (R / 8) / NT : R * 8 / NT;
+  static constexpr int kRegs = MNC ? 8 * kChunks : kChunks;
+  uint4 r[kRegs];
+
+  // r0: first tile row (m or n); k0: first k; rows: M or N; ld: row stride.
+  __device__ __forceinline__ void load(const uint16_t *g, uint32_t ld, uint32_t r0, uint32_t rows,
+                                       uint32_t k0, uint32_t K, bool vec, int tid) {
+    if constexpr (!MNC) {
+#pragma unroll
+      for (int i = 0; i < kChunks; ++i) {
+        const int q = tid + i * NT;
+        const int row = q >> 3, c = q & 7;
+        r[i] = load_chunk_b16<EDGE>(g, ld, r0 + row, rows, k0 + c * 8, K, vec);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kChunks; ++i) {
+        const int q = tid + i * NT;
+        const int kb = q / (R / 8), nb = q % (R / 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          r[i * 8 + e] = load_mnrow_b16<EDGE>(g, ld, k0 + kb * 8 + e, K, r0 + nb * 8, rows, vec);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(uint16_t *s, int tid) const {
+    uint4 *s4 = reinterpret_cast<uint4 *>(s);  // [R][8] chunks
+    if constexpr (!MNC) {
+#pragma unroll
+      for (int i = 0; i < kChunks; ++i) {
+        const int q = tid + i * NT;
+        const int row = q >> 3, c = q & 7;
+        s4[row * 8 + (c ^ (row & 7))] = r[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kChunks; ++i) {
+        const int q = tid + i * NT;
+        const int kb = q / (R / 8), nb = q % (R / 8);
+        uint4 in[8], out[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) in[e] = r[i * 8 + e];
+        transpose8x8_b16(in, out);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s4[(nb * 8 + e) * 8 + (kb ^ e)] = out[e];
+      }
+    }
+  }
+};
+
+template <bool TA, bool TB, bool EDGE>
+__device__ __forceinline__ void gemm_bf16(const BwppGemmArgs &a) {
+  constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 2;
+  constexpr int NT = 64 * WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int kBuf = (BM + BN) * BK;
+  constexpr int kCld = BN + 8;  // epilogue tile row stride (bf16)
+  constexpr int kSmem = 2 * kBuf > BM * kCld ? 2 * kBuf : BM * kCld;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[kSmem];  // 132 KiB
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  uint32_t tm, tn;
+  tile_coords(a, tm, tn);
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  const uint16_t *A = static_cast<const uint16_t *>(a.a);
+  const uint16_t *B = static_cast<const uint16_t *>(a.b);
+  const bool vec = a.vec_ok != 0;
+
+  StageB16<BM, NT, TA, EDGE> sa;  // rows m
+  StageB16<BN, NT, !TB, EDGE> sb; // rows n
+
+  f32x16_t acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const uint32_t nk = (a.K + BK - 1) / BK;
+  if (nk > 0) {
+    sa.load(A, a.lda, m0, a.M, 0, a.K, vec, tid);
+    sb.load(B, a.ldb, n0, a.N, 0, a.K, vec, tid);
+    sa.store(smem, tid);
+    sb.store(smem + BM * BK, tid);
+  }
+  __syncthreads();
+
+  // MFMA operand reads: lane row = lane % 32 within a 32-row fragment,
+  // chunk (2 * ks + lane / 32) of the row, swizzled by (row & 7) = lane & 7.
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  for (uint32_t kt = 0; kt < nk; ++kt) {
+    // Prefetch the next K tile (the last tile again on the final trip, so
+    // the staging registers are written on every path).
+    const uint32_t kn = (kt + 1 < nk ? kt + 1 : kt) * BK;
+    sa.load(A, a.lda, m0, a.M, kn, a.K, vec, tid);
+    sb.load(B, a.ldb, n0, a.N, kn, a.K, vec, tid);
+    const uint16_t *As = smem + (kt & 1) * kBuf;
+    const uint16_t *Bs = As + BM * BK;
+    const uint4 *As4 = reinterpret_cast<const uint4 *>(As);
+    const uint4 *Bs4 = reinterpret_cast<const uint4 *>(Bs);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int chunk = (2 * ks + lhalf) ^ (lane & 7);
+      bf16x8_t af[FM], bf[FN];
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const uint4 v = As4[(wm * TM + j * 32 + lrow) * 8 + chunk];
+        af[j] = __builtin_bit_cast(bf16x8_t, v);
+      }
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        const uint4 v = Bs4[(wn * TN + i * 32 + lrow) * 8 + chunk];
+        bf[i] = __builtin_bit_cast(bf16x8_t, v);
+      }
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[i], af[j], acc[i][j], 0, 0, 0);
+    }
+    uint16_t *nxt = smem + ((kt + 1) & 1) * kBuf;
+    sa.store(nxt, tid);
+    sb.store(nxt + BM * BK, tid);
+    __syncthreads();
+  }
+
+  // Epilogue, through LDS: each lane owns output row m and, per q, columns
+  // n .. n+3 of the tile; bias + SiLU in fp32, rounded to bf16 and written to
+  // an LDS C tile [BM][BN + 8], then stored row-contiguously in 16-byte
+  // chunks.  The loop's final barrier has freed both operand buffers.
+  const uint16_t *bias = static_cast<const uint16_t *>(a.bias);
+  const bool add = (a.epilogue & kEpiAdd) && bias;
+  const bool act = (a.epilogue & kEpiSilu) != 0;
+#pragma unroll
+  for (int i = 0; i < FN; ++i) {
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int ml = wm * TM + j * 32 + lrow;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = wn * TN + i * 32 + q * 8 + lhalf * 4;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float t = acc[i][j][q * 4 + e];
+          if (add) t += bf16_bits_to_f32(bias[min(n0 + nl + e, a.N - 1)]);
+          if (act) t = silu(t);
+          v[e] = t;
+        }
+        uint2 o;
+        o.x = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
+        o.y = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+        *reinterpret_cast<uint2 *>(smem + ml * kCld + nl) = o;
+      }
+    }
+  }
+  __syncthreads();
+  uint16_t *C = static_cast<uint16_t *>(a.c);
+  constexpr int kRowChunks = BN / 8;
+#pragma unroll 4
+  for (int it = 0; it < BM * kRowChunks / NT; ++it) {
+    const int q = tid + it * NT;
+    const int row = q / kRowChunks, c = q % kRowChunks;
+    const uint32_t m = m0 + row, n = n0 + c * 8;
+    const uint4 v = *reinterpret_cast<const uint4 *>(smem + row * kCld + c * 8);
+    if (!EDGE || (m < a.M && n + 8 <= a.N && vec)) {
+      *reinterpret_cast<uint4 *>(C + (size_t)m * a.ldc + n) = v;
+    } else if (m < a.M) {
+      const uint16_t *h = smem + row * kCld + c * 8;
+      for (int e = 0; e < 8; ++e)
+        if (n + e < a.N) C[(size_t)m * a.ldc + n + e] = h[e];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- fp32
+
+template <int R, int BK, int NT, bool MNC, bool EDGE>
+struct StageF32 {
+  // MNC: tile kept [BK][R + 32]; else [R][BK + 2].
+  static constexpr int kLd = MNC ? R + 32 : BK + 2;
+  static constexpr int kVecs = R * BK / 4 / NT;
+  float4 r[kVecs];
+
+  __device__ __forceinline__ void load(const float *g, uint32_t ld, uint32_t r0, uint32_t rows,
+                                       uint32_t k0, uint32_t K, bool vec, int tid) {
+#pragma unroll
+    for (int i = 0; i < kVecs; ++i) {
+      const int q = tid + i * NT;
+      uint32_t grow, gcol, lim_row, lim_col;
+      if constexpr (MNC) {  // memory rows are k, columns mn
+        const int k = q / (R / 4), c = q % (R / 4);
+        grow = k0 + k;
+        gcol = r0 + c * 4;
+        lim_row = K;
+        lim_col = rows;
+      } else {  // memory rows are mn, columns k
+        const int row = q / (BK / 4), c = q % (BK / 4);
+        grow = r0 + row;
+        gcol = k0 + c * 4;
+        lim_row = rows;
+        lim_col = K;
+      }
+      const float *p = g + (size_t)grow * ld + gcol;
+      if (!EDGE) {
+        r[i] = *reinterpret_cast<const float4 *>(p);
+      } else {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (grow < lim_row) {
+          if (vec && gcol + 4 <= lim_col) {
+            v = *reinterpret_cast<const float4 *>(p);
+          } else {
+            if (gcol + 0 < lim_col) v.x = p[0];
+            if (gcol + 1 < lim_col) v.y = p[1];
+            if (gcol + 2 < lim_col) v.z = p[2];
+            if (gcol + 3 < lim_col) v.w = p[3];
+          }
+        }
+        r[i] = v;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float *s, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kVecs; ++i) {
+      const int q = tid + i * NT;
+      if constexpr (MNC) {
+        const int k = q / (R / 4), c = q % (R / 4);
+        *reinterpret_cast<float4 *>(s + k * kLd + c * 4) = r[i];
+      } else {
+        const int row = q / (BK / 4), c = q % (BK / 4);
+        float2 *d = reinterpret_cast<float2 *>(s + row * kLd + c * 4);
+        d[0] = make_float2(r[i].x, r[i].y);
+        d[1] = make_float2(r[i].z, r[i].w);
+      }
+    }
+  }
+
+  // Element (k, mn) of the tile.
+  __device__ __forceinline__ static float at(const float *s, int k, int mn) {
+    return MNC ? s[k * kLd + mn] : s[mn * kLd + k];
+  }
+  static constexpr int kSize = MNC ? BK * (R + 32) : R * (BK + 2);
+};
+
+template <bool TA, bool TB, bool EDGE>
+__device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
+  constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 2;
+  constexpr int NT = 64 * WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  using SA = StageF32<BM, BK, NT, TA, EDGE>;   // A MN-contiguous when transposed
+  using SB = StageF32<BN, BK, NT, !TB, EDGE>;  // B MN-contiguous when not transposed
+  constexpr int kBuf = SA::kSize + SB::kSize;
+  __shared__ __attribute__((aligned(16))) float smemf[2 * kBuf];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  uint32_t tm, tn;
+  tile_coords(a, tm, tn);
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  const float *A = static_cast<const float *>(a.a);
+  const float *B = static_cast<const float *>(a.b);
+  const bool vec = a.vec_ok != 0;
+  SA sa;
+  SB sb;
+
+  f32x16_t acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const uint32_t nk = (a.K + BK - 1) / BK;
+  if (nk > 0) {
+    sa.load(A, a.lda, m0, a.M, 0, a.K, vec, tid);
+    sb.load(B, a.ldb, n0, a.N, 0, a.K, vec, tid);
+    sa.store(smemf, tid);
+    sb.store(smemf + SA::kSize, tid);
+  }
+  __syncthreads();
+
+  const int lrow = lane & 31, lk = lane >> 5;
+  for (uint32_t kt = 0; kt < nk; ++kt) {
+    const uint32_t kn = (kt + 1 < nk ? kt + 1 : kt) * BK;
+    sa.load(A, a.lda, m0, a.M, kn, a.K, vec, tid);
+    sb.load(B, a.ldb, n0, a.N, kn, a.K, vec, tid);
+    const float *As = smemf + (kt & 1) * kBuf;
+    const float *Bs = As + SA::kSize;
+#pragma unroll
+    for (int ks = 0; ks < BK / 2; ++ks) {
+      const int k = 2 * ks + lk;
+      float af[FM], bf[FN];
+#pragma unroll
+      for (int j = 0; j < FM; ++j) af[j] = SA::at(As, k, wm * TM + j * 32 + lrow);
+#pragma unroll
+      for (int i = 0; i < FN; ++i) bf[i] = SB::at(Bs, k, wn * TN + i * 32 + lrow);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[i], af[j], acc[i][j], 0, 0, 0);
+    }
+    float *nxt = smemf + ((kt + 1) & 1) * kBuf;
+    sa.store(nxt, tid);
+    sb.store(nxt + SA::kSize, tid);
+    __syncthreads();
+  }
+
+  // Epilogue through LDS as in the bf16 kernel: C tile [BM][BN + 4] fp32.
+  constexpr int kCld = BN + 4;
+  static_assert(BM * kCld <= 2 * kBuf, "epilogue tile must fit the operand buffers");
+  const float *bias = static_cast<const float *>(a.bias);
+  const bool add = (a.epilogue & kEpiAdd) && bias;
+  const bool act = (a.epilogue & kEpiSilu) != 0;
+  const int lhalf = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < FN; ++i) {
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int ml = wm * TM + j * 32 + lrow;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = wn * TN + i * 32 + q * 8 + lhalf * 4;
+        float vv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float t = acc[i][j][q * 4 + e];
+          if (add) t += bias[min(n0 + nl + e, a.N - 1)];
+          if (act) t = silu(t);
+          vv[e] = t;
+        }
+        *reinterpret_cast<float4 *>(smemf + ml * kCld + nl) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+      }
+    }
+  }
+  __syncthreads();
+  float *C = static_cast<float *>(a.c);
+  constexpr int kRowVecs = BN / 4;
+#pragma unroll 4
+  for (int it = 0; it < BM * kRowVecs / NT; ++it) {
+    const int q = tid + it * NT;
+    const int row = q / kRowVecs, c = q % kRowVecs;
+    const uint32_t m = m0 + row, n = n0 + c * 4;
+    const float4 v = *reinterpret_cast<const float4 *>(smemf + row * kCld + c * 4);
+    if (!EDGE || (m < a.M && n + 4 <= a.N && vec)) {
+      *reinterpret_cast<float4 *>(C + (size_t)m * a.ldc + n) = v;
+    } else if (m < a.M) {
+      const float *h = smemf + row * kCld + c * 4;
+      for (int e = 0; e < 4; ++e)
+        if (n + e < a.N) C[(size_t)m * a.ldc + n + e] = h[e];
+    }
+  }
+}
+
+}  // namespace
+
+// Entry points: bwpp_gemm_<bf16|f32>_t<TA><TB>_<f|e>  (f: no edges, aligned)
+#define BWPP_GEMM_BF16(TA, TB, EDGE, SUF)                                                  \
+  extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(256, 256),            \
+                                       amdgpu_waves_per_eu(1, 1))) void                  \
+      bwpp_gemm_bf16_t##TA##TB##_##SUF(const BwppGemmArgs a) {                            \
+    gemm_bf16<TA, TB, EDGE>(a);                                                           \
+  }
+#define BWPP_GEMM_F32(TA, TB, EDGE, SUF)                                                   \
+  extern "C" __global__ __launch_bounds__(256) void bwpp_gemm_f32_t##TA##TB##_##SUF(     \
+      const BwppGemmArgs a) {                                                             \
+    gemm_f32<TA, TB, EDGE>(a);                                                            \
+  }
+#define BWPP_GEMM_ALL(MAC) \
+  MAC(0, 0, false, f)      \
+  MAC(0, 1, false, f)      \
+  MAC(1, 0, false, f)      \
+  MAC(1, 1, false, f)      \
+  MAC(0, 0, true, e)       \
+  MAC(0, 1, true, e)       \
+  MAC(1, 0, true, e)       \
+  MAC(1, 1, true, e)
+
+BWPP_GEMM_ALL(BWPP_GEMM_BF16)
+BWPP_GEMM_ALL(BWPP_GEMM_F32)

@@ -27,7 +27,7 @@ namespace {
 thread_local std::string g_create_error;
 
 // Code objects built by the package Makefile, all required.
-const char *const kModules[] = {"bwpp_rowops.hsaco"};
+const char *const kModules[] = {"bwpp_rowops.hsaco", "bwpp_gemm.hsaco"};
 
 // Row-op kernels: bwpp_row_<op>_v<VPT>_w<WPR>_<f|p>, see rowops.hip.
 enum RowOpId { ROW_SOFTMAX, ROW_RMSNORM, ROW_LAYERNORM, ROW_MAX, ROW_MAXGRAD, ROW_MASK, ROW_NOPS };
@@ -69,6 +69,9 @@ struct BwppHip {
   hipFunction_t col_max = nullptr;
   hipFunction_t col_maxgrad = nullptr;
   hipFunction_t col_mask = nullptr;
+  // bwpp_gemm_<bf16|f32>_t<TA><TB>_<e|f>: [dtype][ta][tb][full]
+  hipFunction_t gemm[2][2][2][2] = {};
+  uint32_t gemm_group_m = 8;  // BWPP_GEMM_GROUP_M
 };
 
 namespace {
@@ -93,8 +96,10 @@ BwppHipStatus resolve(BwppHip *h, const std::string &name, hipFunction_t *out) {
       *out = f;
       return BWPP_HIP_OK;
     }
+    // A miss in one code object is expected; do not leave it as the
+    // thread's last HIP error for the caller (or torch) to trip over.
+    (void)hipGetLastError();
   }
-  (void)hipGetLastError();  // clear the lookup misses
   return fail(h, BWPP_HIP_ERR_NO_KERNEL, "kernel %s not found in any loaded code object", name.c_str());
 }
 
@@ -122,6 +127,14 @@ BwppHipStatus resolve_all(BwppHip *h) {
   };
   for (auto &e : singles)
     if ((s = resolve(h, e.name, e.slot)) != BWPP_HIP_OK) return s;
+  for (int dt = 0; dt < 2; ++dt)
+    for (int ta = 0; ta < 2; ++ta)
+      for (int tb = 0; tb < 2; ++tb)
+        for (int full = 0; full < 2; ++full) {
+          const std::string n = std::string("bwpp_gemm_") + (dt ? "bf16" : "f32") + "_t" + std::to_string(ta) +
+                                std::to_string(tb) + (full ? "_f" : "_e");
+          if ((s = resolve(h, n, &h->gemm[dt][ta][tb][full])) != BWPP_HIP_OK) return s;
+        }
   return BWPP_HIP_OK;
 }
 
@@ -238,6 +251,10 @@ BwppHipStatus bwpp_hip_create(BwppHip **out, int device, const char *code_object
   (void)hipDeviceGetAttribute(&h->cus, hipDeviceAttributeMultiprocessorCount, device);
   if (const char *cfg = getenv("BWPP_ROW_CFG")) h->row_cfg_override = atoi(cfg);
   if (const char *gc = getenv("BWPP_ROW_GRID")) h->row_grid_cap = (uint32_t)strtoul(gc, nullptr, 10);
+  if (const char *gm = getenv("BWPP_GEMM_GROUP_M")) {
+    const uint32_t v = (uint32_t)strtoul(gm, nullptr, 10);
+    if (v > 0) h->gemm_group_m = v;
+  }
 
   const std::string dir = code_object_dir ? std::string(code_object_dir) : library_dir();
   for (const char *mod : kModules) {
@@ -491,14 +508,74 @@ BwppHipStatus bwpp_hip_dispatch_reduce_max_grad_argmax(BwppHip *h, const float *
 
 }  // extern "C"
 
-// ------------------------------------------------- contractions (pending)
+// ------------------------------------------------------------- matmul
+
+namespace {
+
+// Byte range [lo, hi) of a row-major matrix view.
+struct Extent {
+  uintptr_t lo = 0, hi = 0;
+};
+Extent extent(const void *p, uint64_t rows, uint64_t cols, uint64_t ld, uint64_t es) {
+  Extent e;
+  if (!p || rows == 0 || cols == 0) return e;
+  e.lo = (uintptr_t)p;
+  e.hi = e.lo + ((rows - 1) * ld + cols) * es;
+  return e;
+}
+bool overlaps(const Extent &a, const Extent &b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; }
+
+}  // namespace
 
 extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, const void *b, void *c,
                                                   const void *bias, BwppMatmulParams p) {
   BwppHipStatus s = enter(h);
   if (s != BWPP_HIP_OK) return s;
-  (void)a; (void)b; (void)c; (void)bias; (void)p;
-  return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "matmul kernels not built yet");
+  if (!a || !b || !c) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "matmul: NULL a, b or c");
+  if (p.dtype > BWPP_HIP_BF16) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "matmul: unknown dtype %u", p.dtype);
+  if (p.epilogue > BWPP_HIP_EPILOGUE_ADD_SILU)
+    return fail(h, BWPP_HIP_ERR_INVALID_ARG, "matmul: unknown epilogue %u", p.epilogue);
+  const bool ta = p.trans_a != 0, tb = p.trans_b != 0;
+  const uint32_t a_cols = ta ? p.M : p.K, b_cols = tb ? p.K : p.N;
+  const uint32_t lda = p.lda ? p.lda : a_cols, ldb = p.ldb ? p.ldb : b_cols, ldc = p.ldc ? p.ldc : p.N;
+  if (lda < a_cols || ldb < b_cols || ldc < p.N)
+    return fail(h, BWPP_HIP_ERR_INVALID_ARG, "matmul: leading dimension smaller than the row (lda %u ldb %u ldc %u)",
+                lda, ldb, ldc);
+  if (p.M == 0 || p.N == 0) return BWPP_HIP_OK;
+  const bool bf16 = p.dtype == BWPP_HIP_BF16;
+  const uint64_t es = bf16 ? 2 : 4;
+  const Extent ec = extent(c, p.M, p.N, ldc, es);
+  const Extent ea = extent(a, ta ? p.K : p.M, a_cols, lda, es);
+  const Extent eb = extent(b, tb ? p.N : p.K, b_cols, ldb, es);
+  const bool use_bias = (p.epilogue & BWPP_HIP_EPILOGUE_ADD) && bias;
+  const Extent ebias = use_bias ? extent(bias, 1, p.N, p.N, es) : Extent{};
+  if (overlaps(ec, ea) || overlaps(ec, eb) || overlaps(ec, ebias))
+    return fail(h, BWPP_HIP_ERR_ALIAS, "matmul: C overlaps A, B or bias");
+
+  const uint32_t BM = bf16 ? 256 : 128, BN = bf16 ? 256 : 128, BK = bf16 ? 64 : 32;
+  const uint32_t vecw = bf16 ? 8 : 4;  // elements per 16 bytes
+  const bool vec = aligned16(a) && aligned16(b) && aligned16(c) && lda % vecw == 0 && ldb % vecw == 0 &&
+                   ldc % vecw == 0;
+  const bool full = vec && p.M % BM == 0 && p.N % BN == 0 && p.K % BK == 0;
+  BwppGemmArgs g = {};
+  g.a = a;
+  g.b = b;
+  g.bias = use_bias ? bias : nullptr;
+  g.c = c;
+  g.M = p.M;
+  g.N = p.N;
+  g.K = p.K;
+  g.lda = lda;
+  g.ldb = ldb;
+  g.ldc = ldc;
+  g.epilogue = p.epilogue;
+  g.tiles_m = (p.M + BM - 1) / BM;
+  g.tiles_n = (p.N + BN - 1) / BN;
+  g.group_m = h->gemm_group_m;
+  g.vec_ok = vec ? 1u : 0u;
+  const uint64_t tiles = (uint64_t)g.tiles_m * g.tiles_n;
+  if (tiles > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "matmul: too many tiles");
+  return launch(h, h->gemm[bf16 ? 1 : 0][ta][tb][full ? 1 : 0], (uint32_t)tiles, 1, 1, 256, g);
 }
 
 extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, const void *k, const void *v,

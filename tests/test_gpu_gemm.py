@@ -1,0 +1,199 @@
+"""GPU parity of bwpp_hip_dispatch_matmul against the oracle (through the C ABI).
+
+Bars: fp32 within 1e-4 relative max-norm; bf16 inputs
+with fp32 accumulation within 2e-2.  bf16 inputs are rounded to bf16 first
+and the oracle gets their exact fp32 values.  The full C3 shape is checked
+against the oracle on a row subset (rows are independent, so those rows are
+exact comparisons) and against torch's fp32 GEMM on every output."""
+import numpy as np
+import pytest
+
+import bwpp
+from bwpp import synth
+from conftest import rel_max_err
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-4
+BF16_TOL = 2e-2
+EPIS = [(0, False, False), (1, False, True), (2, True, False), (3, True, True)]  # (code, silu, add)
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def f32_dev(x):
+    return _torch().from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+
+
+def bf16_dev(x):
+    """Device bf16 tensor of x rounded to nearest even, and its exact fp32 value."""
+    torch = _torch()
+    bits = synth.to_bf16_bits(x)
+    return torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16), synth.bf16_bits_to_f32(bits)
+
+
+def bf16_host(t):
+    torch = _torch()
+    torch.cuda.synchronize()
+    return synth.bf16_bits_to_f32(t.view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+def f32_host(t):
+    _torch().cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def stored(x, trans):
+    """Storage of logical matrix x: itself, or its transpose (row-major)."""
+    return np.ascontiguousarray(x.T) if trans else x
+
+
+def run(be, dtype, a, b, bias, M, N, K, epi, ta=0, tb=0):
+    torch = _torch()
+    dt = torch.bfloat16 if dtype == bwpp.DType.BF16 else torch.float32
+    c = torch.full((M, N), 7.0, dtype=dt, device="cuda")
+    be.dispatch_matmul(a, b, c, bias, bwpp.MatmulParams(M, N, K, 0, 0, N, int(dtype), epi, ta, tb))
+    return c
+
+
+def test_reference_ramp_fixture_f32(be, golden):
+    """runtime/cpu/test_matmul.c fixture, all epilogues, vs the reference's outputs."""
+    for tag in ("none", "add", "silu", "add_silu"):
+        g = lambda k: golden[f"matmul_ramp4_{tag}/{k}"]
+        epi = (2 if g("silu") else 0) | (1 if g("add") else 0)
+        c = run(be, bwpp.DType.F32, f32_dev(g("a")), f32_dev(g("b")), f32_dev(g("bias")), 4, 4, 4, epi)
+        assert rel_max_err(f32_host(c), g("c")) <= F32_TOL, tag
+    for tag in ("none", "add_silu"):
+        g = lambda k: golden[f"matmul_seed_{tag}/{k}"]
+        M, K = g("a").shape
+        N = g("b").shape[1]
+        epi = (2 if g("silu") else 0) | (1 if g("add") else 0)
+        c = run(be, bwpp.DType.F32, f32_dev(g("a")), f32_dev(g("b")), f32_dev(g("bias")), M, N, K, epi)
+        assert rel_max_err(f32_host(c), g("c")) <= F32_TOL, tag
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (4, 4, 4), (17, 23, 29), (128, 128, 32), (256, 128, 96),
+                                   (200, 300, 70), (384, 256, 512)])
+@pytest.mark.parametrize("epi,silu,add", EPIS)
+def test_f32_vs_oracle(be, oracle, M, N, K, epi, silu, add):
+    a = synth.uniform((M, K), M + K, 0, -1, 1)
+    b = synth.uniform((K, N), N + K, 1, -1, 1)
+    bias = synth.uniform((N,), N, 2, -1, 1)
+    c = run(be, bwpp.DType.F32, f32_dev(a), f32_dev(b), f32_dev(bias), M, N, K, epi)
+    want = oracle.matmul(a, b, bias, apply_silu=silu, apply_bias=add)
+    assert rel_max_err(f32_host(c), want) <= F32_TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 7, 3), (64, 96, 40), (128, 256, 64), (300, 260, 100)])
+@pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("dtype", [bwpp.DType.F32, bwpp.DType.BF16])
+def test_transposed_operands(be, oracle, M, N, K, ta, tb, dtype):
+    """op(A) from a stored [K x M] and op(B) from a stored [N x K]: the GEMMs
+    autodiff emits for matmul (graph_ir.c:1529-1583)."""
+    a = synth.normal((M, K), 3, 0)
+    b = synth.normal((K, N), 3, 1)
+    if dtype == bwpp.DType.BF16:
+        ad, a = bf16_dev(stored(a, ta))
+        bd, b = bf16_dev(stored(b, tb))
+        a = a.T.copy() if ta else a
+        b = b.T.copy() if tb else b
+        tol, host = BF16_TOL, bf16_host
+    else:
+        ad, bd = f32_dev(stored(a, ta)), f32_dev(stored(b, tb))
+        tol, host = F32_TOL, f32_host
+    c = run(be, dtype, ad, bd, None, M, N, K, 0, ta, tb)
+    assert rel_max_err(host(c), oracle.matmul(a, b)) <= tol
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (7, 9, 13), (256, 256, 64), (512, 512, 512), (300, 520, 100),
+                                   (256, 768, 1000), (64, 11008, 64)])
+@pytest.mark.parametrize("epi,silu,add", EPIS)
+def test_bf16_vs_oracle(be, oracle, M, N, K, epi, silu, add):
+    ad, a = bf16_dev(synth.normal((M, K), 11, 0, 0.0, 0.5))
+    bd, b = bf16_dev(synth.normal((K, N), 11, 1, 0.0, 0.5))
+    biasd, bias = bf16_dev(synth.normal((N,), 11, 2, 0.0, 0.5))
+    c = run(be, bwpp.DType.BF16, ad, bd, biasd, M, N, K, epi)
+    want = oracle.matmul(a, b, bias, apply_silu=silu, apply_bias=add)
+    assert rel_max_err(bf16_host(c), want) <= BF16_TOL
+
+
+def test_bias_null_means_zero(be, oracle):
+    ad, a = bf16_dev(synth.normal((256, 64), 5, 0))
+    bd, b = bf16_dev(synth.normal((64, 256), 5, 1))
+    c = run(be, bwpp.DType.BF16, ad, bd, None, 256, 256, 64, 3)  # ADD_SILU, no bias
+    assert rel_max_err(bf16_host(c), oracle.matmul(a, b, None, apply_silu=True)) <= BF16_TOL
+
+
+def test_zero_k_gives_epilogue_of_zero(be):
+    torch = _torch()
+    bias = f32_dev(np.array([1.0, -2.0, 0.5], np.float32))
+    a = torch.zeros(1, dtype=torch.float32, device="cuda")
+    c = run(be, bwpp.DType.F32, a, a, bias, 2, 3, 0, 3)
+    x = np.array([1.0, -2.0, 0.5])
+    want = np.tile(x / (1 + np.exp(-x)), (2, 1))
+    assert np.allclose(f32_host(c), want, rtol=1e-5)
+
+
+def test_alias_and_invalid(be):
+    torch = _torch()
+    a = torch.zeros((64, 64), dtype=torch.float32, device="cuda")
+    b = torch.zeros((64, 64), dtype=torch.float32, device="cuda")
+    with pytest.raises(bwpp.BwppError) as e:
+        be.dispatch_matmul(a, b, a, None, bwpp.MatmulParams(64, 64, 64, 64, 64, 64))
+    assert e.value.status == bwpp.Status.ALIAS
+    with pytest.raises(bwpp.BwppError) as e:
+        be.dispatch_matmul(a, b, b[32:], None, bwpp.MatmulParams(32, 64, 64, 64, 64, 64))
+    assert e.value.status == bwpp.Status.ALIAS
+    c = torch.zeros((64, 64), dtype=torch.float32, device="cuda")
+    with pytest.raises(bwpp.BwppError) as e:
+        be.dispatch_matmul(a, b, c, None, bwpp.MatmulParams(64, 64, 64, 64, 64, 64, 5))
+    assert e.value.status == bwpp.Status.INVALID_ARG
+    with pytest.raises(bwpp.BwppError) as e:
+        be.dispatch_matmul(a, b, c, None, bwpp.MatmulParams(64, 64, 64, 32, 64, 64))
+    assert e.value.status == bwpp.Status.INVALID_ARG
+
+
+def test_c1_f32_256(be, oracle):
+    """Config 1: fp32 C = A·B, M = N = K = 256, A, B ~ U[-1,1]."""
+    a = synth.uniform((256, 256), 0, 0, -1, 1)
+    b = synth.uniform((256, 256), 0, 1, -1, 1)
+    c = run(be, bwpp.DType.F32, f32_dev(a), f32_dev(b), None, 256, 256, 256, 0)
+    assert rel_max_err(f32_host(c), oracle.matmul(a, b)) <= F32_TOL
+
+
+def test_c3_f32_2048(be, oracle):
+    """Config 3 fp32 variant: SiLU(X·W + b) at M = N = K = 2048, U[-1,1]; all
+    outputs vs torch fp32, the first 32 rows vs the oracle."""
+    torch = _torch()
+    n = 2048
+    x = synth.uniform((n, n), 0, 0, -1, 1)
+    w = synth.uniform((n, n), 0, 1, -1, 1)
+    bias = synth.uniform((n,), 0, 2, -1, 1)
+    xd, wd, bd = f32_dev(x), f32_dev(w), f32_dev(bias)
+    c = run(be, bwpp.DType.F32, xd, wd, bd, n, n, n, 3)
+    got = f32_host(c)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ref = torch.nn.functional.silu(xd @ wd + bd).cpu().numpy()
+    assert rel_max_err(got, ref) <= F32_TOL
+    want = oracle.matmul(x[:32], w, bias, apply_silu=True, apply_bias=True)
+    assert rel_max_err(got[:32], want) <= F32_TOL
+
+
+def test_c3_bf16_full(be, oracle):
+    """Config 3: Y = SiLU(X·W + b), X [4096 x 4096], W [4096 x 11008],
+    b [11008], bf16 ~ N(0, 0.02), fp32 accumulation, bf16 out."""
+    torch = _torch()
+    M, K, N = 4096, 4096, 11008
+    xd, x = bf16_dev(synth.normal((M, K), 0, 0, 0.0, 0.02))
+    wd, w = bf16_dev(synth.normal((K, N), 0, 1, 0.0, 0.02))
+    bd, bias = bf16_dev(synth.normal((N,), 0, 2, 0.0, 0.02))
+    c = run(be, bwpp.DType.BF16, xd, wd, bd, M, N, K, 3)
+    got = bf16_host(c)
+    ref = torch.nn.functional.silu(xd.float() @ wd.float() + bd.float()).cpu().numpy()
+    assert rel_max_err(got, ref) <= BF16_TOL
+    rows = np.r_[0:32, M - 32:M]
+    want = oracle.matmul(x[rows], w, bias, apply_silu=True, apply_bias=True)
+    assert rel_max_err(got[rows], want) <= BF16_TOL
