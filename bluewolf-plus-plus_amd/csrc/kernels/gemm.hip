@@ -293,6 +293,219 @@ __device__ __forceinline__ void gemm_bf16(const BwppGemmArgs &a) {
   }
 }
 
+// ------------------------------------------------- bf16, pipelined (full tiles)
+//
+// Register-free staging: every operand byte goes global -> LDS with
+// global_load_lds (16 bytes per lane; the lanes of one instruction fill
+// 1 KiB of LDS in lane order, each lane from its own global address), into
+// a ring of kStages stages of BK = 32.  Three K tiles are in flight while
+// the fourth is multiplied.
+//   K-contiguous operand ("KC": A, or B with TB): LDS [256 rows][32 k],
+//     64-byte rows of four 16-byte chunks, chunk c of row r at
+//     c ^ ((r >> 2) & 3), so the 16 rows read by 16 lanes of a ds_read_b128
+//     hit 16 distinct 16-byte bank groups.
+//   MN-contiguous operand ("MNC": row-major B, or A with TA): LDS
+//     [32 k][256], 512-byte rows, chunk c of row k at c ^ (4 * (k & 3)); the
+//     MFMA operand (8 consecutive k of one row/column per lane) is read with
+//     two ds_read_b64_tr_b16: in each 16-lane group, lane L fetches 4
+//     elements of k-row kb + L/4 at column c0 + 4 * (L % 4), and the
+//     hardware returns to lane j the 4 k-values of column c0 + j.
+// Needs M, N multiples of 256, K a multiple of 32, 16-byte aligned rows.
+
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  // s_waitcnt with expcnt / lgkmcnt at their maxima (gfx9 encoding).
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+constexpr int kPipeStages = 4;
+constexpr int kPipeBK = 32;
+constexpr int kPipeTile = 256 * kPipeBK * 2;  // bytes of one operand tile
+
+__device__ __forceinline__ uint32_t kc_off(uint32_t row, uint32_t c) {
+  return row * 64u + 16u * (c ^ ((row >> 2) & 3u));
+}
+__device__ __forceinline__ uint32_t mnc_off(uint32_t k, uint32_t c) {
+  return k * 512u + 16u * (c ^ (4u * (k & 3u)));
+}
+
+// 16 bytes per lane, global -> LDS (M0 holds the wave's LDS destination;
+// lane l lands at M0 + 16 * l).  Issued as inline asm so that the
+// compiler's conservative LDS-DMA tracking (an s_waitcnt vmcnt(0) before
+// every later LDS read) does not flatten the stage ring: completion is
+// awaited explicitly with wait_vmcnt() + a barrier before a stage is read.
+__device__ __forceinline__ void g2lds16(const void *gptr, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(gptr)
+               : "memory", "m0");
+}
+
+// Source of this lane's 16-byte chunk in 1 KiB block `blk` of an operand
+// tile whose first K index is 0 (the caller adds the K advance).
+template <bool MNC>
+__device__ __forceinline__ const uint16_t *tile_src(const uint16_t *g, uint32_t ld, uint32_t r0, uint32_t blk,
+                                                    int lane) {
+  const uint32_t q = blk * 64u + (uint32_t)lane;
+  if constexpr (!MNC) {
+    const uint32_t row = q >> 2, c = (q & 3u) ^ ((row >> 2) & 3u);
+    return g + (size_t)(r0 + row) * ld + 8u * c;
+  } else {
+    const uint32_t k = q >> 5, c = (q & 31u) ^ (4u * (k & 3u));
+    return g + (size_t)k * ld + r0 + 8u * c;
+  }
+}
+
+// MFMA operand (8 bf16: rows rb + lane%32, k = 16*ks + 8*(lane/32) .. +7).
+template <bool MNC>
+__device__ __forceinline__ bf16x8_t read_operand(const unsigned char *tile, uint32_t rb, int ks, int lane) {
+  if constexpr (!MNC) {
+    const uint32_t row = rb + (uint32_t)(lane & 31);
+    const uint32_t c = (uint32_t)(2 * ks + (lane >> 5));
+    return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(tile + kc_off(row, c)));
+  } else {
+    const uint32_t g = (uint32_t)((lane >> 4) & 3), L = (uint32_t)(lane & 15);
+    const uint32_t col = rb + 16u * (g & 1u) + 4u * (L & 3u);
+    const uint32_t c = col >> 3;
+    const uint32_t sub = (col & 7u) * 2u;
+    const uint32_t k0 = (uint32_t)(16 * ks) + 8u * (g >> 1) + (L >> 2);
+    const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4s_t *)(tile + mnc_off(k0, c) + sub));
+    const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4s_t *)(tile + mnc_off(k0 + 4u, c) + sub));
+    typedef short v8s_t __attribute__((ext_vector_type(8)));
+    const v8s_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+  }
+}
+
+// WM x WN waves (4 or 8); each wave owns a (256/WM) x (256/WN) sub-tile.
+template <bool TA, bool TB, int WM, int WN>
+__device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
+  constexpr int BM = 256, BN = 256;
+  constexpr int NW = WM * WN, NT = 64 * NW;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  constexpr int LPW = 16 / NW;  // 1 KiB DMA blocks per wave per operand tile
+  constexpr int kStage = 2 * kPipeTile;
+  constexpr int kCld = BN + 8;
+  constexpr int kSmem = kPipeStages * kStage > BM * kCld * 2 ? kPipeStages * kStage : BM * kCld * 2;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmem];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  uint32_t tm, tn;
+  tile_coords(a, tm, tn);
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  const uint16_t *A = static_cast<const uint16_t *>(a.a);
+  const uint16_t *B = static_cast<const uint16_t *>(a.b);
+  const uint32_t nk = a.K / kPipeBK;
+
+  // Per-lane DMA sources at K = 0, advanced by a fixed step per K tile.
+  const uint16_t *srcA[LPW], *srcB[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    srcA[i] = tile_src<TA>(A, a.lda, m0, (uint32_t)(wave * LPW + i), lane);
+    srcB[i] = tile_src<!TB>(B, a.ldb, n0, (uint32_t)(wave * LPW + i), lane);
+  }
+  const size_t stepA = TA ? (size_t)kPipeBK * a.lda : (size_t)kPipeBK;
+  const size_t stepB = TB ? (size_t)kPipeBK : (size_t)kPipeBK * a.ldb;
+  const uint32_t lds0 =
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)smem + (uint32_t)(wave * LPW) * 1024u;
+
+  auto issue = [&](uint32_t kt) {
+    const uint32_t st = lds0 + (kt % kPipeStages) * kStage;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) g2lds16(srcA[i] + kt * stepA, st + (uint32_t)i * 1024u);
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) g2lds16(srcB[i] + kt * stepB, st + kPipeTile + (uint32_t)i * 1024u);
+  };
+
+  f32x16_t acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+#pragma unroll
+  for (int st = 0; st < kPipeStages - 1; ++st)
+    if ((uint32_t)st < nk) issue((uint32_t)st);
+
+  constexpr int kPerTile = 2 * LPW;  // DMA instructions per wave per K tile
+  for (uint32_t kt = 0; kt < nk; ++kt) {
+    // This wave's loads for tile kt are done once at most the loads of the
+    // younger tiles are outstanding; the barrier then makes every wave's
+    // part of the tile visible, and frees stage (kt - 1) for reuse.
+    const uint32_t younger = min(nk - 1 - kt, (uint32_t)(kPipeStages - 2));
+    if (younger >= 2) wait_vmcnt<2 * kPerTile>();
+    else if (younger == 1) wait_vmcnt<kPerTile>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    if (kt + kPipeStages - 1 < nk) issue(kt + kPipeStages - 1);
+
+    const unsigned char *As = smem + (kt % kPipeStages) * kStage;
+    const unsigned char *Bs = As + kPipeTile;
+#pragma unroll
+    for (int ks = 0; ks < kPipeBK / 16; ++ks) {
+      bf16x8_t af[FM], bf[FN];
+#pragma unroll
+      for (int j = 0; j < FM; ++j) af[j] = read_operand<TA>(As, (uint32_t)(wm * TM + j * 32), ks, lane);
+#pragma unroll
+      for (int i = 0; i < FN; ++i) bf[i] = read_operand<!TB>(Bs, (uint32_t)(wn * TN + i * 32), ks, lane);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[i], af[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  __syncthreads();
+
+  // Epilogue through LDS (see gemm_bf16).
+  uint16_t *cs = reinterpret_cast<uint16_t *>(smem);
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const uint16_t *bias = static_cast<const uint16_t *>(a.bias);
+  const bool add = (a.epilogue & kEpiAdd) && bias;
+  const bool act = (a.epilogue & kEpiSilu) != 0;
+#pragma unroll
+  for (int i = 0; i < FN; ++i) {
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int ml = wm * TM + j * 32 + lrow;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = wn * TN + i * 32 + q * 8 + lhalf * 4;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float t = acc[i][j][q * 4 + e];
+          if (add) t += bf16_bits_to_f32(bias[n0 + nl + e]);
+          if (act) t = silu(t);
+          v[e] = t;
+        }
+        uint2 o;
+        o.x = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
+        o.y = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+        *reinterpret_cast<uint2 *>(cs + ml * kCld + nl) = o;
+      }
+    }
+  }
+  __syncthreads();
+  uint16_t *C = static_cast<uint16_t *>(a.c);
+  constexpr int kRowChunks = BN / 8;
+#pragma unroll 4
+  for (int it = 0; it < BM * kRowChunks / NT; ++it) {
+    const int q = tid + it * NT;
+    const int row = q / kRowChunks, c = q % kRowChunks;
+    *reinterpret_cast<uint4 *>(C + (size_t)(m0 + row) * a.ldc + n0 + c * 8) =
+        *reinterpret_cast<const uint4 *>(cs + row * kCld + c * 8);
+  }
+}
+
 // ---------------------------------------------------------------- fp32
 
 template <int R, int BK, int NT, bool MNC, bool EDGE>
@@ -483,7 +696,17 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
   extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(256, 256),            \
                                        amdgpu_waves_per_eu(1, 1))) void                  \
       bwpp_gemm_bf16_t##TA##TB##_##SUF(const BwppGemmArgs a) {                            \
-    gemm_bf16<TA, TB, EDGE>(a);                                                           \
+    if constexpr (EDGE)                                                                   \
+      gemm_bf16<TA, TB, true>(a);                                                         \
+    else                                                                                  \
+      gemm_bf16_pipe<TA, TB, 2, 2>(a);                                                    \
+  }
+// 8-wave (2 per SIMD) variant of the pipelined full-tile kernel.
+#define BWPP_GEMM_BF16_W8(TA, TB)                                                          \
+  extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(512, 512),            \
+                                       amdgpu_waves_per_eu(2, 2))) void                  \
+      bwpp_gemm_bf16w8_t##TA##TB##_f(const BwppGemmArgs a) {                              \
+    gemm_bf16_pipe<TA, TB, 2, 4>(a);                                                      \
   }
 #define BWPP_GEMM_F32(TA, TB, EDGE, SUF)                                                   \
   extern "C" __global__ __launch_bounds__(256) void bwpp_gemm_f32_t##TA##TB##_##SUF(     \
@@ -501,4 +724,8 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
   MAC(1, 1, true, e)
 
 BWPP_GEMM_ALL(BWPP_GEMM_BF16)
+BWPP_GEMM_BF16_W8(0, 0)
+BWPP_GEMM_BF16_W8(0, 1)
+BWPP_GEMM_BF16_W8(1, 0)
+BWPP_GEMM_BF16_W8(1, 1)
 BWPP_GEMM_ALL(BWPP_GEMM_F32)

@@ -52,3 +52,40 @@ extern "C" __global__ __launch_bounds__(64) void probe_mfma_16x16x4_f32(ProbeArg
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
   for (int r = 0; r < 4; ++r) p.c[l * 4 + r] = acc[r];
 }
+
+// ds_read_b64_tr_b16: LDS holds s[i] = i (4096 shorts).  Lane l reads at
+// element offset addr(l) = (mode == 0) ? 4 * l : 64 * l; out[l*4 .. l*4+3]
+// receives the four 16-bit results.
+typedef short v4s __attribute__((ext_vector_type(4)));
+struct TrArgs {
+  int *out;
+  int mode;
+};
+extern "C" __global__ __launch_bounds__(64) void probe_ds_read_tr16_b64(TrArgs p) {
+  __shared__ short s[4096];
+  const int l = threadIdx.x;
+  for (int i = l; i < 4096; i += 64) s[i] = (short)i;
+  __syncthreads();
+  const int off = p.mode == 0 ? 4 * l : 64 * l;
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s *)(s + off));
+  for (int e = 0; e < 4; ++e) p.out[l * 4 + e] = r[e];
+}
+
+// global_load_lds (16 bytes per lane): lane l loads ints src[4*(63-l) ..
+// 4*(63-l)+3] into LDS; the 1 KiB of LDS is then copied out in order, so
+// dst shows where each lane's 16 bytes landed.
+struct LdsArgs {
+  const int *src;
+  int *dst;
+};
+extern "C" __global__ __launch_bounds__(64) void probe_global_load_lds16(LdsArgs p) {
+  __shared__ int s[512];
+  const int l = threadIdx.x;
+  for (int i = l; i < 512; i += 64) s[i] = -1;
+  __syncthreads();
+  __builtin_amdgcn_global_load_lds(p.src + 4 * (63 - l), (__attribute__((address_space(3))) void *)s, 16, 0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int i = l; i < 512; i += 64) p.dst[i] = s[i];
+}

@@ -71,7 +71,9 @@ struct BwppHip {
   hipFunction_t col_mask = nullptr;
   // bwpp_gemm_<bf16|f32>_t<TA><TB>_<e|f>: [dtype][ta][tb][full]
   hipFunction_t gemm[2][2][2][2] = {};
+  hipFunction_t gemm_bf16_w8[2][2] = {};  // 8-wave full-tile bf16: [ta][tb]
   uint32_t gemm_group_m = 8;  // BWPP_GEMM_GROUP_M
+  uint32_t gemm_waves = 8;    // BWPP_GEMM_WAVES: 4 or 8 waves for full bf16 tiles
 };
 
 namespace {
@@ -135,6 +137,11 @@ BwppHipStatus resolve_all(BwppHip *h) {
                                 std::to_string(tb) + (full ? "_f" : "_e");
           if ((s = resolve(h, n, &h->gemm[dt][ta][tb][full])) != BWPP_HIP_OK) return s;
         }
+  for (int ta = 0; ta < 2; ++ta)
+    for (int tb = 0; tb < 2; ++tb) {
+      const std::string n = "bwpp_gemm_bf16w8_t" + std::to_string(ta) + std::to_string(tb) + "_f";
+      if ((s = resolve(h, n, &h->gemm_bf16_w8[ta][tb])) != BWPP_HIP_OK) return s;
+    }
   return BWPP_HIP_OK;
 }
 
@@ -251,6 +258,7 @@ BwppHipStatus bwpp_hip_create(BwppHip **out, int device, const char *code_object
   (void)hipDeviceGetAttribute(&h->cus, hipDeviceAttributeMultiprocessorCount, device);
   if (const char *cfg = getenv("BWPP_ROW_CFG")) h->row_cfg_override = atoi(cfg);
   if (const char *gc = getenv("BWPP_ROW_GRID")) h->row_grid_cap = (uint32_t)strtoul(gc, nullptr, 10);
+  if (const char *gw = getenv("BWPP_GEMM_WAVES")) h->gemm_waves = (uint32_t)strtoul(gw, nullptr, 10) == 4 ? 4 : 8;
   if (const char *gm = getenv("BWPP_GEMM_GROUP_M")) {
     const uint32_t v = (uint32_t)strtoul(gm, nullptr, 10);
     if (v > 0) h->gemm_group_m = v;
@@ -552,7 +560,10 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
   if (overlaps(ec, ea) || overlaps(ec, eb) || overlaps(ec, ebias))
     return fail(h, BWPP_HIP_ERR_ALIAS, "matmul: C overlaps A, B or bias");
 
-  const uint32_t BM = bf16 ? 256 : 128, BN = bf16 ? 256 : 128, BK = bf16 ? 64 : 32;
+  // Full-tile kernels: bf16 256 x 256 with K in steps of 32 (pipelined),
+  // fp32 128 x 128 with K in steps of 32; anything else takes the guarded
+  // edge kernels.
+  const uint32_t BM = bf16 ? 256 : 128, BN = bf16 ? 256 : 128, BK = 32;
   const uint32_t vecw = bf16 ? 8 : 4;  // elements per 16 bytes
   const bool vec = aligned16(a) && aligned16(b) && aligned16(c) && lda % vecw == 0 && ldb % vecw == 0 &&
                    ldc % vecw == 0;
@@ -575,6 +586,8 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
   g.vec_ok = vec ? 1u : 0u;
   const uint64_t tiles = (uint64_t)g.tiles_m * g.tiles_n;
   if (tiles > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "matmul: too many tiles");
+  if (bf16 && full && h->gemm_waves == 8)
+    return launch(h, h->gemm_bf16_w8[ta][tb], (uint32_t)tiles, 1, 1, 512, g);
   return launch(h, h->gemm[bf16 ? 1 : 0][ta][tb][full ? 1 : 0], (uint32_t)tiles, 1, 1, 256, g);
 }
 

@@ -197,3 +197,29 @@ def test_c3_bf16_full(be, oracle):
     rows = np.r_[0:32, M - 32:M]
     want = oracle.matmul(x[rows], w, bias, apply_silu=True, apply_bias=True)
     assert rel_max_err(got[rows], want) <= BF16_TOL
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("waves", [4, 8])
+def test_full_tile_kernels(oracle, monkeypatch, ta, tb, waves):
+    """Both full-tile bf16 kernels (4 waves x 128x128, 8 waves x 128x64 per
+    wave), every operand orientation, several K tiles of the stage ring."""
+    torch = _torch()
+    monkeypatch.setenv("BWPP_GEMM_WAVES", str(waves))
+    be = bwpp.HipBackend(0)
+    be.set_stream(torch.cuda.current_stream())
+    try:
+        M, N, K = 512, 256, 32 * 7
+        a = synth.normal((M, K), 21, 0)
+        b = synth.normal((K, N), 21, 1)
+        bias = synth.normal((N,), 21, 2)
+        ad, ah = bf16_dev(stored(a, ta))
+        bd, bh = bf16_dev(stored(b, tb))
+        biasd, biash = bf16_dev(bias)
+        ah = ah.T.copy() if ta else ah
+        bh = bh.T.copy() if tb else bh
+        c = run(be, bwpp.DType.BF16, ad, bd, biasd, M, N, K, 3, ta, tb)
+        want = oracle.matmul(ah, bh, biash, apply_silu=True, apply_bias=True)
+        assert rel_max_err(bf16_host(c), want) <= BF16_TOL
+    finally:
+        be.close()
