@@ -44,4 +44,22 @@ typedef struct {
   uint32_t vec_ok;   /* 1: rows are 16-byte aligned (edge kernels only) */
 } BwppGemmArgs;
 
+/* Attention: O = softmax(scale * Q K^T [causal]) V per (batch, head). */
+typedef struct {
+  const void *q;
+  const void *k;
+  const void *v;
+  void *o;
+  uint32_t M; /* queries */
+  uint32_t N; /* keys */
+  uint32_t ldq, ldk, ldv, ldo;
+  uint32_t heads;
+  uint32_t q_tiles; /* ceil(M / queries per block) */
+  uint64_t q_bs, q_hs, k_bs, k_hs, v_bs, v_hs, o_bs, o_hs;
+  float scale_log2; /* scale * log2(e) (flash path); the plain scale (generic path) */
+  uint32_t causal;
+  uint32_t kdim; /* Q/K head dim (generic path) */
+  uint32_t vdim; /* V/O head dim (generic path) */
+} BwppAttnArgs;
+
 #endif /* BWPP_KARGS_H */

@@ -340,7 +340,7 @@ __device__ __forceinline__ uint32_t mnc_off(uint32_t k, uint32_t c) {
 // awaited explicitly with wait_vmcnt() + a barrier before a stage is read.
 __device__ __forceinline__ void g2lds16(const void *gptr, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(gptr)
-               : "memory", "m0");
+               : "memory");
 }
 
 // Source of this lane's 16-byte chunk in 1 KiB block `blk` of an operand

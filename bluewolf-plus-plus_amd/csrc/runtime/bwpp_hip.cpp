@@ -27,7 +27,7 @@ namespace {
 thread_local std::string g_create_error;
 
 // Code objects built by the package Makefile, all required.
-const char *const kModules[] = {"bwpp_rowops.hsaco", "bwpp_gemm.hsaco"};
+const char *const kModules[] = {"bwpp_rowops.hsaco", "bwpp_gemm.hsaco", "bwpp_attention.hsaco"};
 
 // Row-op kernels: bwpp_row_<op>_v<VPT>_w<WPR>_<f|p>, see rowops.hip.
 enum RowOpId { ROW_SOFTMAX, ROW_RMSNORM, ROW_LAYERNORM, ROW_MAX, ROW_MAXGRAD, ROW_MASK, ROW_NOPS };
@@ -72,6 +72,8 @@ struct BwppHip {
   // bwpp_gemm_<bf16|f32>_t<TA><TB>_<e|f>: [dtype][ta][tb][full]
   hipFunction_t gemm[2][2][2][2] = {};
   hipFunction_t gemm_bf16_w8[2][2] = {};  // 8-wave full-tile bf16: [ta][tb]
+  hipFunction_t attn_flash[2] = {};       // bf16, d = 128: [causal]
+  hipFunction_t attn_generic[2][2] = {};  // [bf16][causal]
   uint32_t gemm_group_m = 8;  // BWPP_GEMM_GROUP_M
   uint32_t gemm_waves = 8;    // BWPP_GEMM_WAVES: 4 or 8 waves for full bf16 tiles
 };
@@ -142,6 +144,14 @@ BwppHipStatus resolve_all(BwppHip *h) {
       const std::string n = "bwpp_gemm_bf16w8_t" + std::to_string(ta) + std::to_string(tb) + "_f";
       if ((s = resolve(h, n, &h->gemm_bf16_w8[ta][tb])) != BWPP_HIP_OK) return s;
     }
+  for (int causal = 0; causal < 2; ++causal) {
+    const char *cs = causal ? "_causal" : "";
+    if ((s = resolve(h, std::string("bwpp_attn_bf16_d128") + cs, &h->attn_flash[causal])) != BWPP_HIP_OK) return s;
+    if ((s = resolve(h, std::string("bwpp_attn_generic_f32") + cs, &h->attn_generic[0][causal])) != BWPP_HIP_OK)
+      return s;
+    if ((s = resolve(h, std::string("bwpp_attn_generic_bf16") + cs, &h->attn_generic[1][causal])) != BWPP_HIP_OK)
+      return s;
+  }
   return BWPP_HIP_OK;
 }
 
@@ -595,6 +605,77 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, 
                                                      void *o, BwppAttentionParams p) {
   BwppHipStatus s = enter(h);
   if (s != BWPP_HIP_OK) return s;
-  (void)q; (void)k; (void)v; (void)o; (void)p;
-  return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention kernels not built yet");
+  if (!q || !k || !v || !o) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "attention: NULL q, k, v or o");
+  if (p.dtype > BWPP_HIP_BF16) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "attention: unknown dtype %u", p.dtype);
+  const uint32_t B = p.batch ? p.batch : 1, H = p.heads ? p.heads : 1;
+  const uint32_t ldq = p.ldq ? p.ldq : p.K, ldk = p.ldk ? p.ldk : p.K;
+  const uint32_t ldv = p.ldv ? p.ldv : p.D, ldo = p.ldo ? p.ldo : p.D;
+  if (ldq < p.K || ldk < p.K || ldv < p.D || ldo < p.D)
+    return fail(h, BWPP_HIP_ERR_INVALID_ARG, "attention: leading dimension smaller than the row");
+  if (p.M == 0 || p.D == 0) return BWPP_HIP_OK;
+  if (p.K == 0 || p.K > 512 || p.D > 512)
+    return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: head dims K=%u D=%u outside 1..512", p.K, p.D);
+  const bool bf16 = p.dtype == BWPP_HIP_BF16;
+  const uint64_t es = bf16 ? 2 : 4;
+  // Default slice strides: [B, H, rows, ld] contiguous.
+  auto def = [](uint64_t st, uint64_t dflt) { return st ? st : dflt; };
+  const uint64_t q_hs = def(p.q_head_stride, (uint64_t)p.M * ldq), q_bs = def(p.q_batch_stride, q_hs * H);
+  const uint64_t k_hs = def(p.k_head_stride, (uint64_t)p.N * ldk), k_bs = def(p.k_batch_stride, k_hs * H);
+  const uint64_t v_hs = def(p.v_head_stride, (uint64_t)p.N * ldv), v_bs = def(p.v_batch_stride, v_hs * H);
+  const uint64_t o_hs = def(p.o_head_stride, (uint64_t)p.M * ldo), o_bs = def(p.o_batch_stride, o_hs * H);
+  // Byte hull of each tensor over all slices; O must not meet Q, K or V.
+  auto hull = [&](const void *ptr, uint64_t bs, uint64_t hs, uint64_t rows, uint64_t cols, uint64_t ld) {
+    Extent e;
+    if (rows == 0 || cols == 0) return e;
+    e.lo = (uintptr_t)ptr;
+    e.hi = e.lo + ((uint64_t)(B - 1) * bs + (uint64_t)(H - 1) * hs + (rows - 1) * ld + cols) * es;
+    return e;
+  };
+  const Extent eo = hull(o, o_bs, o_hs, p.M, p.D, ldo);
+  if (overlaps(eo, hull(q, q_bs, q_hs, p.M, p.K, ldq)) || overlaps(eo, hull(k, k_bs, k_hs, p.N, p.K, ldk)) ||
+      overlaps(eo, hull(v, v_bs, v_hs, p.N, p.D, ldv)))
+    return fail(h, BWPP_HIP_ERR_ALIAS, "attention: O overlaps Q, K or V");
+
+  const float scale = p.scale != 0.0f ? p.scale : 1.0f;
+  BwppAttnArgs g = {};
+  g.q = q;
+  g.k = k;
+  g.v = v;
+  g.o = o;
+  g.M = p.M;
+  g.N = p.N;
+  g.ldq = ldq;
+  g.ldk = ldk;
+  g.ldv = ldv;
+  g.ldo = ldo;
+  g.heads = H;
+  g.q_bs = q_bs;
+  g.q_hs = q_hs;
+  g.k_bs = k_bs;
+  g.k_hs = k_hs;
+  g.v_bs = v_bs;
+  g.v_hs = v_hs;
+  g.o_bs = o_bs;
+  g.o_hs = o_hs;
+  g.causal = p.causal ? 1u : 0u;
+  g.kdim = p.K;
+  g.vdim = p.D;
+  const int causal = p.causal ? 1 : 0;
+  const uint64_t slices = (uint64_t)B * H;
+  const bool flash = bf16 && p.K == 128 && p.D == 128 && p.N > 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
+                     aligned16(o) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0 &&
+                     q_bs % 8 == 0 && q_hs % 8 == 0 && k_bs % 8 == 0 && k_hs % 8 == 0 && v_bs % 8 == 0 &&
+                     v_hs % 8 == 0 && o_bs % 8 == 0 && o_hs % 8 == 0;
+  if (flash) {
+    g.scale_log2 = scale * 1.4426950408889634f;
+    g.q_tiles = (p.M + 255) / 256;
+    const uint64_t grid = slices * g.q_tiles;
+    if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: grid too large");
+    return launch(h, h->attn_flash[causal], (uint32_t)grid, 1, 1, 256, g);
+  }
+  g.scale_log2 = scale;
+  g.q_tiles = (p.M + 15) / 16;
+  const uint64_t grid = slices * g.q_tiles;
+  if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: grid too large");
+  return launch(h, h->attn_generic[bf16 ? 1 : 0][causal], (uint32_t)grid, 1, 1, 256, g);
 }

@@ -1,0 +1,172 @@
+"""GPU parity of bwpp_hip_dispatch_attention against the oracle (C ABI).
+
+The reference computes single-head, unscaled, unmasked fp32 attention
+(runtime/cpu/bwpp_cpu_ref.c:92-144); the build adds batch x heads, a score
+scale and a bottom-right aligned causal mask (oracle_attention_bh_f32).
+Bars: fp32 1e-4 relative max-norm, bf16 inputs with fp32 softmax and
+accumulation 2e-2.  bf16 inputs are rounded first; the oracle sees their
+exact fp32 values.  d = 128 bf16 runs the MFMA flash kernel; everything
+else the generic kernel."""
+import numpy as np
+import pytest
+
+import bwpp
+from bwpp import synth
+from conftest import assert_bits_equal, rel_max_err
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def f32_dev(x):
+    return _torch().from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+
+
+def bf16_dev(x):
+    torch = _torch()
+    bits = synth.to_bf16_bits(np.ascontiguousarray(x, np.float32))
+    return torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16), synth.bf16_bits_to_f32(bits)
+
+
+def host(t):
+    torch = _torch()
+    torch.cuda.synchronize()
+    if t.dtype == torch.bfloat16:
+        return synth.bf16_bits_to_f32(t.view(torch.int16).cpu().numpy().view(np.uint16))
+    return t.cpu().numpy()
+
+
+def params(B, H, M, N, K, D, scale, causal, dtype):
+    return bwpp.AttentionParams(M=M, N=N, K=K, D=D, ldq=K, ldk=K, ldv=D, ldo=D, batch=B, heads=H,
+                                scale=scale, causal=int(causal), dtype=int(dtype))
+
+
+def run(be, q, k, v, B, H, M, N, K, D, scale, causal, dtype):
+    torch = _torch()
+    dt = torch.bfloat16 if dtype == bwpp.DType.BF16 else torch.float32
+    o = torch.full((B, H, M, D), 3.0, dtype=dt, device="cuda")
+    be.dispatch_attention(q, k, v, o, params(B, H, M, N, K, D, scale, causal, dtype))
+    return o
+
+
+def inputs(B, H, M, N, K, D, seed, bf16):
+    q = synth.normal((B, H, M, K), seed, 0)
+    k = synth.normal((B, H, N, K), seed, 1)
+    v = synth.normal((B, H, N, D), seed, 2)
+    if bf16:
+        (qd, q), (kd, k), (vd, v) = bf16_dev(q), bf16_dev(k), bf16_dev(v)
+    else:
+        qd, kd, vd = f32_dev(q), f32_dev(k), f32_dev(v)
+    return (qd, kd, vd), (q, k, v)
+
+
+def test_reference_fixtures_f32(be, golden):
+    """test_metal_parity.c:237-248 fixture and a seeded case, vs the
+    reference's own outputs (scale 1, no mask, one head)."""
+    for name in ("attention_ramp", "attention_seed"):
+        q, k, v = (golden[f"{name}/{t}"] for t in "qkv")
+        M, K = q.shape
+        N, D = v.shape
+        o = run(be, f32_dev(q), f32_dev(k), f32_dev(v), 1, 1, M, N, K, D, 0.0, False, bwpp.DType.F32)
+        assert rel_max_err(host(o)[0, 0], golden[f"{name}/o"]) <= F32_TOL, name
+
+
+@pytest.mark.parametrize("B,H,M,N,K,D", [(1, 1, 1, 1, 1, 1), (2, 3, 37, 37, 16, 24), (1, 2, 70, 130, 64, 64),
+                                         (1, 1, 130, 70, 32, 8), (1, 1, 65, 200, 512, 100)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_generic_f32(be, oracle, B, H, M, N, K, D, causal):
+    (qd, kd, vd), (q, k, v) = inputs(B, H, M, N, K, D, M + N, False)
+    scale = 1.0 / np.sqrt(K)
+    o = run(be, qd, kd, vd, B, H, M, N, K, D, scale, causal, bwpp.DType.F32)
+    assert rel_max_err(host(o), oracle.attention_bh(q, k, v, scale, causal)) <= F32_TOL
+
+
+@pytest.mark.parametrize("B,H,M,N,D", [(1, 2, 100, 100, 64), (2, 1, 33, 90, 32)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_generic_bf16(be, oracle, B, H, M, N, D, causal):
+    (qd, kd, vd), (q, k, v) = inputs(B, H, M, N, D, D, 7, True)
+    scale = 1.0 / np.sqrt(D)
+    o = run(be, qd, kd, vd, B, H, M, N, D, D, scale, causal, bwpp.DType.BF16)
+    assert rel_max_err(host(o), oracle.attention_bh(q, k, v, scale, causal)) <= BF16_TOL
+
+
+@pytest.mark.parametrize("B,H,M,N", [(1, 2, 256, 256), (1, 1, 300, 300), (2, 2, 200, 513), (1, 1, 513, 200),
+                                     (1, 1, 64, 1000), (1, 3, 1024, 1024), (1, 1, 1, 1)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_bf16_d128(be, oracle, B, H, M, N, causal):
+    (qd, kd, vd), (q, k, v) = inputs(B, H, M, N, 128, 128, B * 1000 + M + N, True)
+    scale = 1.0 / np.sqrt(128)
+    o = run(be, qd, kd, vd, B, H, M, N, 128, 128, scale, causal, bwpp.DType.BF16)
+    assert rel_max_err(host(o), oracle.attention_bh(q, k, v, scale, causal)) <= BF16_TOL
+
+
+def test_flash_unscaled_matches_reference_semantics(be, oracle):
+    """scale 0 means 1 (the reference applies no scale)."""
+    (qd, kd, vd), (q, k, v) = inputs(1, 1, 128, 192, 128, 128, 5, True)
+    q2 = q * 0.1  # keep the unscaled scores in a sane range
+    qd2, q2 = bf16_dev(q2)
+    o = run(be, qd2, kd, vd, 1, 1, 128, 192, 128, 128, 0.0, False, bwpp.DType.BF16)
+    assert rel_max_err(host(o), oracle.attention_bh(q2, k, v, 1.0, False)) <= BF16_TOL
+
+
+@pytest.mark.parametrize("dtype", [bwpp.DType.BF16, bwpp.DType.F32])
+def test_causal_first_row_is_first_value(be, dtype):
+    """Causal, M == N: query 0 sees only key 0, so O[0] = V[0] exactly."""
+    bf = dtype == bwpp.DType.BF16
+    (qd, kd, vd), (q, k, v) = inputs(2, 2, 300, 300, 128, 128, 9, bf)
+    o = run(be, qd, kd, vd, 2, 2, 300, 300, 128, 128, 0.0883883, True, dtype)
+    assert_bits_equal(host(o)[:, :, 0, :], v[:, :, 0, :])
+
+
+def test_alias_rejected(be):
+    torch = _torch()
+    x = torch.zeros((1, 1, 64, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(bwpp.BwppError) as e:
+        be.dispatch_attention(x, x.clone(), x.clone(), x, params(1, 1, 64, 64, 128, 128, 0, 0, bwpp.DType.BF16))
+    assert e.value.status == bwpp.Status.ALIAS
+
+
+def _torch_attention(q, k, v, scale, causal):
+    """fp32 math on the GPU (library matmuls), heads in chunks."""
+    torch = _torch()
+    B, H, M, _ = q.shape
+    N = k.shape[2]
+    out = torch.empty((B, H, M, v.shape[3]), dtype=torch.float32, device="cuda")
+    mask = None
+    if causal:
+        mask = torch.arange(N, device="cuda")[None, :] > (torch.arange(M, device="cuda")[:, None] + (N - M))
+    for b in range(B):
+        for h0 in range(0, H, 8):
+            qs = q[b, h0:h0 + 8].float().contiguous()
+            ks = k[b, h0:h0 + 8].float().transpose(1, 2).contiguous()
+            s = torch.matmul(qs, ks) * scale
+            if mask is not None:
+                s = s.masked_fill(mask, float("-inf"))
+            out[b, h0:h0 + 8] = torch.matmul(torch.softmax(s, dim=-1), v[b, h0:h0 + 8].float().contiguous())
+    return out
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_c4_full(be, oracle, causal):
+    """Config 4: B 8, H 32, S 2048, d 128, bf16 Q/K/V ~ N(0,1), scale
+    1/sqrt(128).  Two (b, h) slices vs the oracle; every slice vs torch fp32."""
+    torch = _torch()
+    B, H, S, d = 8, 32, 2048, 128
+    scale = 1.0 / np.sqrt(d)
+    (qd, kd, vd), (q, k, v) = inputs(B, H, S, S, d, d, 0, True)
+    o = run(be, qd, kd, vd, B, H, S, S, d, d, scale, causal, bwpp.DType.BF16)
+    got = host(o)
+    ref = _torch_attention(qd, kd, vd, scale, causal).cpu().numpy()
+    assert rel_max_err(got, ref) <= BF16_TOL
+    for b, h in ((0, 0), (7, 31)):
+        want = oracle.attention_bh(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1], scale, causal)
+        assert rel_max_err(got[b:b + 1, h:h + 1], want) <= BF16_TOL
+    del ref
+    torch.cuda.empty_cache()
