@@ -5,14 +5,15 @@ objects (lib/); this package only binds them.  There is no CPU fallback:
 if the library or a code object is missing, HipBackend() raises.
 """
 from . import _lib, synth
-from ._lib import (AttentionParams, DType, Epilogue, LibraryMissing,
-                   MatmulParams, ReduceParams, RmsnormParams, SoftmaxParams,
-                   Status)
+from ._lib import (AttentionParams, DType, ElementwiseParams, Epilogue,
+                   LibraryMissing, MatmulParams, ReduceParams, RmsnormParams,
+                   SoftmaxParams, Status)
 from .backend import BwppError, HipBackend
 
 __all__ = ["HipBackend", "BwppError", "LibraryMissing", "Status", "DType",
            "Epilogue", "MatmulParams", "SoftmaxParams", "RmsnormParams",
-           "AttentionParams", "ReduceParams", "synth", "load_library"]
+           "AttentionParams", "ReduceParams", "ElementwiseParams", "synth",
+           "load_library"]
 
 
 def load_library():

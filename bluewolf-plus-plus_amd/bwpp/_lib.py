@@ -76,6 +76,11 @@ class ReduceParams(Structure):
                 ("axis", c_int32)]
 
 
+class ElementwiseParams(Structure):
+    _fields_ = [("rows", c_uint32), ("cols", c_uint32), ("ld", c_uint32),
+                ("op", c_uint32), ("bmode", c_uint32)]
+
+
 class Arena(Structure):
     _fields_ = [("buffer", c_void_p), ("capacity", c_size_t),
                 ("offset", c_size_t), ("device", c_int)]
@@ -107,6 +112,11 @@ SIGNATURES = {
     "bwpp_hip_dispatch_reduce_max_mask": (c_int, [_P, _P, _P, ReduceParams]),
     "bwpp_hip_dispatch_reduce_max_grad": (c_int, [_P, _P, _P, _P, ReduceParams]),
     "bwpp_hip_dispatch_reduce_max_grad_argmax": (c_int, [_P, _P, _P, _P, _P, ReduceParams]),
+    "bwpp_hip_dispatch_silu_grad": (c_int, [_P, _P, _P, _P, c_uint64]),
+    "bwpp_hip_dispatch_softmax_grad": (c_int, [_P, _P, _P, _P, SoftmaxParams]),
+    "bwpp_hip_dispatch_rmsnorm_grad": (c_int, [_P, _P, _P, _P, _P, _P, _P, RmsnormParams]),
+    "bwpp_hip_dispatch_reduce_sum": (c_int, [_P, _P, _P, ReduceParams]),
+    "bwpp_hip_dispatch_elementwise": (c_int, [_P, _P, _P, _P, ElementwiseParams]),
     "bwpp_synth_uniform_f32": (None, [_P, c_uint64, c_uint64, c_uint64, c_float, c_float]),
     "bwpp_synth_normal_f32": (None, [_P, c_uint64, c_uint64, c_uint64, c_float, c_float]),
     "bwpp_synth_ramp_f32": (None, [_P, c_uint32, c_uint32, c_float]),
@@ -149,6 +159,6 @@ def load():
 
 
 __all__ = ["Status", "DType", "Epilogue", "MatmulParams", "SoftmaxParams",
-           "RmsnormParams", "AttentionParams", "ReduceParams", "Arena",
+           "RmsnormParams", "AttentionParams", "ReduceParams", "ElementwiseParams", "Arena",
            "SIGNATURES", "load", "LIB_PATH", "LIB_DIR", "HEADER_PATH",
            "LibraryMissing", "byref", "c_void_p", "c_uint16"]

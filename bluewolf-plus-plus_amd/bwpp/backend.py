@@ -13,8 +13,8 @@ from __future__ import annotations
 import ctypes
 
 from . import _lib
-from ._lib import (AttentionParams, MatmulParams, ReduceParams, RmsnormParams,
-                   SoftmaxParams, Status)
+from ._lib import (AttentionParams, ElementwiseParams, MatmulParams, ReduceParams,
+                   RmsnormParams, SoftmaxParams, Status)
 
 
 class BwppError(RuntimeError):
@@ -120,3 +120,20 @@ class HipBackend:
                                         params: ReduceParams):
         self._check(self.lib.bwpp_hip_dispatch_reduce_max_grad_argmax(
             self._h, _ptr(x), _ptr(argmax), _ptr(dy), _ptr(dx), params))
+
+    # ------------------------------------------------------ grad ops / glue
+    def dispatch_silu_grad(self, x, dy, dx, n: int):
+        self._check(self.lib.bwpp_hip_dispatch_silu_grad(self._h, _ptr(x), _ptr(dy), _ptr(dx), n))
+
+    def dispatch_softmax_grad(self, y, dy, dx, params: SoftmaxParams):
+        self._check(self.lib.bwpp_hip_dispatch_softmax_grad(self._h, _ptr(y), _ptr(dy), _ptr(dx), params))
+
+    def dispatch_rmsnorm_grad(self, x, gamma, dy, dx, dgamma, dbeta, params: RmsnormParams):
+        self._check(self.lib.bwpp_hip_dispatch_rmsnorm_grad(
+            self._h, _ptr(x), _ptr(gamma), _ptr(dy), _ptr(dx), _ptr(dgamma), _ptr(dbeta), params))
+
+    def dispatch_reduce_sum(self, x, out, params: ReduceParams):
+        self._check(self.lib.bwpp_hip_dispatch_reduce_sum(self._h, _ptr(x), _ptr(out), params))
+
+    def dispatch_elementwise(self, a, b, out, params: ElementwiseParams):
+        self._check(self.lib.bwpp_hip_dispatch_elementwise(self._h, _ptr(a), _ptr(b), _ptr(out), params))

@@ -62,4 +62,24 @@ typedef struct {
   uint32_t vdim; /* V/O head dim (generic path) */
 } BwppAttnArgs;
 
+/* Grad ops and elementwise glue (grad.hip). */
+typedef struct {
+  const float *a;   /* x, y or the left operand */
+  const float *b;   /* dy or the right operand */
+  const float *gamma;
+  float *out;       /* dx or the result */
+  float *out2;      /* dbeta (bwpp_col_partials_sum) */
+  float *part_g;    /* [nblocks][cols] dgamma partials (rmsnorm_grad) */
+  float *part_b;    /* [nblocks][cols] dbeta partials */
+  uint64_t n;       /* element count (flat ops) */
+  uint32_t rows;
+  uint32_t cols;
+  uint32_t ld;
+  float eps;
+  uint32_t op;      /* elementwise op */
+  uint32_t bmode;   /* broadcast of b: 0 full, 1 row vector [cols], 2 column vector [rows], 3 scalar */
+  uint32_t nparts;  /* partial rows to reduce */
+  uint32_t vec;     /* 1: a, b, out are 16-byte aligned (flat ops) */
+} BwppGradArgs;
+
 #endif /* BWPP_KARGS_H */

@@ -68,10 +68,6 @@ __device__ __forceinline__ void g2lds16(const void *gptr, uint32_t lds_addr) {
 __device__ __forceinline__ uint32_t k_off(uint32_t r, uint32_t c) { return r * 256u + 16u * (c ^ (r & 15u)); }
 __device__ __forceinline__ uint32_t v_off(uint32_t r, uint32_t c) { return r * 256u + 16u * (c ^ (4u * (r & 3u))); }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
-}
-
 template <bool CAUSAL>
 __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
   constexpr int D = 128;
@@ -184,45 +180,57 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
       }
     }
 
-    // Online softmax per query (lane-local + partner lane ^ 32).
+    // Online softmax per query (lane-local + partner lane ^ 32), in base 2:
+    // the running max m is kept in scaled units (scale * log2 e * score),
+    // p = exp2(score * c - m) is one FMA and one v_exp_f32.
+    const float c = a.scale_log2;
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-      const int64_t qi = (int64_t)(q0 + 32u * g + lq);
       float mx = -INFINITY;
+      // Key of register r in block kb is k0 + 4 lh + (32 kb + 8 (r >> 2) +
+      // (r & 3)); visible iff that offset is below `lim` (key < N and, when
+      // causal, key <= query + diag).
+      int64_t lim64 = (int64_t)a.N - (int64_t)(k0 + 4u * lh);
+      if (CAUSAL) {
+        const int64_t c64 = (int64_t)(q0 + 32u * g + lq) + diag + 1 - (int64_t)(k0 + 4u * lh);
+        lim64 = c64 < lim64 ? c64 : lim64;
+      }
+      const int lim = (int)(lim64 < -1 ? -1 : (lim64 > 64 ? 64 : lim64));
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float x = s[kb][g][r] * a.scale_log2;
+          float x = s[kb][g][r];
           if (need_mask) {
-            const uint32_t key = k0 + 32u * kb + 8u * (r >> 2) + 4u * lh + (r & 3);
-            const bool vis = key < a.N && (!CAUSAL || (int64_t)key <= qi + diag);
-            x = vis ? x : -INFINITY;
+            x = (32 * kb + 8 * (r >> 2) + (r & 3)) < lim ? x : -INFINITY;
+            s[kb][g][r] = x;
           }
-          s[kb][g][r] = x;
           mx = fmaxf(mx, x);
         }
       }
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(mrow[g], mx);
+      const float mnew = fmaxf(mrow[g], mx * c);
       const float muse = mnew == -INFINITY ? 0.0f : mnew;
-      const float alpha = exp2f(mrow[g] - muse);
+      const float alpha = __builtin_amdgcn_exp2f(mrow[g] - muse);
       mrow[g] = mnew;
       float sum = 0.0f;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = exp2f(s[kb][g][r] - muse);
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][g][r], c, -muse));
           s[kb][g][r] = p;
           sum += p;
         }
       sum += __shfl_xor(sum, 32, 64);
       lrow[g] = lrow[g] * alpha + sum;
+      // Rescale the output only when some query's maximum moved.
+      if (__ballot(alpha != 1.0f)) {
 #pragma unroll
-      for (int d = 0; d < DB; ++d)
+        for (int d = 0; d < DB; ++d)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[g][d][r] *= alpha;
+          for (int r = 0; r < 16; ++r) o[g][d][r] *= alpha;
+      }
     }
 
     // O^T += V^T P^T over the 4 blocks of 16 keys.

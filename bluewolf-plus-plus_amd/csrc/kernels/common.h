@@ -109,12 +109,14 @@ __device__ __forceinline__ void store_nt4(float *p, const float4 &o) {
   __builtin_nontemporal_store(t, reinterpret_cast<f32x4 *>(p));
 }
 
-// bf16 <-> fp32.  Round to nearest even; NaN stays a quiet NaN.
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+// bf16 <-> fp32.  fp32 -> bf16 uses the gfx950 conversion instruction
+// (v_cvt_pk_bf16_f32: round to nearest even, NaN stays NaN), two values per
+// instruction when packed.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
 }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
   return __uint_as_float((uint32_t)h << 16);

@@ -268,8 +268,8 @@ __device__ __forceinline__ void gemm_bf16(const BwppGemmArgs &a) {
           v[e] = t;
         }
         uint2 o;
-        o.x = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
-        o.y = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+        o.x = pack_bf16x2(v[0], v[1]);
+        o.y = pack_bf16x2(v[2], v[3]);
         *reinterpret_cast<uint2 *>(smem + ml * kCld + nl) = o;
       }
     }
@@ -488,8 +488,8 @@ __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
           v[e] = t;
         }
         uint2 o;
-        o.x = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
-        o.y = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+        o.x = pack_bf16x2(v[0], v[1]);
+        o.y = pack_bf16x2(v[2], v[3]);
         *reinterpret_cast<uint2 *>(cs + ml * kCld + nl) = o;
       }
     }

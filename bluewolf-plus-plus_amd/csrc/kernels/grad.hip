@@ -1,0 +1,177 @@
+// Autodiff grad ops and elementwise glue for gfx950 (fp32).
+//
+// The reference's autodiff (compiler/graph_ir.c:1485-1839) emits these
+// internal ops; the reference has no numeric kernels for them, so the
+// semantics are the closed forms restated in oracle/bwpp_oracle.c:
+//   silu_grad      (graph_ir.c:1709-1720)  dx = dy * s * (1 + x (1 - s))
+//   softmax_grad   (graph_ir.c:1722-1733)  dx = y * (dy - sum(dy * y))
+//   rmsnorm_grad   (graph_ir.c:1735-1789)  dx, dgamma = sum_r dy * xhat,
+//                                          dbeta = sum_r dy
+//   reduce_sum     (graph_ir.c:1410-1455)  along rows or over rows
+//   add/sub/mul/div with broadcasting, broadcast (graph_ir.c:697-770,
+//   1457-1470, 1585-1654)
+// All are HBM-bound: one read of each input, one write of each output,
+// 128-bit accesses where rows are 16-byte aligned.
+#include "common.h"
+#include "../kargs.h"
+
+using namespace bwpp;
+
+namespace {
+
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __forceinline__ float silu_grad1(float x, float dy) {
+  const float s = 1.0f / (1.0f + __expf(-x));
+  return dy * (s * (1.0f + x * (1.0f - s)));
+}
+
+}  // namespace
+
+// Flat elementwise silu_grad over n elements; vec: 16-byte aligned buffers.
+extern "C" __global__ __launch_bounds__(256) void bwpp_silu_grad(const BwppGradArgs g) {
+  const uint64_t stride = (uint64_t)gridDim.x * 256u;
+  const uint64_t n4 = g.vec ? g.n / 4 : 0;
+  const float4 *x4 = reinterpret_cast<const float4 *>(g.a);
+  const float4 *d4 = reinterpret_cast<const float4 *>(g.b);
+  float4 *o4 = reinterpret_cast<float4 *>(g.out);
+  for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n4; i += stride) {
+    const float4 x = load_nt4(reinterpret_cast<const float *>(x4 + i));
+    const float4 d = load_nt4(reinterpret_cast<const float *>(d4 + i));
+    store_nt4(reinterpret_cast<float *>(o4 + i),
+              make_float4(silu_grad1(x.x, d.x), silu_grad1(x.y, d.y), silu_grad1(x.z, d.z), silu_grad1(x.w, d.w)));
+  }
+  for (uint64_t i = n4 * 4 + (uint64_t)blockIdx.x * 256u + threadIdx.x; i < g.n; i += stride)
+    g.out[i] = silu_grad1(g.a[i], g.b[i]);
+}
+
+// Row-wise softmax_grad: one block per row (grid-stride); the dot product is
+// reduced in fp32 across the block, the second pass re-reads the row (L2).
+extern "C" __global__ __launch_bounds__(256) void bwpp_softmax_grad(const BwppGradArgs g) {
+  __shared__ float red[4];
+  for (uint32_t r = blockIdx.x; r < g.rows; r += gridDim.x) {
+    const float *y = g.a + (size_t)r * g.ld;
+    const float *dy = g.b + (size_t)r * g.ld;
+    float *dx = g.out + (size_t)r * g.ld;
+    float dot = 0.0f;
+    for (uint32_t c = threadIdx.x; c < g.cols; c += 256) dot += dy[c] * y[c];
+    dot = block_sum256(dot, red);
+    for (uint32_t c = threadIdx.x; c < g.cols; c += 256) dx[c] = y[c] * (dy[c] - dot);
+  }
+}
+
+// Row-wise rmsnorm_grad with per-block column partials of dgamma / dbeta
+// (summed by bwpp_col_partials_sum).  gamma NULL means 1.
+extern "C" __global__ __launch_bounds__(256) void bwpp_rmsnorm_grad(const BwppGradArgs g) {
+  __shared__ float red[4];
+  extern __shared__ float colacc[];  // [2][cols] when partials are requested
+  const bool parts = g.part_g != nullptr;
+  if (parts)
+    for (uint32_t c = threadIdx.x; c < 2 * g.cols; c += 256) colacc[c] = 0.0f;
+  __syncthreads();
+  for (uint32_t r = blockIdx.x; r < g.rows; r += gridDim.x) {
+    const float *x = g.a + (size_t)r * g.ld;
+    const float *dy = g.b + (size_t)r * g.ld;
+    float *dx = g.out + (size_t)r * g.ld;
+    float ss = 0.0f, t = 0.0f;
+    for (uint32_t c = threadIdx.x; c < g.cols; c += 256) {
+      const float xv = x[c];
+      const float gd = g.gamma ? g.gamma[c] * dy[c] : dy[c];
+      ss += xv * xv;
+      t += xv * gd;
+    }
+    ss = block_sum256(ss, red);
+    t = block_sum256(t, red);
+    const float inv = 1.0f / sqrtf(ss / (float)g.cols + g.eps);
+    const float mdot = inv * t / (float)g.cols;  // mean(xhat * gamma * dy)
+    for (uint32_t c = threadIdx.x; c < g.cols; c += 256) {
+      const float xh = x[c] * inv;
+      const float d = dy[c];
+      const float gd = g.gamma ? g.gamma[c] * d : d;
+      dx[c] = inv * (gd - xh * mdot);
+      if (parts) {
+        colacc[c] += d * xh;
+        colacc[g.cols + c] += d;
+      }
+    }
+  }
+  if (parts) {
+    __syncthreads();
+    for (uint32_t c = threadIdx.x; c < g.cols; c += 256) {
+      g.part_g[(size_t)blockIdx.x * g.cols + c] = colacc[c];
+      g.part_b[(size_t)blockIdx.x * g.cols + c] = colacc[g.cols + c];
+    }
+  }
+}
+
+// out[c] = sum_p part[p][c] for the two partial arrays (dgamma, dbeta); the
+// outputs may be NULL.
+extern "C" __global__ __launch_bounds__(256) void bwpp_col_partials_sum(const BwppGradArgs g) {
+  const uint32_t c = blockIdx.x * 256u + threadIdx.x;
+  if (c >= g.cols) return;
+  float sg = 0.0f, sb = 0.0f;
+  for (uint32_t p = 0; p < g.nparts; ++p) {
+    sg += g.part_g[(size_t)p * g.cols + c];
+    sb += g.part_b[(size_t)p * g.cols + c];
+  }
+  if (g.out) g.out[c] = sg;
+  if (g.out2) g.out2[c] = sb;
+}
+
+// reduce_sum along each row (axis 1): one block per row.
+extern "C" __global__ __launch_bounds__(256) void bwpp_reduce_sum_rows(const BwppGradArgs g) {
+  __shared__ float red[4];
+  for (uint32_t r = blockIdx.x; r < g.rows; r += gridDim.x) {
+    const float *x = g.a + (size_t)r * g.ld;
+    float s = 0.0f;
+    for (uint32_t c = threadIdx.x; c < g.cols; c += 256) s += x[c];
+    s = block_sum256(s, red);
+    if (threadIdx.x == 0) g.out[r] = s;
+  }
+}
+
+// reduce_sum over rows (axis 0): column partials over row bands (blockIdx.y)
+// into part_g, then bwpp_col_partials_sum.
+extern "C" __global__ __launch_bounds__(256) void bwpp_reduce_sum_cols(const BwppGradArgs g) {
+  const uint32_t c = blockIdx.x * 256u + threadIdx.x;
+  if (c >= g.cols) return;
+  const uint32_t band = (g.rows + gridDim.y - 1) / gridDim.y;
+  const uint32_t r0 = blockIdx.y * band, r1 = min(g.rows, r0 + band);
+  float s = 0.0f;
+  for (uint32_t r = r0; r < r1; ++r) s += g.a[(size_t)r * g.ld + c];
+  g.part_g[(size_t)blockIdx.y * g.cols + c] = s;
+}
+
+// Binary elementwise with broadcasting of b, and broadcast itself (op 4:
+// out = b broadcast).  rows x cols, leading dimension ld for a / out (and b
+// when full).
+extern "C" __global__ __launch_bounds__(256) void bwpp_elementwise(const BwppGradArgs g) {
+  for (uint32_t r = blockIdx.x; r < g.rows; r += gridDim.x) {
+    const float *ar = g.a ? g.a + (size_t)r * g.ld : nullptr;
+    float *orow = g.out + (size_t)r * g.ld;
+    for (uint32_t c = threadIdx.x; c < g.cols; c += 256) {
+      float bv;
+      switch (g.bmode) {
+        case 0: bv = g.b[(size_t)r * g.ld + c]; break;
+        case 1: bv = g.b[c]; break;
+        case 2: bv = g.b[r]; break;
+        default: bv = g.b[0]; break;
+      }
+      float v;
+      switch (g.op) {
+        case 0: v = ar[c] + bv; break;
+        case 1: v = ar[c] - bv; break;
+        case 2: v = ar[c] * bv; break;
+        case 3: v = ar[c] / bv; break;
+        default: v = bv; break;
+      }
+      orow[c] = v;
+    }
+  }
+}

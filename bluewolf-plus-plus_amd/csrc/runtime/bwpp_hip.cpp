@@ -27,7 +27,7 @@ namespace {
 thread_local std::string g_create_error;
 
 // Code objects built by the package Makefile, all required.
-const char *const kModules[] = {"bwpp_rowops.hsaco", "bwpp_gemm.hsaco", "bwpp_attention.hsaco"};
+const char *const kModules[] = {"bwpp_rowops.hsaco", "bwpp_gemm.hsaco", "bwpp_attention.hsaco", "bwpp_grad.hsaco"};
 
 // Row-op kernels: bwpp_row_<op>_v<VPT>_w<WPR>_<f|p>, see rowops.hip.
 enum RowOpId { ROW_SOFTMAX, ROW_RMSNORM, ROW_LAYERNORM, ROW_MAX, ROW_MAXGRAD, ROW_MASK, ROW_NOPS };
@@ -74,6 +74,13 @@ struct BwppHip {
   hipFunction_t gemm_bf16_w8[2][2] = {};  // 8-wave full-tile bf16: [ta][tb]
   hipFunction_t attn_flash[2] = {};       // bf16, d = 128: [causal]
   hipFunction_t attn_generic[2][2] = {};  // [bf16][causal]
+  hipFunction_t silu_grad = nullptr, softmax_grad = nullptr, rmsnorm_grad = nullptr, col_partials_sum = nullptr,
+                reduce_sum_rows = nullptr, reduce_sum_cols = nullptr, elementwise = nullptr;
+  // Library-owned device workspace (column partials), grown on demand and
+  // freed by bwpp_hip_destroy.  Calls on one handle are stream-ordered, so
+  // reuse across calls is safe.
+  void *ws = nullptr;
+  size_t ws_bytes = 0;
   uint32_t gemm_group_m = 8;  // BWPP_GEMM_GROUP_M
   uint32_t gemm_waves = 8;    // BWPP_GEMM_WAVES: 4 or 8 waves for full bf16 tiles
 };
@@ -128,6 +135,10 @@ BwppHipStatus resolve_all(BwppHip *h) {
       {"bwpp_row_maskgrad", &h->row_maskgrad},       {"bwpp_col_maskgrad", &h->col_maskgrad},
       {"bwpp_col_max", &h->col_max},                 {"bwpp_col_maxgrad", &h->col_maxgrad},
       {"bwpp_col_mask", &h->col_mask},
+      {"bwpp_silu_grad", &h->silu_grad},             {"bwpp_softmax_grad", &h->softmax_grad},
+      {"bwpp_rmsnorm_grad", &h->rmsnorm_grad},       {"bwpp_col_partials_sum", &h->col_partials_sum},
+      {"bwpp_reduce_sum_rows", &h->reduce_sum_rows}, {"bwpp_reduce_sum_cols", &h->reduce_sum_cols},
+      {"bwpp_elementwise", &h->elementwise},
   };
   for (auto &e : singles)
     if ((s = resolve(h, e.name, e.slot)) != BWPP_HIP_OK) return s;
@@ -298,6 +309,11 @@ BwppHipStatus bwpp_hip_create(BwppHip **out, int device, const char *code_object
 
 void bwpp_hip_destroy(BwppHip *h) {
   if (!h) return;
+  if (h->ws) {
+    (void)hipSetDevice(h->device);
+    (void)hipStreamSynchronize(h->stream);
+    (void)hipFree(h->ws);
+  }
   for (hipModule_t m : h->modules) (void)hipModuleUnload(m);
   delete h;
 }
@@ -678,4 +694,167 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, 
   const uint64_t grid = slices * g.q_tiles;
   if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: grid too large");
   return launch(h, h->attn_generic[bf16 ? 1 : 0][causal], (uint32_t)grid, 1, 1, 256, g);
+}
+
+// ------------------------------------------------------------- grad ops
+
+namespace {
+
+// Ensures the handle's workspace holds `bytes`; waits for queued work on the
+// handle's stream before replacing a smaller buffer.
+BwppHipStatus ensure_ws(BwppHip *h, size_t bytes) {
+  if (h->ws_bytes >= bytes) return BWPP_HIP_OK;
+  if (h->ws) {
+    hipError_t e = hipStreamSynchronize(h->stream);
+    if (e != hipSuccess) return fail(h, BWPP_HIP_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+    (void)hipFree(h->ws);
+    h->ws = nullptr;
+    h->ws_bytes = 0;
+  }
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(h, BWPP_HIP_ERR_OUT_OF_MEMORY, "workspace hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  }
+  h->ws = p;
+  h->ws_bytes = bytes;
+  return BWPP_HIP_OK;
+}
+
+uint32_t row_grid(const BwppHip *h, uint32_t rows) {
+  const uint32_t cap = h->cus > 0 ? 8u * (uint32_t)h->cus : 2048u;
+  return rows < cap ? rows : cap;
+}
+
+}  // namespace
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_silu_grad(BwppHip *h, const float *x, const float *dy, float *dx,
+                                                     uint64_t n) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!x || !dy || !dx) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "silu_grad: NULL pointer");
+  if (n == 0) return BWPP_HIP_OK;
+  BwppGradArgs g = {};
+  g.a = x;
+  g.b = dy;
+  g.out = dx;
+  g.n = n;
+  g.vec = (aligned16(x) && aligned16(dy) && aligned16(dx)) ? 1u : 0u;
+  const uint64_t items = g.vec ? (n + 3) / 4 : n;
+  const uint64_t blocks = (items + 255) / 256;
+  return launch(h, h->silu_grad, (uint32_t)(blocks < 65536 ? blocks : 65536), 1, 1, 256, g);
+}
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_softmax_grad(BwppHip *h, const float *y, const float *dy, float *dx,
+                                                        BwppSoftmaxParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!y || !dy || !dx) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "softmax_grad: NULL pointer");
+  const uint32_t ld = eff_ld(p.ld, p.cols);
+  if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
+  if (p.rows == 0 || p.cols == 0) return BWPP_HIP_OK;
+  BwppGradArgs g = {};
+  g.a = y;
+  g.b = dy;
+  g.out = dx;
+  g.rows = p.rows;
+  g.cols = p.cols;
+  g.ld = ld;
+  return launch(h, h->softmax_grad, row_grid(h, p.rows), 1, 1, 256, g);
+}
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad(BwppHip *h, const float *x, const float *gamma,
+                                                        const float *dy, float *dx, float *dgamma, float *dbeta,
+                                                        BwppRmsnormParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!x || !dy || !dx) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "rmsnorm_grad: NULL x, dy or dx");
+  const uint32_t ld = eff_ld(p.ld, p.cols);
+  if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
+  if (p.cols == 0) return BWPP_HIP_OK;
+  const bool parts = dgamma || dbeta;
+  if (parts && p.cols > 8192)
+    return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "rmsnorm_grad: dgamma/dbeta need cols <= 8192 (got %u)", p.cols);
+  BwppGradArgs g = {};
+  g.a = x;
+  g.b = dy;
+  g.gamma = gamma;
+  g.out = dx;
+  g.rows = p.rows;
+  g.cols = p.cols;
+  g.ld = ld;
+  g.eps = p.eps;
+  const uint32_t grid = p.rows == 0 ? 1u : row_grid(h, p.rows);
+  if (parts) {
+    if ((s = ensure_ws(h, (size_t)2 * grid * p.cols * sizeof(float))) != BWPP_HIP_OK) return s;
+    g.part_g = static_cast<float *>(h->ws);
+    g.part_b = g.part_g + (size_t)grid * p.cols;
+  }
+  if (p.rows > 0 || parts) {
+    if ((s = launch(h, h->rmsnorm_grad, grid, 1, 1, 256, g, parts ? 2u * p.cols * 4u : 0u)) != BWPP_HIP_OK)
+      return s;
+  }
+  if (!parts) return BWPP_HIP_OK;
+  BwppGradArgs r = {};
+  r.part_g = g.part_g;
+  r.part_b = g.part_b;
+  r.out = dgamma;
+  r.out2 = dbeta;
+  r.cols = p.cols;
+  r.nparts = grid;
+  return launch(h, h->col_partials_sum, (p.cols + 255) / 256, 1, 1, 256, r);
+}
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_reduce_sum(BwppHip *h, const float *x, float *out, BwppReduceParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!x || !out) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "reduce_sum: NULL pointer");
+  const uint32_t ld = eff_ld(p.ld, p.cols);
+  if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
+  BwppGradArgs g = {};
+  g.a = x;
+  g.out = out;
+  g.rows = p.rows;
+  g.cols = p.cols;
+  g.ld = ld;
+  if (p.axis != 0) {
+    if (p.rows == 0) return BWPP_HIP_OK;
+    return launch(h, h->reduce_sum_rows, row_grid(h, p.rows), 1, 1, 256, g);
+  }
+  if (p.cols == 0) return BWPP_HIP_OK;
+  const uint32_t bands = p.rows == 0 ? 1u : (p.rows < 64u ? p.rows : 64u);
+  if ((s = ensure_ws(h, (size_t)bands * p.cols * sizeof(float))) != BWPP_HIP_OK) return s;
+  g.part_g = static_cast<float *>(h->ws);
+  if ((s = launch(h, h->reduce_sum_cols, (p.cols + 255) / 256, bands, 1, 256, g)) != BWPP_HIP_OK) return s;
+  BwppGradArgs r = {};
+  r.part_g = g.part_g;
+  r.part_b = g.part_g;
+  r.out = out;
+  r.cols = p.cols;
+  r.nparts = bands;
+  return launch(h, h->col_partials_sum, (p.cols + 255) / 256, 1, 1, 256, r);
+}
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_elementwise(BwppHip *h, const float *a, const float *b, float *out,
+                                                       BwppElementwiseParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (p.op > BWPP_HIP_OP_COPY || p.bmode > BWPP_HIP_BCAST_SCALAR)
+    return fail(h, BWPP_HIP_ERR_INVALID_ARG, "elementwise: bad op %u or broadcast %u", p.op, p.bmode);
+  if (!b || !out || (p.op != BWPP_HIP_OP_COPY && !a))
+    return fail(h, BWPP_HIP_ERR_INVALID_ARG, "elementwise: NULL pointer");
+  const uint32_t ld = eff_ld(p.ld, p.cols);
+  if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
+  if (p.rows == 0 || p.cols == 0) return BWPP_HIP_OK;
+  BwppGradArgs g = {};
+  g.a = p.op == BWPP_HIP_OP_COPY ? nullptr : a;
+  g.b = b;
+  g.out = out;
+  g.rows = p.rows;
+  g.cols = p.cols;
+  g.ld = ld;
+  g.op = p.op;
+  g.bmode = p.bmode;
+  return launch(h, h->elementwise, row_grid(h, p.rows), 1, 1, 256, g);
 }

@@ -135,6 +135,31 @@ typedef struct {
   int32_t axis;
 } BwppReduceParams;
 
+/* Elementwise glue of the autodiff graph (graph_ir.c:697-770, 1457-1470,
+ * 1585-1654): out = a (op) b with b broadcast as selected; op COPY writes
+ * the broadcast b (a unused).  rows x cols with leading dimension ld
+ * (0 = cols) for a, out and a full b. */
+typedef enum {
+  BWPP_HIP_OP_ADD = 0,
+  BWPP_HIP_OP_SUB = 1,
+  BWPP_HIP_OP_MUL = 2,
+  BWPP_HIP_OP_DIV = 3,
+  BWPP_HIP_OP_COPY = 4
+} BwppHipElementwiseOp;
+typedef enum {
+  BWPP_HIP_BCAST_FULL = 0,   /* b is rows x cols */
+  BWPP_HIP_BCAST_ROW = 1,    /* b[cols], repeated for every row */
+  BWPP_HIP_BCAST_COL = 2,    /* b[rows], repeated along each row */
+  BWPP_HIP_BCAST_SCALAR = 3  /* b[0] */
+} BwppHipBroadcast;
+typedef struct {
+  uint32_t rows;
+  uint32_t cols;
+  uint32_t ld;
+  uint32_t op;    /* BwppHipElementwiseOp */
+  uint32_t bmode; /* BwppHipBroadcast */
+} BwppElementwiseParams;
+
 typedef struct BwppHip BwppHip;
 
 /* ---- handle ---- */
@@ -241,6 +266,35 @@ BwppHipStatus bwpp_hip_dispatch_reduce_max_grad(BwppHip *h, const float *mask,
 BwppHipStatus bwpp_hip_dispatch_reduce_max_grad_argmax(
     BwppHip *h, const float *x, const int32_t *argmax, const float *dy,
     float *dx, BwppReduceParams params);
+
+/* ---- autodiff grad ops (graph_ir.c:1485-1839 emits them; the reference
+ * has no numeric kernels, the closed forms are in oracle/bwpp_oracle.h) ---- */
+
+/* BWPP_GOP_SILU_GRAD (graph_ir.c:1709-1720), n contiguous elements:
+ * s = 1/(1+e^-x); dx = dy * s * (1 + x (1 - s)). */
+BwppHipStatus bwpp_hip_dispatch_silu_grad(BwppHip *h, const float *x, const float *dy, float *dx,
+                                          uint64_t n);
+
+/* BWPP_GOP_SOFTMAX_GRAD (graph_ir.c:1722-1733), along rows:
+ * dx = y * (dy - sum_c dy*y). */
+BwppHipStatus bwpp_hip_dispatch_softmax_grad(BwppHip *h, const float *y, const float *dy, float *dx,
+                                             BwppSoftmaxParams params);
+
+/* BWPP_GOP_RMSNORM_GRAD (graph_ir.c:1735-1789): dx for every row, and the
+ * column sums dgamma = sum_r dy * xhat, dbeta = sum_r dy when those
+ * pointers are non-NULL (needs cols <= 8192).  gamma NULL means 1. */
+BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad(BwppHip *h, const float *x, const float *gamma,
+                                             const float *dy, float *dx, float *dgamma,
+                                             float *dbeta, BwppRmsnormParams params);
+
+/* BWPP_GOP_REDUCE_SUM / reduce_to_shape (graph_ir.c:1410-1455): axis 0 sums
+ * over rows (out[cols]), any other axis along each row (out[rows]). */
+BwppHipStatus bwpp_hip_dispatch_reduce_sum(BwppHip *h, const float *x, float *out,
+                                           BwppReduceParams params);
+
+/* add / sub / mul / div with broadcasting, and broadcast (op COPY). */
+BwppHipStatus bwpp_hip_dispatch_elementwise(BwppHip *h, const float *a, const float *b, float *out,
+                                            BwppElementwiseParams params);
 
 /* ---- synthetic inputs (host memory, no device needed) ----
  * Counter-based: element i of (seed, stream) is a pure function of

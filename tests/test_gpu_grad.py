@@ -1,0 +1,121 @@
+"""GPU parity of the autodiff grad ops and elementwise glue (C ABI) against
+the oracle, whose closed forms are pinned by finite differences in
+tests/test_oracle_closed_forms.py.  fp32 bar: 1e-4 relative max-norm; the
+broadcast/elementwise ops are single roundings and must match bit for bit.
+Shapes include config 5's ([4096 x 1024] activations, [65536 x 512]
+attention probabilities)."""
+import numpy as np
+import pytest
+
+import bwpp
+from bwpp import synth
+from conftest import assert_bits_equal, rel_max_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def dev(a):
+    return _torch().from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+
+def host(t):
+    _torch().cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("n", [1, 5, 12289, 4096 * 4096])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_silu_grad(be, oracle, n, offset):
+    torch = _torch()
+    x = synth.normal((n,), n, 0, 0.0, 3.0)
+    dy = synth.normal((n,), n, 1)
+    xb = torch.zeros(n + 1, device="cuda")
+    db = torch.zeros(n + 1, device="cuda")
+    ob = torch.zeros(n + 1, device="cuda")
+    xb[offset:offset + n] = dev(x)
+    db[offset:offset + n] = dev(dy)
+    be.dispatch_silu_grad(xb[offset:], db[offset:], ob[offset:], n)
+    assert rel_max_err(host(ob)[offset:offset + n], oracle.silu_grad(x, dy)) <= TOL
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 7), (9, 4096), (8 * 16 * 512, 512)])
+def test_softmax_grad(be, oracle, rows, cols):
+    torch = _torch()
+    y = oracle.softmax(synth.normal((rows, cols), cols, 0))
+    dy = synth.normal((rows, cols), cols, 1)
+    dx = torch.empty((rows, cols), device="cuda")
+    be.dispatch_softmax_grad(dev(y), dev(dy), dx, bwpp.SoftmaxParams(rows, cols, cols))
+    assert rel_max_err(host(dx), oracle.softmax_grad(y, dy)) <= TOL
+
+
+# cols = 1 is excluded: there dx = inv * g * eps / (x^2 + eps) is pure
+# cancellation and its relative error only measures rounding order.
+@pytest.mark.parametrize("rows,cols", [(1, 8), (5, 33), (300, 1000), (4096, 1024)])
+@pytest.mark.parametrize("with_gamma", [True, False])
+def test_rmsnorm_grad(be, oracle, rows, cols, with_gamma):
+    torch = _torch()
+    x = synth.normal((rows, cols), rows + cols, 0)
+    g = synth.uniform((cols,), cols, 1, 0.5, 1.5) if with_gamma else None
+    dy = synth.normal((rows, cols), rows + cols, 2)
+    dx = torch.empty((rows, cols), device="cuda")
+    dg = torch.full((cols,), 9.0, device="cuda")
+    db = torch.full((cols,), 9.0, device="cuda")
+    be.dispatch_rmsnorm_grad(dev(x), None if g is None else dev(g), dev(dy), dx, dg, db,
+                             bwpp.RmsnormParams(rows, cols, cols, 1e-5))
+    wdx, wdg, wdb = oracle.rmsnorm_grad(x, g, dy, 1e-5)
+    assert rel_max_err(host(dx), wdx) <= TOL
+    assert rel_max_err(host(dg), wdg) <= TOL
+    assert rel_max_err(host(db), wdb) <= TOL
+    # dx alone (no column sums requested)
+    dx2 = torch.empty((rows, cols), device="cuda")
+    be.dispatch_rmsnorm_grad(dev(x), None if g is None else dev(g), dev(dy), dx2, None, None,
+                             bwpp.RmsnormParams(rows, cols, cols, 1e-5))
+    assert rel_max_err(host(dx2), wdx) <= TOL
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 300), (4096, 1024), (1000, 3)])
+@pytest.mark.parametrize("axis", [0, 1])
+def test_reduce_sum(be, oracle, rows, cols, axis):
+    torch = _torch()
+    x = synth.normal((rows, cols), rows * cols, 0)
+    out = torch.empty(cols if axis == 0 else rows, device="cuda")
+    be.dispatch_reduce_sum(dev(x), out, bwpp.ReduceParams(rows, cols, cols, axis))
+    assert rel_max_err(host(out), oracle.reduce_sum(x, axis)) <= TOL
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("bmode", [0, 1, 2, 3])
+def test_elementwise(be, op, bmode):
+    torch = _torch()
+    rows, cols = 13, 70
+    a = synth.normal((rows, cols), 1, 0)
+    bshape = {0: (rows, cols), 1: (cols,), 2: (rows,), 3: (1,)}[bmode]
+    b = synth.uniform(bshape, 2, 1, 0.5, 2.0)
+    out = torch.empty((rows, cols), device="cuda")
+    be.dispatch_elementwise(dev(a), dev(b), out, bwpp.ElementwiseParams(rows, cols, cols, op, bmode))
+    bb = b if bmode == 0 else b[None, :] if bmode == 1 else b[:, None] if bmode == 2 else b.reshape(1, 1)
+    bb = np.broadcast_to(bb, (rows, cols)).astype(np.float32)
+    want = {0: a + bb, 1: a - bb, 2: a * bb, 3: a / bb, 4: bb}[op].astype(np.float32)
+    assert_bits_equal(host(out), want)
+
+
+def test_grad_invalid_args(be):
+    torch = _torch()
+    x = torch.zeros(8, device="cuda")
+    with pytest.raises(bwpp.BwppError):
+        be.dispatch_silu_grad(x, None, x, 8)
+    with pytest.raises(bwpp.BwppError) as e:
+        be.dispatch_elementwise(x, x, x, bwpp.ElementwiseParams(2, 4, 4, 9, 0))
+    assert e.value.status == bwpp.Status.INVALID_ARG
+    big = torch.zeros((2, 9000), device="cuda")
+    with pytest.raises(bwpp.BwppError) as e:
+        be.dispatch_rmsnorm_grad(big, None, big, big.clone(), torch.zeros(9000, device="cuda"), None,
+                                 bwpp.RmsnormParams(2, 9000, 9000, 1e-5))
+    assert e.value.status == bwpp.Status.UNSUPPORTED
