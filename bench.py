@@ -17,8 +17,12 @@ stream the kernels run on.  `cpu_baseline` = the oracle (this repo's C
 restatement of runtime/cpu/bwpp_cpu_ref.c) timed for the same five operators
 on one host core, at full size.
 
-Extra contraction configs (C3 GEMM, C4 attention) are reported under "ops"
-once their kernels exist; they are not part of `value`.
+The contraction configs run in the same invocation and are reported under
+"extras" (not part of `value`): C3 bf16 SiLU(X W + b) 4096 x 4096 x 11008
+and its fp32 2048^3 variant (TFLOP/s vs dense MFMA peak), C4 attention
+B8 H32 S2048 d128 bf16 unmasked and causal (causal FLOPs counted as half),
+and C1's 256^3 fp32 GEMM latency.  Each has a CPU oracle timing on a
+bounded slice (rows or heads are independent, so the rate extrapolates).
 """
 from __future__ import annotations
 
@@ -37,6 +41,8 @@ sys.path.insert(0, PKG)
 
 METRIC = "fused matmul & attention TFLOP/s, norm/softmax GB/s on 1 MI355X; % of roofline"
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+F32_PEAK_TFLOPS = 157.3
 ROWS, COLS = 8192, 4096
 F = 4  # bytes per fp32
 
@@ -179,6 +185,109 @@ def cpu_baseline_c2(seed, reps):
     }
 
 
+def _events_us(torch, fn, iters, warmup=3):
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(iters):
+        fn()
+    e.record(stream)
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters * 1e3
+
+
+def _bf16(torch, x):
+    from bwpp import synth
+    return torch.from_numpy(synth.to_bf16_bits(x).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def extras(be, torch, seed, iters, with_cpu):
+    """Contraction configs C3, C3-fp32, C4 (both masks) and C1."""
+    import bwpp
+    from bwpp import synth
+    out = {}
+    orc = None
+    if with_cpu:
+        sys.path.insert(0, ROOT)
+        from oracle.oracle import Oracle
+        orc = Oracle()
+
+    # C3: Y = SiLU(X W + b), bf16 ~ N(0, 0.02), fp32 accumulation
+    M, K, N = 4096, 4096, 11008
+    xh = synth.normal((M, K), seed, 0, 0.0, 0.02)
+    wh = synth.normal((K, N), seed, 1, 0.0, 0.02)
+    bh = synth.normal((N,), seed, 2, 0.0, 0.02)
+    x, w, b = _bf16(torch, xh), _bf16(torch, wh), _bf16(torch, bh)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    p = bwpp.MatmulParams(M, N, K, K, N, N, int(bwpp.DType.BF16), 3, 0, 0)
+    us = _events_us(torch, lambda: be.dispatch_matmul(x, w, y, b, p), iters)
+    fl = 2.0 * M * N * K
+    c3 = {"kernel": "bwpp_gemm_bf16w8_t00_f", "us_per_launch": round(us, 1),
+          "TFLOP_s": round(fl / us / 1e6, 1), "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    if orc is not None:
+        rows = 32
+        xr = synth.bf16_bits_to_f32(synth.to_bf16_bits(xh[:rows]))
+        wr = synth.bf16_bits_to_f32(synth.to_bf16_bits(wh))
+        br = synth.bf16_bits_to_f32(synth.to_bf16_bits(bh))
+        t0 = time.perf_counter()
+        orc.matmul(xr, wr, br, apply_silu=True, apply_bias=True)
+        dt = time.perf_counter() - t0
+        c3["cpu"] = {"GFLOP_s": round(2.0 * rows * N * K / dt / 1e9, 3), "cores": 1, "kind": "port",
+                     "sample": f"first {rows} rows (exact rows; extrapolated rate)"}
+    out["c3_gemm_bf16_bias_silu"] = c3
+    del x, w, y, xh, wh
+
+    # C3 fp32 variant: 2048^3, U[-1, 1]
+    n = 2048
+    xf = torch.from_numpy(synth.uniform((n, n), seed, 0, -1, 1)).cuda()
+    wf = torch.from_numpy(synth.uniform((n, n), seed, 1, -1, 1)).cuda()
+    bf = torch.from_numpy(synth.uniform((n,), seed, 2, -1, 1)).cuda()
+    yf = torch.empty((n, n), device="cuda")
+    p = bwpp.MatmulParams(n, n, n, n, n, n, int(bwpp.DType.F32), 3, 0, 0)
+    us = _events_us(torch, lambda: be.dispatch_matmul(xf, wf, yf, bf, p), iters)
+    fl = 2.0 * n ** 3
+    out["c3_gemm_f32_2048"] = {"kernel": "bwpp_gemm_f32_t00_f", "us_per_launch": round(us, 1),
+                               "TFLOP_s": round(fl / us / 1e6, 1),
+                               "frac_f32_peak": round(fl / us / 1e6 / F32_PEAK_TFLOPS, 4)}
+    # C1: 256^3 fp32 (latency)
+    a1, b1 = xf[:256, :256].contiguous(), wf[:256, :256].contiguous()
+    c1 = torch.empty((256, 256), device="cuda")
+    p = bwpp.MatmulParams(256, 256, 256, 256, 256, 256)
+    us = _events_us(torch, lambda: be.dispatch_matmul(a1, b1, c1, None, p), iters)
+    out["c1_gemm_f32_256"] = {"us_per_launch": round(us, 2), "TFLOP_s": round(2.0 * 256 ** 3 / us / 1e6, 2)}
+    del xf, wf, yf
+
+    # C4: attention B 8, H 32, S 2048, d 128, bf16 ~ N(0, 1)
+    B, H, S, d = 8, 32, 2048, 128
+    qh = synth.normal((B, H, S, d), seed, 0)
+    kh = synth.normal((B, H, S, d), seed, 1)
+    vh = synth.normal((B, H, S, d), seed, 2)
+    q, k, v = _bf16(torch, qh), _bf16(torch, kh), _bf16(torch, vh)
+    o = torch.empty_like(q)
+    full = 4.0 * B * H * S * S * d
+    for causal in (0, 1):
+        p = bwpp.AttentionParams(M=S, N=S, K=d, D=d, ldq=d, ldk=d, ldv=d, ldo=d, batch=B, heads=H,
+                                 scale=d ** -0.5, causal=causal, dtype=int(bwpp.DType.BF16))
+        us = _events_us(torch, lambda: be.dispatch_attention(q, k, v, o, p), iters)
+        fl = full / 2 if causal else full
+        entry = {"kernel": "bwpp_attn_bf16_d128" + ("_causal" if causal else ""),
+                 "us_per_launch": round(us, 1), "TFLOP_s": round(fl / us / 1e6, 1),
+                 "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
+        if orc is not None:
+            sl = lambda t: synth.bf16_bits_to_f32(synth.to_bf16_bits(t[:1, :1]))
+            t0 = time.perf_counter()
+            orc.attention_bh(sl(qh), sl(kh), sl(vh), d ** -0.5, bool(causal))
+            dt = time.perf_counter() - t0
+            entry["cpu"] = {"GFLOP_s": round(fl / (B * H) / dt / 1e9, 3), "cores": 1, "kind": "port",
+                            "sample": "one (batch, head) slice (extrapolated rate)"}
+        out["c4_attention_causal" if causal else "c4_attention"] = entry
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -188,6 +297,7 @@ def main():
     ap.add_argument("--nbuf", type=int, default=3, help="rotating input/output buffer sets")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-extras", action="store_true", help="skip the C1/C3/C4 contraction configs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -247,6 +357,10 @@ def main():
         out["cpu_baseline"] = cpu_baseline_c2(args.seed, args.cpu_reps)
     else:
         out["cpu_baseline"] = None
+    del bench
+    if not args.no_extras:
+        torch.cuda.empty_cache()
+        out["extras"] = extras(be, torch, args.seed, 20, not args.no_cpu)
     be.close()
     print(json.dumps(out))
 
