@@ -129,6 +129,8 @@ class C2Bench:
 
 
 def time_c2(bench, steps, warmup):
+    """The timed region: `steps` passes of the five operators, back to back
+    on one stream, bracketed by synchronizations and HIP events."""
     torch = bench.torch
     ops = list(C2_BYTES)
     stream = torch.cuda.current_stream()
@@ -137,22 +139,87 @@ def time_c2(bench, steps, warmup):
         for op in ops:
             bench.launch(op, k % bench.nbuf)
             k += 1
-    ev = {op: [] for op in ops}
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    s.record(stream)
     for _ in range(steps):
         for op in ops:
-            s = torch.cuda.Event(enable_timing=True)
-            e = torch.cuda.Event(enable_timing=True)
-            s.record(stream)
             bench.launch(op, k % bench.nbuf)
-            e.record(stream)
-            ev[op].append((s, e))
             k += 1
+    e.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per_op_ms = {op: float(np.mean([s.elapsed_time(e) for s, e in ev[op]])) for op in ops}
-    return wall, per_op_ms
+    return wall, s.elapsed_time(e) * 1e-3
+
+
+def time_c2_ops(bench, reps):
+    """Average launch duration per operator: `reps` back-to-back launches
+    over the rotating buffer sets, between two events on the launch stream."""
+    torch = bench.torch
+    stream = torch.cuda.current_stream()
+    out = {}
+    for op in C2_BYTES:
+        for i in range(bench.nbuf):
+            bench.launch(op, i)
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for i in range(reps):
+            bench.launch(op, i % bench.nbuf)
+        e.record(stream)
+        torch.cuda.synchronize()
+        out[op] = s.elapsed_time(e) / reps
+    return out
+
+
+def copy_calibration(bench, launches):
+    """A plain copy of known size (X -> Y, 128 MiB each way) through the
+    elementwise kernel, for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    import bwpp
+    p = bwpp.ElementwiseParams(ROWS, COLS, COLS, 4, 0)
+    for i in range(launches):
+        j = i % bench.nbuf
+        bench.be.dispatch_elementwise(None, bench.x[j], bench.y[j], p)
+    bench.torch.cuda.synchronize()
+
+
+def traffic_from_pmc(fetch_dir, write_dir):
+    """HBM bytes per launch from two rocprofv3 --pmc runs (FETCH_SIZE, then
+    WRITE_SIZE, in KiB per dispatch).  Each counter is scaled by what it
+    reads for the copy calibration (bwpp_elementwise moving a known
+    134,217,728 bytes each way).  Returns {kernel: record}."""
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        vals = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(f, newline="") as fh:
+                for row in csv.DictReader(fh):
+                    if row["Counter_Name"] != counter:
+                        continue
+                    name = row["Kernel_Name"]
+                    if name.startswith("bwpp_"):
+                        vals.setdefault(name, []).append(float(row["Counter_Value"]))
+        return {k: float(np.median(v)) for k, v in vals.items()}
+
+    fetch = per_kernel(fetch_dir, "FETCH_SIZE")
+    write = per_kernel(write_dir, "WRITE_SIZE")
+    known = ROWS * COLS * 4
+    f_scale = known / (fetch["bwpp_elementwise"] * 1024.0)
+    w_scale = known / (write["bwpp_elementwise"] * 1024.0)
+    out = {"_calibration": {"kernel": "bwpp_elementwise (copy)", "bytes_each_way": known,
+                            "fetch_kib": fetch["bwpp_elementwise"], "write_kib": write["bwpp_elementwise"],
+                            "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}}
+    for k in sorted(set(fetch) & set(write)):
+        if k == "bwpp_elementwise":
+            continue
+        fb = fetch[k] * 1024.0 * f_scale
+        wb = write[k] * 1024.0 * w_scale
+        out[k] = {"fetch_bytes": int(fb), "write_bytes": int(wb), "traffic": int(fb + wb)}
+    return out
 
 
 def cpu_baseline_c2(seed, reps):
@@ -298,7 +365,20 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true", help="skip the C1/C3/C4 contraction configs")
+    ap.add_argument("--op-reps", type=int, default=30, help="launches per operator for per-kernel timing")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="N",
+                    help="also run N plain copies of known size (for scaling --pmc byte counters)")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="no GPU: turn two rocprofv3 --pmc output dirs into profiles/traffic.json")
     args = ap.parse_args()
+
+    if args.traffic_from:
+        t = traffic_from_pmc(*args.traffic_from)
+        with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as f:
+            json.dump(t, f, indent=1, sort_keys=True)
+            f.write("\n")
+        print(json.dumps(t, indent=1, sort_keys=True))
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (single-GPU kernels; "
@@ -315,20 +395,27 @@ def main():
 
     bench = C2Bench(be, torch, args.seed, args.nbuf)
     torch.cuda.synchronize()
-    wall, per_op_ms = time_c2(bench, args.steps, args.warmup)
+    wall, gpu_s = time_c2(bench, args.steps, args.warmup)
+    per_op_ms = time_c2_ops(bench, args.op_reps)
+    if args.copy_calibration:
+        copy_calibration(bench, args.copy_calibration)
     step_bytes = sum(C2_BYTES.values())
     ms_per_step = wall / args.steps * 1e3
     value = step_bytes / (wall / args.steps) / 1e9
 
     dom = max(per_op_ms, key=per_op_ms.get)
     achieved = C2_BYTES[dom] / (per_op_ms[dom] * 1e-3) / 1e9
-    traffic = load_traffic().get(C2_KERNEL[dom])
+    tr = load_traffic().get(C2_KERNEL[dom])
+    traffic = tr["traffic"] if tr else None
     ops = {}
     for op, ms in per_op_ms.items():
         gbs = C2_BYTES[op] / (ms * 1e-3) / 1e9
         ops[op] = {"kernel": C2_KERNEL[op], "us_per_launch": round(ms * 1e3, 2),
                    "algorithmic_bytes": C2_BYTES[op], "GB_s": round(gbs, 1),
                    "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        t = load_traffic().get(C2_KERNEL[op])
+        if t:
+            ops[op]["traffic"] = t["traffic"]
 
     out = {
         "metric": METRIC,
@@ -338,6 +425,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
+        "gpu_ms_per_step": round(gpu_s / args.steps * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
