@@ -26,9 +26,10 @@
  *  - launches are asynchronous on the handle's stream; bwpp_hip_sync() waits
  *    (the reference waits inside every dispatch, dispatch_stub.m:139-140);
  *  - the function cache is filled once in bwpp_hip_create() and read-only
- *    afterwards, so one handle may be used from several threads as long as
- *    they do not race on the stream setting (the reference's function-static
- *    PSO caches are not thread-safe, dispatch_stub.m:81).
+ *    afterwards (the reference's function-static PSO caches are not
+ *    thread-safe, dispatch_stub.m:81), but a handle also holds its stream,
+ *    its last-error text and the grad ops' workspace: use one handle per
+ *    host thread, or serialise calls on a shared one.
  */
 #ifndef BWPP_HIP_H
 #define BWPP_HIP_H
@@ -83,14 +84,15 @@ typedef struct {
   uint32_t trans_b;  /* 0 = B row-major [K x N] */
 } BwppMatmulParams;
 
-/* dispatch_stub.h:18-22 */
+/* dispatch_stub.h:18-22.  ld is the row stride of x and y (0 = cols). */
 typedef struct {
   uint32_t rows;
   uint32_t cols;
   uint32_t ld;
 } BwppSoftmaxParams;
 
-/* dispatch_stub.h:24-29; also used by LayerNorm and the norm grads. */
+/* dispatch_stub.h:24-29; also used by LayerNorm and the norm grads.
+ * ld is the row stride of x, y and dy (0 = cols). */
 typedef struct {
   uint32_t rows;
   uint32_t cols;
