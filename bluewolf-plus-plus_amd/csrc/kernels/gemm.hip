@@ -30,6 +30,8 @@
 // block b is remapped to tile (b % 8) * (T / 8) + b / 8 (when 8 | T), giving
 // each XCD a contiguous run of tiles; runs are walked group_m tile-rows at a
 // time so tiles that share A rows and B columns meet in the same L2.
+#include <type_traits>
+
 #include "common.h"
 #include "../kargs.h"
 
@@ -56,7 +58,12 @@ __device__ __forceinline__ void tile_coords(const BwppGemmArgs &a, uint32_t &tm,
   tn = idx / rows;
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+// x / (1 + e^-x) with the hardware exp2 and reciprocal (about 2 ulp):
+// e^-x overflows to +inf for x < -88 and the result is then -0, as the
+// reference's x / (1 + expf(-x)).
+__device__ __forceinline__ float silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+}
 
 // ---------------------------------------------------------------- bf16
 
@@ -381,7 +388,22 @@ __device__ __forceinline__ bf16x8_t read_operand(const unsigned char *tile, uint
   }
 }
 
+template <bool V>
+using bool_tag = std::integral_constant<bool, V>;
+
 // WM x WN waves (4 or 8); each wave owns a (256/WM) x (256/WN) sub-tile.
+//
+// Schedule of one K tile (two 16-deep MFMA k-steps), per wave:
+//   phase A: the k-step-0 MFMAs, interleaved with the LDS reads of k-step 1
+//            and the DMA of K tile kt + 3 into the stage freed by kt - 1;
+//   then:    lgkmcnt(0) (this wave is done reading tile kt), vmcnt down to
+//            the tiles younger than kt + 1, barrier (tile kt + 1 is in LDS
+//            for every wave, and nobody reads tile kt any more);
+//   phase B: the k-step-1 MFMAs, interleaved with the LDS reads of k-step 0
+//            of tile kt + 1.
+// The MFMA pipe thus always has work queued while LDS reads and DMA issue,
+// and there is one barrier per K tile.  sched_barrier(0) pins the order the
+// source gives (the DMA is inline asm, which the scheduler cannot classify).
 template <bool TA, bool TB, int WM, int WN>
 __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
   constexpr int BM = 256, BN = 256;
@@ -390,8 +412,10 @@ __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
   constexpr int LPW = 16 / NW;  // 1 KiB DMA blocks per wave per operand tile
   constexpr int kStage = 2 * kPipeTile;
   constexpr int kCld = BN + 8;
-  constexpr int kSmem = kPipeStages * kStage > BM * kCld * 2 ? kPipeStages * kStage : BM * kCld * 2;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmem];
+  constexpr int kRing = kPipeStages * kStage;
+  constexpr int kEpi = BM * kCld * 2;
+  constexpr int kBiasOff = kRing > kEpi ? kRing : kEpi;  // bias row (bf16) after both
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kBiasOff + BN * 2];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -402,6 +426,11 @@ __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
   const uint16_t *A = static_cast<const uint16_t *>(a.a);
   const uint16_t *B = static_cast<const uint16_t *>(a.b);
   const uint32_t nk = a.K / kPipeBK;
+  const uint16_t *bias = static_cast<const uint16_t *>(a.bias);
+  const bool add = (a.epilogue & kEpiAdd) && bias;
+  const bool act = (a.epilogue & kEpiSilu) != 0;
+
+  const uint16_t *bias_s = reinterpret_cast<const uint16_t *>(smem + kBiasOff);
 
   // Per-lane DMA sources at K = 0, advanced by a fixed step per K tile.
   const uint16_t *srcA[LPW], *srcB[LPW];
@@ -415,12 +444,13 @@ __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
   const uint32_t lds0 =
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)smem + (uint32_t)(wave * LPW) * 1024u;
 
-  auto issue = [&](uint32_t kt) {
+  // DMA instruction d (0 .. 2*LPW-1) of K tile kt.
+  auto dma = [&](int d, uint32_t kt) {
     const uint32_t st = lds0 + (kt % kPipeStages) * kStage;
-#pragma unroll
-    for (int i = 0; i < LPW; ++i) g2lds16(srcA[i] + kt * stepA, st + (uint32_t)i * 1024u);
-#pragma unroll
-    for (int i = 0; i < LPW; ++i) g2lds16(srcB[i] + kt * stepB, st + kPipeTile + (uint32_t)i * 1024u);
+    if (d < LPW)
+      g2lds16(srcA[d] + kt * stepA, st + (uint32_t)d * 1024u);
+    else
+      g2lds16(srcB[d - LPW] + kt * stepB, st + kPipeTile + (uint32_t)(d - LPW) * 1024u);
   };
 
   f32x16_t acc[FN][FM];
@@ -431,59 +461,120 @@ __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+  // fa/fb[0]: operands of k-step 0, [1]: of k-step 1.
+  bf16x8_t fa[2][FM], fb[2][FN];
+  constexpr int kReads = FM + FN, kMfma = FM * FN, kDma = 2 * LPW;
+  static_assert(kReads <= kMfma && kDma <= kMfma, "interleave needs an MFMA slot per read and DMA");
+
+  auto stage_ptr = [&](uint32_t kt) { return smem + (kt % kPipeStages) * kStage; };
+  auto read = [&](auto buf, int r, const unsigned char *As, int ks) {
+    constexpr int b = decltype(buf)::value ? 1 : 0;
+    if (r < FM)
+      fa[b][r] = read_operand<TA>(As, (uint32_t)(wm * TM + r * 32), ks, lane);
+    else
+      fb[b][r - FM] = read_operand<!TB>(As + kPipeTile, (uint32_t)(wn * TN + (r - FM) * 32), ks, lane);
+  };
+  auto mfma = [&](auto buf, int s) {
+    constexpr int b = decltype(buf)::value ? 1 : 0;
+    const int i = s / FM, j = s % FM;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][i], fa[b][j], acc[i][j], 0, 0, 0);
+  };
+
+  // The tile's 256 bias values (512 bytes, 16-byte aligned) are copied to
+  // LDS by the first half of wave 0, ahead of its first K tile, so the
+  // prologue wait and barrier publish them and the epilogue never waits on a
+  // global load.
+  if (add && wave == 0 && lane < BN / 8)
+    g2lds16(bias + n0 + 8 * lane,
+            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)smem + (uint32_t)kBiasOff);
 #pragma unroll
   for (int st = 0; st < kPipeStages - 1; ++st)
-    if ((uint32_t)st < nk) issue((uint32_t)st);
-
-  constexpr int kPerTile = 2 * LPW;  // DMA instructions per wave per K tile
-  for (uint32_t kt = 0; kt < nk; ++kt) {
-    // This wave's loads for tile kt are done once at most the loads of the
-    // younger tiles are outstanding; the barrier then makes every wave's
-    // part of the tile visible, and frees stage (kt - 1) for reuse.
-    const uint32_t younger = min(nk - 1 - kt, (uint32_t)(kPipeStages - 2));
-    if (younger >= 2) wait_vmcnt<2 * kPerTile>();
-    else if (younger == 1) wait_vmcnt<kPerTile>();
-    else wait_vmcnt<0>();
-    __syncthreads();
-    if (kt + kPipeStages - 1 < nk) issue(kt + kPipeStages - 1);
-
-    const unsigned char *As = smem + (kt % kPipeStages) * kStage;
-    const unsigned char *Bs = As + kPipeTile;
+    if ((uint32_t)st < nk) {
 #pragma unroll
-    for (int ks = 0; ks < kPipeBK / 16; ++ks) {
-      bf16x8_t af[FM], bf[FN];
-#pragma unroll
-      for (int j = 0; j < FM; ++j) af[j] = read_operand<TA>(As, (uint32_t)(wm * TM + j * 32), ks, lane);
-#pragma unroll
-      for (int i = 0; i < FN; ++i) bf[i] = read_operand<!TB>(Bs, (uint32_t)(wn * TN + i * 32), ks, lane);
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int j = 0; j < FM; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[i], af[j], acc[i][j], 0, 0, 0);
+      for (int d = 0; d < kDma; ++d) dma(d, (uint32_t)st);
     }
+  if (nk >= 3) wait_vmcnt<2 * kDma>();
+  else if (nk == 2) wait_vmcnt<kDma>();
+  else wait_vmcnt<0>();
+  __syncthreads();
+  if (nk > 0) {
+#pragma unroll
+    for (int r = 0; r < kReads; ++r) read(bool_tag<false>{}, r, stage_ptr(0), 0);
   }
+
+  // One K tile; DMA: issue tile kt + 3, NEXT: a tile kt + 1 exists.
+  auto ktile = [&](uint32_t kt, auto dma_tag, auto next_tag) {
+    constexpr bool kDmaOn = decltype(dma_tag)::value, kNext = decltype(next_tag)::value;
+    const unsigned char *cur = stage_ptr(kt);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < kMfma; ++s) {
+      mfma(bool_tag<false>{}, s);
+      __builtin_amdgcn_sched_barrier(0);
+      if (s < kReads) {
+        read(bool_tag<true>{}, s, cur, 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (kDmaOn) {
+        if (s < kDma) {
+          dma(s, kt + kPipeStages - 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    if constexpr (kNext) {
+      // Tiles issued after kt + 1 may stay in flight.
+      const uint32_t younger = min(nk - 2 - kt, (uint32_t)(kPipeStages - 2));
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): done reading tile kt
+      if (younger >= 2) wait_vmcnt<2 * kDma>();
+      else if (younger == 1) wait_vmcnt<kDma>();
+      else wait_vmcnt<0>();
+      __syncthreads();
+    }
+    const unsigned char *nxt = stage_ptr(kt + 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < kMfma; ++s) {
+      mfma(bool_tag<true>{}, s);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kNext) {
+        if (s < kReads) {
+          read(bool_tag<false>{}, s, nxt, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  };
+
+  uint32_t kt = 0;
+  for (; kt + kPipeStages - 1 < nk; ++kt) ktile(kt, bool_tag<true>{}, bool_tag<true>{});
+  for (; kt + 1 < nk; ++kt) ktile(kt, bool_tag<false>{}, bool_tag<true>{});
+  if (kt < nk) ktile(kt, bool_tag<false>{}, bool_tag<false>{});
   __syncthreads();
 
   // Epilogue through LDS (see gemm_bf16).
   uint16_t *cs = reinterpret_cast<uint16_t *>(smem);
   const int lrow = lane & 31, lhalf = lane >> 5;
-  const uint16_t *bias = static_cast<const uint16_t *>(a.bias);
-  const bool add = (a.epilogue & kEpiAdd) && bias;
-  const bool act = (a.epilogue & kEpiSilu) != 0;
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
 #pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      const int ml = wm * TM + j * 32 + lrow;
+    for (int q = 0; q < 4; ++q) {
+      const int nl = wn * TN + i * 32 + q * 8 + lhalf * 4;
+      float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (add) {
+        const uint2 raw = *reinterpret_cast<const uint2 *>(bias_s + nl);
+        bv[0] = __uint_as_float(raw.x << 16);
+        bv[1] = __uint_as_float(raw.x & 0xffff0000u);
+        bv[2] = __uint_as_float(raw.y << 16);
+        bv[3] = __uint_as_float(raw.y & 0xffff0000u);
+      }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int nl = wn * TN + i * 32 + q * 8 + lhalf * 4;
+      for (int j = 0; j < FM; ++j) {
+        const int ml = wm * TM + j * 32 + lrow;
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float t = acc[i][j][q * 4 + e];
-          if (add) t += bf16_bits_to_f32(bias[n0 + nl + e]);
+          float t = acc[i][j][q * 4 + e] + bv[e];
           if (act) t = silu(t);
           v[e] = t;
         }

@@ -593,7 +593,8 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
   const uint32_t vecw = bf16 ? 8 : 4;  // elements per 16 bytes
   const bool vec = aligned16(a) && aligned16(b) && aligned16(c) && lda % vecw == 0 && ldb % vecw == 0 &&
                    ldc % vecw == 0;
-  const bool full = vec && p.M % BM == 0 && p.N % BN == 0 && p.K % BK == 0;
+  // The full-tile kernels also fetch the bias row with 16-byte copies.
+  const bool full = vec && (!use_bias || aligned16(bias)) && p.M % BM == 0 && p.N % BN == 0 && p.K % BK == 0;
   BwppGemmArgs g = {};
   g.a = a;
   g.b = b;
