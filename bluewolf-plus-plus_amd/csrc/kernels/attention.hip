@@ -6,10 +6,12 @@
 // a bottom-right aligned causal mask (keys n > m + N - M excluded); the MSL
 // kernel it replaces is codegen_metal.c:435-556.
 //
-// Layout of the work: a block of 4 waves owns 256 queries of one
-// (batch, head); each wave owns 64 queries as two 32-query groups.  Keys
-// stream through LDS in tiles of 64 (K and V, 16 KiB each for d = 128) in a
-// 3-stage ring filled by global -> LDS DMA.
+// Layout of the work: a block of 8 waves (two per SIMD) owns 256 queries of
+// one (batch, head); each wave owns 32 queries.  Keys stream through LDS in
+// tiles of 64 (K and V, 16 KiB each for d = 128) in a 3-stage ring filled
+// by global -> LDS DMA.  Two waves per SIMD let one wave's softmax (VALU)
+// run while the other's MFMAs issue; 32 queries per wave keep the
+// registers (Q^T operands, S^T tile, O^T accumulators) under 256 per wave.
 //
 // Why S^T: the wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16
 // (MFMA "A" = a 32-key block of K, "B" = Q^T held in registers).  The
@@ -24,7 +26,12 @@
 // ds_read_b64_tr_b16 at exactly those key rows.
 //
 // Softmax runs in base 2: scores are multiplied by scale * log2(e) and
-// exponentiated with v_exp_f32.
+// exponentiated with v_exp_f32.  The exponent offset (running maximum) is
+// only raised when a tile's maximum exceeds it by more than kLazy (log2
+// units): probabilities then stay below 2^kLazy, the common factor cancels
+// in O = (sum p v) / (sum p), and the O rescale is skipped on most tiles.
+#include <type_traits>
+
 #include "common.h"
 #include "../kargs.h"
 
@@ -38,11 +45,13 @@ typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kQW = 64;                 // queries per wave
-constexpr int kBQ = kWaves * kQW;       // queries per block
+constexpr int kWaves = 4;               // generic path
+constexpr int kFW = 8;                  // flash path: waves per block
+constexpr int kQW = 32;                 // queries per wave
+constexpr int kBQ = kFW * kQW;          // queries per block
 constexpr int kBKV = 64;                // keys per tile
 constexpr int kStages = 3;
+constexpr float kLazy = 8.0f;
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -77,6 +86,7 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
   constexpr int kStage = 2 * kTile;
   constexpr int kRing = kStages * kStage;
   constexpr int kOut = kBQ * D * 2;
+  constexpr int kBlkPW = 16 / kFW;  // 1 KiB DMA blocks per wave per K (or V) tile
   __shared__ __attribute__((aligned(1024))) unsigned char smem[kRing > kOut ? kRing : kOut];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -94,6 +104,7 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
   const uint32_t qb0 = qt * kBQ;                    // block's first query
   const uint32_t q0 = qb0 + (uint32_t)wave * kQW;   // wave's first query
   const uint32_t lq = (uint32_t)(lane & 31), lh = (uint32_t)(lane >> 5);
+  const uint32_t qi = q0 + lq;                      // this lane's query
 
   // Key tiles this block needs.
   uint32_t kend = a.N;
@@ -104,133 +115,144 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
   }
   const uint32_t nkt = (kend + kBKV - 1) / kBKV;
 
-  // Q^T operands: lane holds query q0 + 32 g + lq, d = 16 ks + 8 lh .. +7.
-  bf16x8_t qf[2][KS];
+  // Q^T operands: lane holds query qi, d = 16 ks + 8 lh .. +7.
+  bf16x8_t qf[KS];
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const uint32_t qi = q0 + 32u * g + lq;
+  for (int ks = 0; ks < KS; ++ks) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (qi < a.M) v = *reinterpret_cast<const uint4 *>(Q + (size_t)qi * a.ldq + 16 * ks + 8 * lh);
+    qf[ks] = __builtin_bit_cast(bf16x8_t, v);
+  }
+
+  // DMA: each wave loads kBlkPW of the 16 1-KiB blocks of the K tile and of
+  // the V tile.  Rows past N re-read row N - 1 (finite data; masked to -inf).
+  // Lane l of block i fills 16-byte slot l of it: key row r = 4 i' + l / 16
+  // of the tile (i' the block index), physical chunk l % 16, which holds the
+  // logical chunk given by the K / V swizzles below.
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)smem;
+  uint32_t dma_row[kBlkPW], dma_kcol[kBlkPW], dma_vcol[kBlkPW];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (qi < a.M) v = *reinterpret_cast<const uint4 *>(Q + (size_t)qi * a.ldq + 16 * ks + 8 * lh);
-      qf[g][ks] = __builtin_bit_cast(bf16x8_t, v);
+  for (int i = 0; i < kBlkPW; ++i) {
+    const uint32_t q = (uint32_t)(wave * kBlkPW + i) * 64u + (uint32_t)lane;
+    const uint32_t r = q >> 4, pc = q & 15u;
+    dma_row[i] = r;
+    dma_kcol[i] = 8u * (pc ^ (r & 15u));
+    dma_vcol[i] = 8u * (pc ^ (4u * (r & 3u)));
+  }
+  auto issue = [&](uint32_t t) {
+    const uint32_t st = lds0 + (t % kStages) * kStage + (uint32_t)(wave * kBlkPW) * 1024u;
+#pragma unroll
+    for (int i = 0; i < kBlkPW; ++i) {
+      uint32_t key = t * kBKV + dma_row[i];
+      key = key < a.N ? key : a.N - 1;
+      g2lds16(K + (size_t)key * a.ldk + dma_kcol[i], st + (uint32_t)i * 1024u);
+      g2lds16(V + (size_t)key * a.ldv + dma_vcol[i], st + kTile + (uint32_t)i * 1024u);
+    }
+  };
+  constexpr int kDmaPerTile = 2 * kBlkPW;
+
+  f32x16_t o[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[d][r] = 0.0f;
+  float mrow = -INFINITY, lrow = 0.0f;
+  const float c = a.scale_log2;
+
+  // Per-lane LDS read offsets inside a stage.  K operand of k-step ks, key
+  // block kb: koff[ks] + kb * 32 rows.  V^T operand of d block d, keys
+  // 32 kb + 16 kq (+8 for the upper four): voff[d] + (32 kb + 16 kq (+8))
+  // rows; the V swizzle depends on the row only through r & 3, which those
+  // row steps keep.
+  const uint32_t grp = (uint32_t)((lane >> 4) & 3), L = (uint32_t)(lane & 15);
+  uint32_t koff[KS], voff[DB];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = k_off(lq, 2u * ks + lh);
+  {
+    const uint32_t kbase = 4u * (grp >> 1) + (L >> 2);
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const uint32_t col = 32u * d + 16u * (grp & 1u) + 4u * (L & 3u);
+      voff[d] = kTile + v_off(kbase, col >> 3) + (col & 7u) * 2u;
     }
   }
 
-  // DMA: each wave loads 4 of the 16 1-KiB blocks of the K tile and of the
-  // V tile.  Rows past N re-read row N - 1 (finite data; masked to -inf).
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)smem;
-  auto issue = [&](uint32_t t) {
-    const uint32_t st = lds0 + (t % kStages) * kStage;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t blk = (uint32_t)(wave * 4 + i);
-      const uint32_t q = blk * 64u + (uint32_t)lane;  // 16-byte slot
-      const uint32_t r = q >> 4, pc = q & 15u;
-      uint32_t key = t * kBKV + r;
-      key = key < a.N ? key : a.N - 1;
-      g2lds16(K + (size_t)key * a.ldk + 8u * (pc ^ (r & 15u)), st + blk * 1024u);
-      g2lds16(V + (size_t)key * a.ldv + 8u * (pc ^ (4u * (r & 3u))), st + kTile + blk * 1024u);
-    }
-  };
-
-  f32x16_t o[2][DB];
-#pragma unroll
-  for (int g = 0; g < 2; ++g)
-#pragma unroll
-    for (int d = 0; d < DB; ++d)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[g][d][r] = 0.0f;
-  float mrow[2] = {-INFINITY, -INFINITY}, lrow[2] = {0.0f, 0.0f};
-
-#pragma unroll
-  for (int s = 0; s < kStages - 1; ++s)
-    if ((uint32_t)s < nkt) issue((uint32_t)s);
-
-  for (uint32_t t = 0; t < nkt; ++t) {
-    if (t + 1 < nkt) wait_vmcnt<8>();  // tile t + 1 may still be in flight
-    else wait_vmcnt<0>();
-    __syncthreads();
-    if (t + kStages - 1 < nkt) issue(t + kStages - 1);
-
-    const uint32_t k0 = t * kBKV;
-    // Whole tile masked for this wave's queries: nothing to do.
-    if (CAUSAL && (int64_t)k0 > (int64_t)(q0 + kQW - 1) + diag) continue;
-    const bool need_mask = (k0 + kBKV > a.N) || (CAUSAL && (int64_t)(k0 + kBKV - 1) > (int64_t)q0 + diag);
-
-    const unsigned char *Ks = smem + (t % kStages) * kStage;
-    const unsigned char *Vs = Ks + kTile;
-
-    // S^T blocks: s[kb][g] = K[kb keys] . Q^T[g queries].
-    f32x16_t s[2][2];
+  // One key tile.  MASK: some (key, query) pair of the tile is masked out.
+  auto tile = [&](auto mask_tag, const unsigned char *Ks, uint32_t k0) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    // S^T blocks: s[kb] = K[32 kb .. 32 kb + 31] . Q^T.
+    f32x16_t s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[kb][g][r] = 0.0f;
+      for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const uint32_t row = 32u * kb + lq;
-        const uint32_t c = 2u * ks + lh;
-        const bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(Ks + k_off(row, c)));
-#pragma unroll
-        for (int g = 0; g < 2; ++g)
-          s[kb][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[g][ks], s[kb][g], 0, 0, 0);
+        const bf16x8_t kf =
+            __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(Ks + koff[ks] + 32u * 256u * kb));
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb], 0, 0, 0);
       }
     }
-
-    // Online softmax per query (lane-local + partner lane ^ 32), in base 2:
-    // the running max m is kept in scaled units (scale * log2 e * score),
-    // p = exp2(score * c - m) is one FMA and one v_exp_f32.
-    const float c = a.scale_log2;
+    // Keep two K reads ahead of the MFMAs instead of hoisting all sixteen
+    // (which would not fit the 256 registers of a two-wave-per-SIMD wave).
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      float mx = -INFINITY;
+    for (int i = 0; i < 2 * KS - 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+
+    // Online softmax for this lane's query (plus partner lane ^ 32).
+    float mx = -INFINITY;
+    if constexpr (MASK) {
       // Key of register r in block kb is k0 + 4 lh + (32 kb + 8 (r >> 2) +
       // (r & 3)); visible iff that offset is below `lim` (key < N and, when
       // causal, key <= query + diag).
       int64_t lim64 = (int64_t)a.N - (int64_t)(k0 + 4u * lh);
       if (CAUSAL) {
-        const int64_t c64 = (int64_t)(q0 + 32u * g + lq) + diag + 1 - (int64_t)(k0 + 4u * lh);
+        const int64_t c64 = (int64_t)qi + diag + 1 - (int64_t)(k0 + 4u * lh);
         lim64 = c64 < lim64 ? c64 : lim64;
       }
       const int lim = (int)(lim64 < -1 ? -1 : (lim64 > 64 ? 64 : lim64));
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = s[kb][g][r];
-          if (need_mask) {
-            x = (32 * kb + 8 * (r >> 2) + (r & 3)) < lim ? x : -INFINITY;
-            s[kb][g][r] = x;
-          }
-          mx = fmaxf(mx, x);
-        }
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(mrow[g], mx * c);
-      const float muse = mnew == -INFINITY ? 0.0f : mnew;
-      const float alpha = __builtin_amdgcn_exp2f(mrow[g] - muse);
-      mrow[g] = mnew;
-      float sum = 0.0f;
-#pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][g][r], c, -muse));
-          s[kb][g][r] = p;
-          sum += p;
+          const float x = (32 * kb + 8 * (r >> 2) + (r & 3)) < lim ? s[kb][r] : -INFINITY;
+          s[kb][r] = x;
+          mx = fmaxf(mx, x);
         }
-      sum += __shfl_xor(sum, 32, 64);
-      lrow[g] = lrow[g] * alpha + sum;
-      // Rescale the output only when some query's maximum moved.
-      if (__ballot(alpha != 1.0f)) {
+    } else {
 #pragma unroll
-        for (int d = 0; d < DB; ++d)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) o[g][d][r] *= alpha;
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+    // Raise the offset only past the lazy margin (or from -inf).
+    float alpha = 1.0f;
+    if (mx > mrow + kLazy) {
+      alpha = __builtin_amdgcn_exp2f(mrow - mx);  // 0 when mrow is -inf
+      mrow = mx;
+    }
+    const float muse = mrow == -INFINITY ? 0.0f : mrow;
+    float sum = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], c, -muse));
+        s[kb][r] = p;
+        sum += p;
       }
+    sum += __shfl_xor(sum, 32, 64);
+    lrow = lrow * alpha + sum;
+    if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
     }
 
     // O^T += V^T P^T over the 4 blocks of 16 keys.
@@ -238,55 +260,89 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int kq = 0; kq < 2; ++kq) {
-        bf16x8_t pf[2];
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          const f32x16_t &p = s[kb][g];
-          const int r0 = 8 * kq;
-          uint4 w;
-          w.x = pack_bf16x2(p[r0 + 0], p[r0 + 1]);
-          w.y = pack_bf16x2(p[r0 + 2], p[r0 + 3]);
-          w.z = pack_bf16x2(p[r0 + 4], p[r0 + 5]);
-          w.w = pack_bf16x2(p[r0 + 6], p[r0 + 7]);
-          pf[g] = __builtin_bit_cast(bf16x8_t, w);
-        }
+        const int r0 = 8 * kq;
+        uint4 w;
+        w.x = pack_bf16x2(s[kb][r0 + 0], s[kb][r0 + 1]);
+        w.y = pack_bf16x2(s[kb][r0 + 2], s[kb][r0 + 3]);
+        w.z = pack_bf16x2(s[kb][r0 + 4], s[kb][r0 + 5]);
+        w.w = pack_bf16x2(s[kb][r0 + 6], s[kb][r0 + 7]);
+        const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, w);
         // Key rows of this lane's operand: 32 kb + 16 kq + 4 h (+8).
-        const uint32_t grp = (uint32_t)((lane >> 4) & 3), L = (uint32_t)(lane & 15);
-        const uint32_t kbase = 32u * kb + 16u * kq + 4u * (grp >> 1) + (L >> 2);
+        constexpr uint32_t kRowB = 256u;
+        const uint32_t rstep = (32u * kb + 16u * kq) * kRowB;
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
-          const uint32_t col = 32u * d + 16u * (grp & 1u) + 4u * (L & 3u);
-          const uint32_t c = col >> 3, sub = (col & 7u) * 2u;
-          const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Vs + v_off(kbase, c) + sub));
-          const v4s_t hi =
-              __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Vs + v_off(kbase + 8u, c) + sub));
+          const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Ks + voff[d] + rstep));
+          const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Ks + voff[d] + rstep + 8u * kRowB));
           const v8s_t vv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, vv);
-#pragma unroll
-          for (int g = 0; g < 2; ++g)
-            o[g][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[g], o[g][d], 0, 0, 0);
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), pf, o[d], 0, 0, 0);
         }
       }
     }
+    // Two V^T operands (four transposing reads) ahead of the MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 4 * DB - 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  };
+
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st)
+    if ((uint32_t)st < nkt) issue((uint32_t)st);
+
+  // Tiles before t_mask need no mask for any wave of the block; the rest
+  // go through the masked variant.  Two loops (not one with a branch) keep
+  // a single copy of the O accumulators live.
+  uint32_t t_mask = a.N / kBKV;  // first tile with keys past N
+  if (CAUSAL) {
+    // First tile holding a key past query qb0's limit qb0 + diag.
+    const int64_t first_hidden = (int64_t)qb0 + diag + 1;
+    const uint32_t tc = first_hidden <= 0 ? 0u : (uint32_t)min<int64_t>(first_hidden / kBKV, (int64_t)nkt);
+    t_mask = min(t_mask, tc);
+  }
+  t_mask = min(t_mask, nkt);
+
+  auto step = [&](uint32_t t) {
+    if (t + 1 < nkt) wait_vmcnt<kDmaPerTile>();  // tile t + 1 may still be in flight
+    else wait_vmcnt<0>();
+    __syncthreads();
+    if (t + kStages - 1 < nkt) issue(t + kStages - 1);
+    // The stage base goes through readfirstlane so that loop strength
+    // reduction does not turn every LDS address into its own induction
+    // variable (it would need ~50 registers); the per-read offsets are then
+    // base + lane offset + an immediate.
+    return smem + __builtin_amdgcn_readfirstlane((t % kStages) * kStage);
+  };
+  for (uint32_t t = 0; t < t_mask; ++t) {
+    const unsigned char *Ks = step(t);
+    tile(std::integral_constant<bool, false>{}, Ks, t * kBKV);
+  }
+  for (uint32_t t = t_mask; t < nkt; ++t) {
+    const unsigned char *Ks = step(t);
+    const uint32_t k0 = t * kBKV;
+    // Whole tile masked for this wave's queries: nothing to do.
+    if (CAUSAL && (int64_t)k0 > (int64_t)(q0 + kQW - 1) + diag) continue;
+    tile(std::integral_constant<bool, true>{}, Ks, k0);
   }
   __syncthreads();
 
   // O = O^T / l, staged through LDS ([query][d] bf16 per wave), then stored
   // with 16-byte row chunks.
   uint16_t *os = reinterpret_cast<uint16_t *>(smem) + (size_t)wave * kQW * D;
-#pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const float inv = lrow[g] > 0.0f ? 1.0f / lrow[g] : 0.0f;
-    const uint32_t ql = 32u * g + lq;
+  {
+    const float inv = lrow > 0.0f ? 1.0f / lrow : 0.0f;
 #pragma unroll
     for (int d = 0; d < DB; ++d)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const uint32_t dd = 32u * d + 8u * q4 + 4u * lh;
         uint2 w;
-        w.x = pack_bf16x2(o[g][d][4 * q4 + 0] * inv, o[g][d][4 * q4 + 1] * inv);
-        w.y = pack_bf16x2(o[g][d][4 * q4 + 2] * inv, o[g][d][4 * q4 + 3] * inv);
-        *reinterpret_cast<uint2 *>(os + ql * D + dd) = w;
+        w.x = pack_bf16x2(o[d][4 * q4 + 0] * inv, o[d][4 * q4 + 1] * inv);
+        w.y = pack_bf16x2(o[d][4 * q4 + 2] * inv, o[d][4 * q4 + 3] * inv);
+        *reinterpret_cast<uint2 *>(os + lq * D + dd) = w;
       }
   }
   __syncthreads();
@@ -294,11 +350,11 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
 #pragma unroll 4
   for (int it = 0; it < kQW * kRowChunks / 64; ++it) {
     const int q = lane + it * 64;
-    const uint32_t ql = (uint32_t)(q / kRowChunks), c = (uint32_t)(q % kRowChunks);
-    const uint32_t qi = q0 + ql;
-    if (qi < a.M)
-      *reinterpret_cast<uint4 *>(O + (size_t)qi * a.ldo + 8u * c) =
-          *reinterpret_cast<const uint4 *>(os + ql * D + 8u * c);
+    const uint32_t ql = (uint32_t)(q / kRowChunks), cc = (uint32_t)(q % kRowChunks);
+    const uint32_t qo = q0 + ql;
+    if (qo < a.M)
+      *reinterpret_cast<uint4 *>(O + (size_t)qo * a.ldo + 8u * cc) =
+          *reinterpret_cast<const uint4 *>(os + ql * D + 8u * cc);
   }
 }
 
@@ -417,11 +473,11 @@ BWPP_ATTN_GENERIC(bwpp_attn_generic_f32_causal, float, true)
 BWPP_ATTN_GENERIC(bwpp_attn_generic_bf16, uint16_t, false)
 BWPP_ATTN_GENERIC(bwpp_attn_generic_bf16_causal, uint16_t, true)
 
-extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1))) void
+extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void
 bwpp_attn_bf16_d128(const BwppAttnArgs a) {
   attn_bf16_d128<false>(a);
 }
-extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1))) void
+extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void
 bwpp_attn_bf16_d128_causal(const BwppAttnArgs a) {
   attn_bf16_d128<true>(a);
 }

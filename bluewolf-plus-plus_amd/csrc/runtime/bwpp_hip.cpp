@@ -16,6 +16,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <cmath>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -679,7 +680,9 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, 
   g.vdim = p.D;
   const int causal = p.causal ? 1 : 0;
   const uint64_t slices = (uint64_t)B * H;
-  const bool flash = bf16 && p.K == 128 && p.D == 128 && p.N > 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
+  // The flash kernel takes the row maximum of the raw scores and scales it
+  // afterwards, which needs a positive scale (finite: NaN / inf go generic).
+  const bool flash = bf16 && p.K == 128 && p.D == 128 && p.N > 0 && scale > 0.0f && scale < INFINITY && aligned16(q) && aligned16(k) && aligned16(v) &&
                      aligned16(o) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0 &&
                      q_bs % 8 == 0 && q_hs % 8 == 0 && k_bs % 8 == 0 && k_hs % 8 == 0 && v_bs % 8 == 0 &&
                      v_hs % 8 == 0 && o_bs % 8 == 0 && o_hs % 8 == 0;
@@ -688,7 +691,7 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, 
     g.q_tiles = (p.M + 255) / 256;
     const uint64_t grid = slices * g.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: grid too large");
-    return launch(h, h->attn_flash[causal], (uint32_t)grid, 1, 1, 256, g);
+    return launch(h, h->attn_flash[causal], (uint32_t)grid, 1, 1, 512, g);
   }
   g.scale_log2 = scale;
   g.q_tiles = (p.M + 15) / 16;

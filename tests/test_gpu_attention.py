@@ -170,3 +170,25 @@ def test_c4_full(be, oracle, causal):
         assert rel_max_err(got[b:b + 1, h:h + 1], want) <= BF16_TOL
     del ref
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("growth", [0.05, -0.05])
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_running_max_moves(be, oracle, growth, causal):
+    """Scores whose row maximum keeps rising (or falling) from tile to tile,
+    so the running offset is raised many times (and the output rescaled)."""
+    B, H, M, N, d = 1, 2, 256, 1024, 128
+    q = synth.normal((B, H, M, d), 11, 0)
+    k = synth.normal((B, H, N, d), 11, 1) * (1.0 + growth * np.arange(N, dtype=np.float32))[None, None, :, None]
+    v = synth.normal((B, H, N, d), 11, 2)
+    (qd, q), (kd, k), (vd, v) = bf16_dev(q), bf16_dev(k.astype(np.float32)), bf16_dev(v)
+    o = run(be, qd, kd, vd, B, H, M, N, d, d, 0.5, causal, bwpp.DType.BF16)
+    assert rel_max_err(host(o), oracle.attention_bh(q, k, v, 0.5, causal)) <= BF16_TOL
+
+
+def test_negative_scale_d128(be, oracle):
+    """A negative scale flips which score is largest; d = 128 bf16 with such
+    a scale runs the generic kernel."""
+    (qd, kd, vd), (q, k, v) = inputs(1, 2, 100, 300, 128, 128, 12, True)
+    o = run(be, qd, kd, vd, 1, 2, 100, 300, 128, 128, -0.1, True, bwpp.DType.BF16)
+    assert rel_max_err(host(o), oracle.attention_bh(q, k, v, -0.1, True)) <= BF16_TOL
