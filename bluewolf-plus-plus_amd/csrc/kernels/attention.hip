@@ -60,12 +60,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // 16 bytes per lane global -> LDS (M0 = destination of lane 0, lane l at
-// +16 l); inline asm keeps the compiler from adding vmcnt(0) before every
+// +16 l), from a wave-uniform 64-bit base in SGPRs plus a 32-bit per-lane
+// byte offset; inline asm keeps the compiler from adding vmcnt(0) before every
 // LDS read (completion is awaited with wait_vmcnt + a barrier).  M0 cannot
 // be declared clobbered (it is reserved); these kernels use M0 for nothing
 // else, which the generated code confirms (only these s_mov_b32 m0 write it).
-__device__ __forceinline__ void g2lds16(const void *gptr, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(gptr)
+__device__ __forceinline__ void g2lds16_so(const void *sbase, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_addr), "v"(voff), "s"(sbase)
                : "memory");
 }
 
@@ -123,6 +124,10 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
     if (qi < a.M) v = *reinterpret_cast<const uint4 *>(Q + (size_t)qi * a.ldq + 16 * ks + 8 * lh);
     qf[ks] = __builtin_bit_cast(bf16x8_t, v);
   }
+  // Let the Q loads land before any DMA is issued: the compiler cannot see
+  // the DMA, and an outstanding Q load at the loop head would make it wait
+  // for vmcnt(0) -- every tile in flight -- on each iteration.
+  wait_vmcnt<0>();
 
   // DMA: each wave loads kBlkPW of the 16 1-KiB blocks of the K tile and of
   // the V tile.  Rows past N re-read row N - 1 (finite data; masked to -inf).
@@ -145,8 +150,10 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
     for (int i = 0; i < kBlkPW; ++i) {
       uint32_t key = t * kBKV + dma_row[i];
       key = key < a.N ? key : a.N - 1;
-      g2lds16(K + (size_t)key * a.ldk + dma_kcol[i], st + (uint32_t)i * 1024u);
-      g2lds16(V + (size_t)key * a.ldv + dma_vcol[i], st + kTile + (uint32_t)i * 1024u);
+      // Byte offsets inside the (batch, head) slice fit 32 bits (the runtime
+      // checks (N - 1) * ld + D < 2^31 before choosing this kernel).
+      g2lds16_so(K, 2u * (key * a.ldk + dma_kcol[i]), st + (uint32_t)i * 1024u);
+      g2lds16_so(V, 2u * (key * a.ldv + dma_vcol[i]), st + kTile + (uint32_t)i * 1024u);
     }
   };
   constexpr int kDmaPerTile = 2 * kBlkPW;

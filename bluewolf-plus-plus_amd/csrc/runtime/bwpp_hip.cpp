@@ -685,7 +685,10 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, 
   const bool flash = bf16 && p.K == 128 && p.D == 128 && p.N > 0 && scale > 0.0f && scale < INFINITY && aligned16(q) && aligned16(k) && aligned16(v) &&
                      aligned16(o) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0 &&
                      q_bs % 8 == 0 && q_hs % 8 == 0 && k_bs % 8 == 0 && k_hs % 8 == 0 && v_bs % 8 == 0 &&
-                     v_hs % 8 == 0 && o_bs % 8 == 0 && o_hs % 8 == 0;
+                     v_hs % 8 == 0 && o_bs % 8 == 0 && o_hs % 8 == 0 &&
+                     // K / V byte offsets inside a slice are 32-bit in the kernel
+                     (uint64_t)(p.N - 1) * ldk + p.K < (1ull << 31) &&
+                     (uint64_t)(p.N - 1) * ldv + p.D < (1ull << 31);
   if (flash) {
     g.scale_log2 = scale * 1.4426950408889634f;
     g.q_tiles = (p.M + 255) / 256;
