@@ -8,7 +8,7 @@
 //
 // Layout of the work: a block of 8 waves (two per SIMD) owns 256 queries of
 // one (batch, head); each wave owns 32 queries.  Keys stream through LDS in
-// tiles of 64 (K and V, 16 KiB each for d = 128) in a 3-stage ring filled
+// tiles of 64 (K and V, 16 KiB each for d = 128) in a 4-stage ring filled
 // by global -> LDS DMA.  Two waves per SIMD let one wave's softmax (VALU)
 // run while the other's MFMAs issue; 32 queries per wave keep the
 // registers (Q^T operands, S^T tile, O^T accumulators) under 256 per wave.
@@ -50,7 +50,7 @@ constexpr int kFW = 8;                  // flash path: waves per block
 constexpr int kQW = 32;                 // queries per wave
 constexpr int kBQ = kFW * kQW;          // queries per block
 constexpr int kBKV = 64;                // keys per tile
-constexpr int kStages = 3;
+constexpr int kStages = 4;
 constexpr float kLazy = 8.0f;
 
 template <int N>
@@ -236,7 +236,11 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+    {
+      // Lanes l and l ^ 32 hold the two halves of one query's keys.
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])) * c;
+    }
     // Raise the offset only past the lazy margin (or from -inf).
     float alpha = 1.0f;
     if (mx > mrow + kLazy) {
@@ -253,7 +257,10 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
         s[kb][r] = p;
         sum += p;
       }
-    sum += __shfl_xor(sum, 32, 64);
+    {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false);
+      sum = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
     lrow = lrow * alpha + sum;
     if (__ballot(alpha != 1.0f)) {
 #pragma unroll
@@ -313,7 +320,10 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
   t_mask = min(t_mask, nkt);
 
   auto step = [&](uint32_t t) {
-    if (t + 1 < nkt) wait_vmcnt<kDmaPerTile>();  // tile t + 1 may still be in flight
+    // Tiles t + 1 .. t + kStages - 2 may still be in flight.
+    const uint32_t younger = min(nkt - 1 - t, (uint32_t)(kStages - 2));
+    if (younger >= 2) wait_vmcnt<2 * kDmaPerTile>();
+    else if (younger == 1) wait_vmcnt<kDmaPerTile>();
     else wait_vmcnt<0>();
     __syncthreads();
     if (t + kStages - 1 < nkt) issue(t + kStages - 1);
