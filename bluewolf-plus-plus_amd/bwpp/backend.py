@@ -104,6 +104,15 @@ class HipBackend:
         self._check(self.lib.bwpp_hip_dispatch_attention(
             self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(o), params))
 
+    def dispatch_attention_lse(self, q, k, v, o, lse, params: AttentionParams):
+        self._check(self.lib.bwpp_hip_dispatch_attention_lse(
+            self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), params))
+
+    def dispatch_attention_grad(self, q, k, v, o, dout, lse, dq, dk, dv, params: AttentionParams):
+        self._check(self.lib.bwpp_hip_dispatch_attention_grad(
+            self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(dout), _ptr(lse),
+            _ptr(dq), _ptr(dk), _ptr(dv), params))
+
     def dispatch_reduce_max(self, x, maxv, argmax, params: ReduceParams):
         self._check(self.lib.bwpp_hip_dispatch_reduce_max(
             self._h, _ptr(x), _ptr(maxv), _ptr(argmax), params))

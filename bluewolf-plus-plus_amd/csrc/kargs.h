@@ -60,6 +60,15 @@ typedef struct {
   uint32_t causal;
   uint32_t kdim; /* Q/K head dim (generic path) */
   uint32_t vdim; /* V/O head dim (generic path) */
+  /* Forward: optional per-query log-sum-exp out ([B*H][M] fp32).
+   * Backward: lse in, dout (O's strides), dq / dk / dv (Q / K / V strides),
+   * dsum = rowsum(dout * o) scratch ([B*H][M] fp32). */
+  float *lse;
+  const void *dout;
+  void *dq;
+  void *dk;
+  void *dv;
+  float *dsum;
 } BwppAttnArgs;
 
 /* Grad ops and elementwise glue (grad.hip). */

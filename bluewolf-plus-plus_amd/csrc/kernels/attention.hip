@@ -474,11 +474,195 @@ __device__ __forceinline__ void attn_generic(const BwppAttnArgs &a) {
       const uint32_t d = (uint32_t)lane + 64u * j;
       if (d < Dv) st_elem(O + (size_t)qi * a.ldo + d, o[j] * inv);
     }
+    if (a.lse && lane == 0) a.lse[(size_t)bh * a.M + qi] = l > 0.0f ? m + logf(l) : -INFINITY;
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// ------------------------------------------------------- backward (generic)
+// O = softmax(scale Q K^T [mask]) V.  With the saved lse (natural-log
+// log-sum-exp per query) the probabilities are recomputed as
+// p = exp(scale q.k - lse) and, with D_m = rowsum(dO * O)[m],
+//   dS = p (dO.v - D_m),  dQ = scale dS K,  dK = scale dS^T Q,  dV = P^T dO.
+// Two passes, both one wave per row with fp32 arithmetic and any head dims
+// up to 512: attn_bwd_dq (one query per wave; also writes D_m) and then
+// attn_bwd_dkdv (one key per wave, looping over the queries that see it).
+
+template <class T, bool CAUSAL>
+__device__ __forceinline__ void attn_bwd_dq(const BwppAttnArgs &a) {
+  const uint32_t Kd = a.kdim, Dv = a.vdim;
+  __shared__ float qs[kWaves][kGenMaxDim];
+  __shared__ float gs[kWaves][kGenMaxDim];
+  __shared__ float ps[kWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t nbh = gridDim.x / a.q_tiles;
+  const uint32_t qt = a.q_tiles - 1 - blockIdx.x / nbh;
+  const uint32_t bh = blockIdx.x % nbh;
+  const uint32_t b = bh / a.heads, h = bh % a.heads;
+  const T *Q = static_cast<const T *>(a.q) + b * a.q_bs + h * a.q_hs;
+  const T *K = static_cast<const T *>(a.k) + b * a.k_bs + h * a.k_hs;
+  const T *V = static_cast<const T *>(a.v) + b * a.v_bs + h * a.v_hs;
+  const T *O = static_cast<const T *>(a.o) + b * a.o_bs + h * a.o_hs;
+  const T *dO = static_cast<const T *>(a.dout) + b * a.o_bs + h * a.o_hs;
+  T *dQ = static_cast<T *>(a.dq) + b * a.q_bs + h * a.q_hs;
+  const int64_t diag = (int64_t)a.N - (int64_t)a.M;
+  const float scale = a.scale_log2;  // the plain scale on this path
+  constexpr int DPL = kGenMaxDim / 64;
+
+  for (uint32_t qq = (uint32_t)wave; qq < kGenQ; qq += kWaves) {
+    const uint32_t qi = qt * kGenQ + qq;
+    if (qi >= a.M) break;  // wave-uniform
+    for (uint32_t k = (uint32_t)lane; k < Kd; k += 64) qs[wave][k] = ld_elem(Q + (size_t)qi * a.ldq + k);
+    float dsum = 0.0f;
+    for (uint32_t d = (uint32_t)lane; d < Dv; d += 64) {
+      const float g = ld_elem(dO + (size_t)qi * a.ldo + d);
+      gs[wave][d] = g;
+      dsum += g * ld_elem(O + (size_t)qi * a.ldo + d);
+    }
+    dsum = wave_sum(dsum);
+    if (lane == 0) a.dsum[(size_t)bh * a.M + qi] = dsum;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float lse = a.lse[(size_t)bh * a.M + qi];
+    int64_t lim = CAUSAL ? (int64_t)qi + diag + 1 : (int64_t)a.N;
+    lim = lim < 0 ? 0 : (lim > (int64_t)a.N ? (int64_t)a.N : lim);
+    const uint32_t kend = (uint32_t)lim;
+    float acc[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] = 0.0f;
+    for (uint32_t n0 = 0; n0 < kend; n0 += 64) {
+      const uint32_t n = n0 + (uint32_t)lane;
+      float ds = 0.0f;
+      if (n < kend) {
+        const T *kr = K + (size_t)n * a.ldk;
+        const T *vr = V + (size_t)n * a.ldv;
+        float s = 0.0f, dp = 0.0f;
+        for (uint32_t k = 0; k < Kd; ++k) s += qs[wave][k] * ld_elem(kr + k);
+        for (uint32_t d = 0; d < Dv; ++d) dp += gs[wave][d] * ld_elem(vr + d);
+        const float p = expf(s * scale - lse);
+        ds = p * (dp - dsum);
+      }
+      __builtin_amdgcn_wave_barrier();
+      ps[wave][lane] = ds;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint32_t cnt = min(64u, kend - n0);
+      for (uint32_t t = 0; t < cnt; ++t) {
+        const float dsn = ps[wave][t];
+        const T *kr = K + (size_t)(n0 + t) * a.ldk;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          const uint32_t k = (uint32_t)lane + 64u * j;
+          if (k < Kd) acc[j] += dsn * ld_elem(kr + k);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const uint32_t k = (uint32_t)lane + 64u * j;
+      if (k < Kd) st_elem(dQ + (size_t)qi * a.ldq + k, acc[j] * scale);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+template <class T, bool CAUSAL>
+__device__ __forceinline__ void attn_bwd_dkdv(const BwppAttnArgs &a) {
+  const uint32_t Kd = a.kdim, Dv = a.vdim;
+  __shared__ float ks[kWaves][kGenMaxDim];
+  __shared__ float vs[kWaves][kGenMaxDim];
+  __shared__ float pp[kWaves][64];
+  __shared__ float dd[kWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t nbh = gridDim.x / a.q_tiles;  // q_tiles holds the key tiles here
+  const uint32_t kt = a.q_tiles - 1 - blockIdx.x / nbh;
+  const uint32_t bh = blockIdx.x % nbh;
+  const uint32_t b = bh / a.heads, h = bh % a.heads;
+  const T *Q = static_cast<const T *>(a.q) + b * a.q_bs + h * a.q_hs;
+  const T *K = static_cast<const T *>(a.k) + b * a.k_bs + h * a.k_hs;
+  const T *V = static_cast<const T *>(a.v) + b * a.v_bs + h * a.v_hs;
+  const T *dO = static_cast<const T *>(a.dout) + b * a.o_bs + h * a.o_hs;
+  T *dK = static_cast<T *>(a.dk) + b * a.k_bs + h * a.k_hs;
+  T *dV = static_cast<T *>(a.dv) + b * a.v_bs + h * a.v_hs;
+  const float *lse = a.lse + (size_t)bh * a.M;
+  const float *dsum = a.dsum + (size_t)bh * a.M;
+  const int64_t diag = (int64_t)a.N - (int64_t)a.M;
+  const float scale = a.scale_log2;
+  constexpr int DPL = kGenMaxDim / 64;
+
+  for (uint32_t kk = (uint32_t)wave; kk < kGenQ; kk += kWaves) {
+    const uint32_t n = kt * kGenQ + kk;
+    if (n >= a.N) break;  // wave-uniform
+    for (uint32_t k = (uint32_t)lane; k < Kd; k += 64) ks[wave][k] = ld_elem(K + (size_t)n * a.ldk + k);
+    for (uint32_t d = (uint32_t)lane; d < Dv; d += 64) vs[wave][d] = ld_elem(V + (size_t)n * a.ldv + d);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // Queries that see key n: m >= n - diag (causal), all otherwise.
+    int64_t first = CAUSAL ? (int64_t)n - diag : 0;
+    first = first < 0 ? 0 : first;
+    const uint32_t mbeg = first > (int64_t)a.M ? a.M : (uint32_t)first;
+    float gk[DPL], gv[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) gk[j] = gv[j] = 0.0f;
+    for (uint32_t m0 = mbeg; m0 < a.M; m0 += 64) {
+      const uint32_t m = m0 + (uint32_t)lane;
+      float p = 0.0f, ds = 0.0f;
+      if (m < a.M) {
+        const T *qr = Q + (size_t)m * a.ldq;
+        const T *gr = dO + (size_t)m * a.ldo;
+        float s = 0.0f, dp = 0.0f;
+        for (uint32_t k = 0; k < Kd; ++k) s += ld_elem(qr + k) * ks[wave][k];
+        for (uint32_t d = 0; d < Dv; ++d) dp += ld_elem(gr + d) * vs[wave][d];
+        p = expf(s * scale - lse[m]);
+        ds = p * (dp - dsum[m]);
+      }
+      __builtin_amdgcn_wave_barrier();
+      pp[wave][lane] = p;
+      dd[wave][lane] = ds;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint32_t cnt = min(64u, a.M - m0);
+      for (uint32_t t = 0; t < cnt; ++t) {
+        const float pm = pp[wave][t], dm = dd[wave][t];
+        const T *qr = Q + (size_t)(m0 + t) * a.ldq;
+        const T *gr = dO + (size_t)(m0 + t) * a.ldo;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          const uint32_t c = (uint32_t)lane + 64u * j;
+          if (c < Kd) gk[j] += dm * ld_elem(qr + c);
+          if (c < Dv) gv[j] += pm * ld_elem(gr + c);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const uint32_t c = (uint32_t)lane + 64u * j;
+      if (c < Kd) st_elem(dK + (size_t)n * a.ldk + c, gk[j] * scale);
+      if (c < Dv) st_elem(dV + (size_t)n * a.ldv + c, gv[j]);
+    }
     __builtin_amdgcn_wave_barrier();
   }
 }
 
 }  // namespace
+
+#define BWPP_ATTN_BWD(NAME, T, CAUSAL)                                                      \
+  extern "C" __global__ __launch_bounds__(256) void NAME##_dq(const BwppAttnArgs a) {       \
+    attn_bwd_dq<T, CAUSAL>(a);                                                             \
+  }                                                                                        \
+  extern "C" __global__ __launch_bounds__(256) void NAME##_dkdv(const BwppAttnArgs a) {     \
+    attn_bwd_dkdv<T, CAUSAL>(a);                                                           \
+  }
+BWPP_ATTN_BWD(bwpp_attn_bwd_f32, float, false)
+BWPP_ATTN_BWD(bwpp_attn_bwd_f32_causal, float, true)
+BWPP_ATTN_BWD(bwpp_attn_bwd_bf16, uint16_t, false)
+BWPP_ATTN_BWD(bwpp_attn_bwd_bf16_causal, uint16_t, true)
 
 // Generic path entry points, one per storage type x mask.
 #define BWPP_ATTN_GENERIC(NAME, T, CAUSAL)                                                  \

@@ -75,6 +75,8 @@ struct BwppHip {
   hipFunction_t gemm_bf16_w8[2][2] = {};  // 8-wave full-tile bf16: [ta][tb]
   hipFunction_t attn_flash[2] = {};       // bf16, d = 128: [causal]
   hipFunction_t attn_generic[2][2] = {};  // [bf16][causal]
+  hipFunction_t attn_bwd_dq[2][2] = {};   // [bf16][causal]
+  hipFunction_t attn_bwd_dkdv[2][2] = {};
   hipFunction_t silu_grad = nullptr, softmax_grad = nullptr, rmsnorm_grad = nullptr, col_partials_sum = nullptr,
                 reduce_sum_rows = nullptr, reduce_sum_cols = nullptr, elementwise = nullptr;
   // Library-owned device workspace (column partials), grown on demand and
@@ -163,6 +165,11 @@ BwppHipStatus resolve_all(BwppHip *h) {
       return s;
     if ((s = resolve(h, std::string("bwpp_attn_generic_bf16") + cs, &h->attn_generic[1][causal])) != BWPP_HIP_OK)
       return s;
+    for (int bf = 0; bf < 2; ++bf) {
+      const std::string base = std::string("bwpp_attn_bwd_") + (bf ? "bf16" : "f32") + cs;
+      if ((s = resolve(h, base + "_dq", &h->attn_bwd_dq[bf][causal])) != BWPP_HIP_OK) return s;
+      if ((s = resolve(h, base + "_dkdv", &h->attn_bwd_dkdv[bf][causal])) != BWPP_HIP_OK) return s;
+    }
   }
   return BWPP_HIP_OK;
 }
@@ -619,10 +626,17 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
   return launch(h, h->gemm[bf16 ? 1 : 0][ta][tb][full ? 1 : 0], (uint32_t)tiles, 1, 1, 256, g);
 }
 
-extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, const void *k, const void *v,
-                                                     void *o, BwppAttentionParams p) {
-  BwppHipStatus s = enter(h);
-  if (s != BWPP_HIP_OK) return s;
+namespace {
+
+BwppHipStatus ensure_ws(BwppHip *h, size_t bytes);
+
+// Validation, default strides and the kernel argument block shared by the
+// attention entry points.  `out` is O for the forward (checked against
+// Q, K, V for overlap); the backward checks its outputs itself.
+BwppHipStatus attn_prepare(BwppHip *h, const void *q, const void *k, const void *v, const void *o,
+                           const BwppAttentionParams &p, BwppAttnArgs &g, uint64_t &slices, bool &skip,
+                           bool forward = true) {
+  skip = false;
   if (!q || !k || !v || !o) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "attention: NULL q, k, v or o");
   if (p.dtype > BWPP_HIP_BF16) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "attention: unknown dtype %u", p.dtype);
   const uint32_t B = p.batch ? p.batch : 1, H = p.heads ? p.heads : 1;
@@ -630,11 +644,13 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, 
   const uint32_t ldv = p.ldv ? p.ldv : p.D, ldo = p.ldo ? p.ldo : p.D;
   if (ldq < p.K || ldk < p.K || ldv < p.D || ldo < p.D)
     return fail(h, BWPP_HIP_ERR_INVALID_ARG, "attention: leading dimension smaller than the row");
-  if (p.M == 0 || p.D == 0) return BWPP_HIP_OK;
+  if (forward && (p.M == 0 || p.D == 0)) {
+    skip = true;
+    return BWPP_HIP_OK;
+  }
   if (p.K == 0 || p.K > 512 || p.D > 512)
     return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: head dims K=%u D=%u outside 1..512", p.K, p.D);
-  const bool bf16 = p.dtype == BWPP_HIP_BF16;
-  const uint64_t es = bf16 ? 2 : 4;
+  const uint64_t es = p.dtype == BWPP_HIP_BF16 ? 2 : 4;
   // Default slice strides: [B, H, rows, ld] contiguous.
   auto def = [](uint64_t st, uint64_t dflt) { return st ? st : dflt; };
   const uint64_t q_hs = def(p.q_head_stride, (uint64_t)p.M * ldq), q_bs = def(p.q_batch_stride, q_hs * H);
@@ -653,13 +669,11 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, 
   if (overlaps(eo, hull(q, q_bs, q_hs, p.M, p.K, ldq)) || overlaps(eo, hull(k, k_bs, k_hs, p.N, p.K, ldk)) ||
       overlaps(eo, hull(v, v_bs, v_hs, p.N, p.D, ldv)))
     return fail(h, BWPP_HIP_ERR_ALIAS, "attention: O overlaps Q, K or V");
-
-  const float scale = p.scale != 0.0f ? p.scale : 1.0f;
-  BwppAttnArgs g = {};
+  g = BwppAttnArgs{};
   g.q = q;
   g.k = k;
   g.v = v;
-  g.o = o;
+  g.o = const_cast<void *>(o);
   g.M = p.M;
   g.N = p.N;
   g.ldq = ldq;
@@ -678,17 +692,32 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, 
   g.causal = p.causal ? 1u : 0u;
   g.kdim = p.K;
   g.vdim = p.D;
+  slices = (uint64_t)B * H;
+  return BWPP_HIP_OK;
+}
+
+BwppHipStatus attn_forward(BwppHip *h, const void *q, const void *k, const void *v, void *o, float *lse,
+                           const BwppAttentionParams &p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  BwppAttnArgs g;
+  uint64_t slices = 0;
+  bool skip = false;
+  if ((s = attn_prepare(h, q, k, v, o, p, g, slices, skip)) != BWPP_HIP_OK || skip) return s;
+  const float scale = p.scale != 0.0f ? p.scale : 1.0f;
   const int causal = p.causal ? 1 : 0;
-  const uint64_t slices = (uint64_t)B * H;
+  const bool bf16 = p.dtype == BWPP_HIP_BF16;
   // The flash kernel takes the row maximum of the raw scores and scales it
-  // afterwards, which needs a positive scale (finite: NaN / inf go generic).
-  const bool flash = bf16 && p.K == 128 && p.D == 128 && p.N > 0 && scale > 0.0f && scale < INFINITY && aligned16(q) && aligned16(k) && aligned16(v) &&
-                     aligned16(o) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0 &&
-                     q_bs % 8 == 0 && q_hs % 8 == 0 && k_bs % 8 == 0 && k_hs % 8 == 0 && v_bs % 8 == 0 &&
-                     v_hs % 8 == 0 && o_bs % 8 == 0 && o_hs % 8 == 0 &&
+  // afterwards, which needs a positive scale (finite: NaN / inf go generic);
+  // it does not write the log-sum-exp.
+  const bool flash = !lse && bf16 && p.K == 128 && p.D == 128 && p.N > 0 && scale > 0.0f && scale < INFINITY &&
+                     aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) && g.ldq % 8 == 0 &&
+                     g.ldk % 8 == 0 && g.ldv % 8 == 0 && g.ldo % 8 == 0 && g.q_bs % 8 == 0 && g.q_hs % 8 == 0 &&
+                     g.k_bs % 8 == 0 && g.k_hs % 8 == 0 && g.v_bs % 8 == 0 && g.v_hs % 8 == 0 &&
+                     g.o_bs % 8 == 0 && g.o_hs % 8 == 0 &&
                      // K / V byte offsets inside a slice are 32-bit in the kernel
-                     (uint64_t)(p.N - 1) * ldk + p.K < (1ull << 31) &&
-                     (uint64_t)(p.N - 1) * ldv + p.D < (1ull << 31);
+                     (uint64_t)(p.N - 1) * g.ldk + p.K < (1ull << 31) &&
+                     (uint64_t)(p.N - 1) * g.ldv + p.D < (1ull << 31);
   if (flash) {
     g.scale_log2 = scale * 1.4426950408889634f;
     g.q_tiles = (p.M + 255) / 256;
@@ -697,10 +726,80 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, 
     return launch(h, h->attn_flash[causal], (uint32_t)grid, 1, 1, 512, g);
   }
   g.scale_log2 = scale;
+  g.lse = lse;
   g.q_tiles = (p.M + 15) / 16;
   const uint64_t grid = slices * g.q_tiles;
   if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: grid too large");
   return launch(h, h->attn_generic[bf16 ? 1 : 0][causal], (uint32_t)grid, 1, 1, 256, g);
+}
+
+}  // namespace
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q, const void *k, const void *v,
+                                                     void *o, BwppAttentionParams p) {
+  return attn_forward(h, q, k, v, o, nullptr, p);
+}
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_attention_lse(BwppHip *h, const void *q, const void *k, const void *v,
+                                                         void *o, float *lse, BwppAttentionParams p) {
+  if (!lse && h) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "attention_lse: NULL lse");
+  return attn_forward(h, q, k, v, o, lse, p);
+}
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_attention_grad(BwppHip *h, const void *q, const void *k, const void *v,
+                                                          const void *o, const void *dout, const float *lse,
+                                                          void *dq, void *dk, void *dv, BwppAttentionParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!dout || !lse || !dq || !dk || !dv)
+    return fail(h, BWPP_HIP_ERR_INVALID_ARG, "attention_grad: NULL dout, lse, dq, dk or dv");
+  BwppAttnArgs g;
+  uint64_t slices = 0;
+  bool skip = false;
+  if ((s = attn_prepare(h, q, k, v, o, p, g, slices, skip, false)) != BWPP_HIP_OK) return s;
+  if (p.M == 0 && p.N == 0) return BWPP_HIP_OK;
+  const uint32_t B = p.batch ? p.batch : 1, H = p.heads ? p.heads : 1;
+  const uint64_t es = p.dtype == BWPP_HIP_BF16 ? 2 : 4;
+  auto hull = [&](const void *ptr, uint64_t bs, uint64_t hs, uint64_t rows, uint64_t cols, uint64_t ld) {
+    Extent e;
+    if (rows == 0 || cols == 0) return e;
+    e.lo = (uintptr_t)ptr;
+    e.hi = e.lo + ((uint64_t)(B - 1) * bs + (uint64_t)(H - 1) * hs + (rows - 1) * ld + cols) * es;
+    return e;
+  };
+  const Extent eq = hull(q, g.q_bs, g.q_hs, p.M, p.K, g.ldq), ek = hull(k, g.k_bs, g.k_hs, p.N, p.K, g.ldk);
+  const Extent ev = hull(v, g.v_bs, g.v_hs, p.N, p.D, g.ldv), eo = hull(o, g.o_bs, g.o_hs, p.M, p.D, g.ldo);
+  const Extent edo = hull(dout, g.o_bs, g.o_hs, p.M, p.D, g.ldo);
+  const Extent edq = hull(dq, g.q_bs, g.q_hs, p.M, p.K, g.ldq), edk = hull(dk, g.k_bs, g.k_hs, p.N, p.K, g.ldk);
+  const Extent edv = hull(dv, g.v_bs, g.v_hs, p.N, p.D, g.ldv);
+  const Extent else_{(uintptr_t)lse, (uintptr_t)lse + slices * p.M * 4};
+  for (const Extent &out : {edq, edk, edv})
+    for (const Extent &in : {eq, ek, ev, eo, edo, else_})
+      if (overlaps(out, in)) return fail(h, BWPP_HIP_ERR_ALIAS, "attention_grad: an output overlaps an input");
+  if (overlaps(edq, edk) || overlaps(edq, edv) || overlaps(edk, edv))
+    return fail(h, BWPP_HIP_ERR_ALIAS, "attention_grad: dq, dk and dv overlap");
+  if ((s = ensure_ws(h, (size_t)slices * p.M * sizeof(float) + 4)) != BWPP_HIP_OK) return s;
+  const int bf = p.dtype == BWPP_HIP_BF16 ? 1 : 0, causal = p.causal ? 1 : 0;
+  g.scale_log2 = p.scale != 0.0f ? p.scale : 1.0f;
+  g.lse = const_cast<float *>(lse);
+  g.dout = dout;
+  g.dq = dq;
+  g.dk = dk;
+  g.dv = dv;
+  g.dsum = static_cast<float *>(h->ws);
+  if (p.M > 0) {
+    g.q_tiles = (p.M + 15) / 16;
+    const uint64_t grid = slices * g.q_tiles;
+    if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
+    if ((s = launch(h, h->attn_bwd_dq[bf][causal], (uint32_t)grid, 1, 1, 256, g)) != BWPP_HIP_OK) return s;
+  }
+  if (p.N > 0) {
+    g.q_tiles = (p.N + 15) / 16;  // key tiles
+    const uint64_t grid = slices * g.q_tiles;
+    if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
+    if ((s = launch(h, h->attn_bwd_dkdv[bf][causal], (uint32_t)grid, 1, 1, 256, g)) != BWPP_HIP_OK) return s;
+  }
+  return BWPP_HIP_OK;
 }
 
 // ------------------------------------------------------------- grad ops

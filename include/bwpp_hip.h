@@ -243,6 +243,29 @@ BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q,
                                           const void *k, const void *v,
                                           void *o, BwppAttentionParams params);
 
+/* Forward attention that also writes lse[(b*H + h)*M + m], the natural-log
+ * log-sum-exp of query m's scaled, masked scores (-inf when it sees no key),
+ * for the backward below.  No reference counterpart (the reference
+ * differentiates attention through its decomposed graph ops,
+ * graph_ir.c:1722-1733, 1529-1583); runs the generic kernel. */
+BwppHipStatus bwpp_hip_dispatch_attention_lse(BwppHip *h, const void *q,
+                                              const void *k, const void *v,
+                                              void *o, float *lse,
+                                              BwppAttentionParams params);
+
+/* Attention backward: dq, dk, dv of O = softmax(scale Q K^T [causal]) V
+ * for the upstream gradient dout, from q, k, v, o and the forward's lse.
+ * dout / dq / dk / dv use the strides of o / q / k / v.  Outputs must not
+ * overlap inputs or each other.  Uses the handle's workspace for
+ * rowsum(dout * o).  Replaces the decomposed path of graph_ir.c:1722-1733
+ * (softmax_grad over materialised probabilities). */
+BwppHipStatus bwpp_hip_dispatch_attention_grad(BwppHip *h, const void *q,
+                                               const void *k, const void *v,
+                                               const void *o, const void *dout,
+                                               const float *lse, void *dq,
+                                               void *dk, void *dv,
+                                               BwppAttentionParams params);
+
 /* reduce_max forward (graph op BWPP_GOP_REDUCE_MAX, graph_ir.h:48; no
  * reference kernel): maxv as the reference's fold, argmax = lowest index
  * holding it (-1 if none).  Either output may be NULL, not both. */

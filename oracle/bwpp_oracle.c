@@ -216,6 +216,103 @@ int oracle_attention_bh_f32(const float *q, const float *k, const float *v,
   return 0;
 }
 
+/* Log-sum-exp of each query's scaled, masked scores (natural log):
+ * lse[m] = max + logf(sum_n expf(s_n - max)), -INFINITY when no key is
+ * visible.  Contiguous [B,H,M,K] / [B,H,N,K] layouts.  Extension (no
+ * reference counterpart): the saved statistic of the attention backward. */
+int oracle_attention_lse_f32(const float *q, const float *k, float *lse,
+                             uint32_t B, uint32_t H, uint32_t M, uint32_t N,
+                             uint32_t K, float scale, int causal) {
+  if (!q || !k || !lse) return -1;
+  float *s = (float *)malloc(sizeof(float) * ((size_t)N + 1));
+  if (!s) return -1;
+  for (uint32_t bh = 0; bh < B * H; ++bh) {
+    const float *qs = q + (size_t)bh * M * K, *ks = k + (size_t)bh * N * K;
+    for (uint32_t m = 0; m < M; ++m) {
+      int64_t last = causal ? (int64_t)m + (int64_t)N - (int64_t)M : (int64_t)N - 1;
+      if (last > (int64_t)N - 1) last = (int64_t)N - 1;
+      uint32_t nvis = last < 0 ? 0u : (uint32_t)(last + 1);
+      float maxv = -INFINITY;
+      for (uint32_t n = 0; n < nvis; ++n) {
+        float acc = 0.0f;
+        for (uint32_t kk = 0; kk < K; ++kk) acc += qs[(size_t)m * K + kk] * ks[(size_t)n * K + kk];
+        s[n] = acc * scale;
+        if (s[n] > maxv) maxv = s[n];
+      }
+      float sum = 0.0f;
+      for (uint32_t n = 0; n < nvis; ++n) sum += expf(s[n] - maxv);
+      lse[(size_t)bh * M + m] = nvis ? maxv + logf(sum) : -INFINITY;
+    }
+  }
+  free(s);
+  return 0;
+}
+
+/* Attention backward for O = softmax(scale Q K^T [causal]) V, closed form
+ * per (b, h) slice with P the softmax probabilities (masked keys 0):
+ *   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - rowsum(dP * P)),
+ *   dQ = scale dS K,  dK = scale dS^T Q.
+ * Contiguous [B,H,M,K] q / dq, [B,H,N,K] k / dk, [B,H,N,D] v / dv,
+ * [B,H,M,D] dout.  fp32, loops in index order.  Extension: the reference
+ * differentiates attention only through its decomposed graph ops
+ * (graph_ir.c:1722-1733, 1529-1583). */
+int oracle_attention_grad_f32(const float *q, const float *k, const float *v,
+                              const float *dout, float *dq, float *dk, float *dv,
+                              uint32_t B, uint32_t H, uint32_t M, uint32_t N,
+                              uint32_t K, uint32_t D, float scale, int causal) {
+  if (!q || !k || !v || !dout || !dq || !dk || !dv) return -1;
+  float *p = (float *)malloc(sizeof(float) * ((size_t)N + 1));
+  float *ds = (float *)malloc(sizeof(float) * ((size_t)N + 1));
+  if (!p || !ds) {
+    free(p);
+    free(ds);
+    return -1;
+  }
+  for (uint32_t bh = 0; bh < B * H; ++bh) {
+    const float *qs = q + (size_t)bh * M * K, *ks = k + (size_t)bh * N * K;
+    const float *vs = v + (size_t)bh * N * D, *dos = dout + (size_t)bh * M * D;
+    float *dqs = dq + (size_t)bh * M * K, *dks = dk + (size_t)bh * N * K, *dvs = dv + (size_t)bh * N * D;
+    for (size_t i = 0; i < (size_t)N * K; ++i) dks[i] = 0.0f;
+    for (size_t i = 0; i < (size_t)N * D; ++i) dvs[i] = 0.0f;
+    for (uint32_t m = 0; m < M; ++m) {
+      int64_t last = causal ? (int64_t)m + (int64_t)N - (int64_t)M : (int64_t)N - 1;
+      if (last > (int64_t)N - 1) last = (int64_t)N - 1;
+      uint32_t nvis = last < 0 ? 0u : (uint32_t)(last + 1);
+      const float *qm = qs + (size_t)m * K, *dom = dos + (size_t)m * D;
+      float maxv = -INFINITY;
+      for (uint32_t n = 0; n < nvis; ++n) {
+        float acc = 0.0f;
+        for (uint32_t kk = 0; kk < K; ++kk) acc += qm[kk] * ks[(size_t)n * K + kk];
+        p[n] = acc * scale;
+        if (p[n] > maxv) maxv = p[n];
+      }
+      float sum = 0.0f;
+      for (uint32_t n = 0; n < nvis; ++n) sum += expf(p[n] - maxv);
+      float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+      float rowdot = 0.0f; /* rowsum(dP * P) */
+      for (uint32_t n = 0; n < nvis; ++n) {
+        p[n] = expf(p[n] - maxv) * inv;
+        float dp = 0.0f;
+        for (uint32_t d = 0; d < D; ++d) dp += dom[d] * vs[(size_t)n * D + d];
+        ds[n] = dp;
+        rowdot += dp * p[n];
+      }
+      for (uint32_t kk = 0; kk < K; ++kk) dqs[(size_t)m * K + kk] = 0.0f;
+      for (uint32_t n = 0; n < nvis; ++n) {
+        const float dsn = p[n] * (ds[n] - rowdot);
+        for (uint32_t kk = 0; kk < K; ++kk) {
+          dqs[(size_t)m * K + kk] += scale * dsn * ks[(size_t)n * K + kk];
+          dks[(size_t)n * K + kk] += scale * dsn * qm[kk];
+        }
+        for (uint32_t d = 0; d < D; ++d) dvs[(size_t)n * D + d] += p[n] * dom[d];
+      }
+    }
+  }
+  free(p);
+  free(ds);
+  return 0;
+}
+
 /* bwpp_cpu_ref.c:146-190 */
 int oracle_reduce_max_mask_f32(const float *x, float *mask, uint32_t rows,
                                uint32_t cols, int axis) {

@@ -103,6 +103,19 @@ int oracle_attention_bh_f32(const float *q, const float *k, const float *v,
                             uint64_t o_bs, uint64_t o_hs, float scale,
                             int causal);
 
+/* Per-query log-sum-exp of the scaled, masked scores (natural log; -INF
+ * for a query with no visible key).  Contiguous layouts. */
+int oracle_attention_lse_f32(const float *q, const float *k, float *lse,
+                             uint32_t B, uint32_t H, uint32_t M, uint32_t N,
+                             uint32_t K, float scale, int causal);
+
+/* Attention backward (closed form, see the .c): dq, dk, dv from q, k, v
+ * and the upstream gradient dout.  Contiguous layouts. */
+int oracle_attention_grad_f32(const float *q, const float *k, const float *v,
+                              const float *dout, float *dq, float *dk, float *dv,
+                              uint32_t B, uint32_t H, uint32_t M, uint32_t N,
+                              uint32_t K, uint32_t D, float scale, int causal);
+
 /* reduce_max forward.  axis 1: one value per row; axis 0: one per column.
  * maxv follows the reference's fold (start at -INF, take strictly greater,
  * bwpp_cpu_ref.c:159-165); argmax is the lowest index whose value equals

@@ -33,6 +33,9 @@ _ORACLE_SIGS = {
     "oracle_rmsnorm_f32": [_P, _P, _P, _P, _U, _U, _U, c_float],
     "oracle_layernorm_f32": [_P, _P, _P, _P, _U, _U, _U, c_float],
     "oracle_attention_f32": [_P, _P, _P, _P, _U, _U, _U, _U, _U, _U, _U, _U],
+    "oracle_attention_lse_f32": [_P, _P, _P, _U, _U, _U, _U, _U, ctypes.c_float, ctypes.c_int],
+    "oracle_attention_grad_f32": [_P, _P, _P, _P, _P, _P, _P, _U, _U, _U, _U, _U, _U, ctypes.c_float,
+                                  ctypes.c_int],
     "oracle_attention_bh_f32": [_P, _P, _P, _P, _U, _U, _U, _U, _U, _U, _U, _U, _U, _U,
                                 c_uint64, c_uint64, c_uint64, c_uint64, c_uint64, c_uint64,
                                 c_uint64, c_uint64, c_float, c_int],
@@ -160,6 +163,25 @@ class Oracle:
             scale, int(causal))
         assert rc == 0
         return o
+
+    def attention_lse(self, q, k, scale=1.0, causal=False):
+        """Per-query natural-log LSE of the scaled scores, [B,H,M]."""
+        q, k = (np.ascontiguousarray(t, dtype=np.float32) for t in (q, k))
+        B, H, M, K = q.shape
+        N = k.shape[2]
+        lse = np.zeros((B, H, M), dtype=np.float32)
+        assert self.lib.oracle_attention_lse_f32(_p(q), _p(k), _p(lse), B, H, M, N, K, scale, int(causal)) == 0
+        return lse
+
+    def attention_grad(self, q, k, v, dout, scale=1.0, causal=False):
+        """(dq, dk, dv) of attention_bh for upstream gradient dout."""
+        q, k, v, dout = (np.ascontiguousarray(t, dtype=np.float32) for t in (q, k, v, dout))
+        B, H, M, K = q.shape
+        N, D = v.shape[2], v.shape[3]
+        dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+        assert self.lib.oracle_attention_grad_f32(_p(q), _p(k), _p(v), _p(dout), _p(dq), _p(dk), _p(dv),
+                                                  B, H, M, N, K, D, scale, int(causal)) == 0
+        return dq, dk, dv
 
     def reduce_max_mask(self, x, axis=1):
         x = np.ascontiguousarray(x, dtype=np.float32)

@@ -192,3 +192,52 @@ def test_negative_scale_d128(be, oracle):
     (qd, kd, vd), (q, k, v) = inputs(1, 2, 100, 300, 128, 128, 12, True)
     o = run(be, qd, kd, vd, 1, 2, 100, 300, 128, 128, -0.1, True, bwpp.DType.BF16)
     assert rel_max_err(host(o), oracle.attention_bh(q, k, v, -0.1, True)) <= BF16_TOL
+
+
+# ------------------------------------------------------------- backward
+@pytest.mark.parametrize("B,H,M,N,K,D", [(1, 1, 1, 1, 1, 1), (2, 3, 37, 37, 16, 24), (1, 2, 70, 130, 64, 64),
+                                         (1, 1, 130, 70, 32, 8), (1, 2, 100, 100, 128, 128)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_attention_grad(be, oracle, B, H, M, N, K, D, causal, bf16):
+    """lse forward + backward vs the oracle's closed form (pinned by finite
+    differences); fp32 bar 1e-4, bf16 storage 2e-2."""
+    torch = _torch()
+    (qd, kd, vd), (q, k, v) = inputs(B, H, M, N, K, D, M * 7 + N, bf16)
+    dout = synth.normal((B, H, M, D), M + N, 3)
+    dt = bwpp.DType.BF16 if bf16 else bwpp.DType.F32
+    if bf16:
+        dod, dout = bf16_dev(dout)
+    else:
+        dod = f32_dev(dout)
+    scale = 1.0 / np.sqrt(K)
+    tdt = torch.bfloat16 if bf16 else torch.float32
+    o = torch.empty((B, H, M, D), dtype=tdt, device="cuda")
+    lse = torch.empty((B, H, M), device="cuda")
+    prm = params(B, H, M, N, K, D, scale, causal, dt)
+    be.dispatch_attention_lse(qd, kd, vd, o, lse, prm)
+    tol = BF16_TOL if bf16 else F32_TOL
+    lse_want = oracle.attention_lse(q, k, scale, causal)
+    fin = np.isfinite(lse_want)
+    got_lse = host(lse)
+    assert np.array_equal(np.isfinite(got_lse), fin)
+    assert np.max(np.abs(got_lse[fin] - lse_want[fin]), initial=0.0) <= 1e-4 * max(1.0, np.abs(lse_want[fin]).max(initial=0.0))
+    dq = torch.full_like(qd, 7.0)
+    dk = torch.full_like(kd, 7.0)
+    dv = torch.full_like(vd, 7.0)
+    be.dispatch_attention_grad(qd, kd, vd, o, dod, lse, dq, dk, dv, prm)
+    # The oracle differentiates the exact forward; feed it the same inputs.
+    wq, wk, wv = oracle.attention_grad(q, k, v, dout, scale, causal)
+    assert rel_max_err(host(dq), wq) <= tol
+    assert rel_max_err(host(dk), wk) <= tol
+    assert rel_max_err(host(dv), wv) <= tol
+
+
+def test_attention_grad_alias_rejected(be):
+    torch = _torch()
+    x = torch.zeros((1, 1, 8, 16), device="cuda")
+    lse = torch.zeros((1, 1, 8), device="cuda")
+    p = params(1, 1, 8, 8, 16, 16, 0.0, False, bwpp.DType.F32)
+    with pytest.raises(bwpp.BwppError) as e:
+        be.dispatch_attention_grad(x, x.clone(), x.clone(), x.clone(), x.clone(), lse, x, x.clone(), x.clone(), p)
+    assert e.value.status == bwpp.Status.ALIAS

@@ -277,3 +277,40 @@ def test_bf16_round_matches_torch(oracle):
     want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
     assert_bits_equal(got, want)
     assert np.isnan(oracle.round_bf16(np.array([np.nan], np.float32)))[0]
+
+
+# ------------------------------------------------------- attention backward
+@pytest.mark.parametrize("B,H,M,N,K,D", [(1, 2, 5, 7, 4, 3), (1, 1, 7, 5, 3, 4), (2, 1, 6, 6, 5, 2)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_grad_vs_finite_differences(oracle, B, H, M, N, K, D, causal):
+    r = _rng(B * 100 + M * 10 + N + int(causal))
+    q = r.normal(size=(B, H, M, K))
+    k = r.normal(size=(B, H, N, K))
+    v = r.normal(size=(B, H, N, D))
+    dout = r.normal(size=(B, H, M, D))
+    scale = 0.7
+    loss = lambda qq, kk, vv: float((_attention64(qq, kk, vv, scale, causal) * dout).sum())
+    fq = _fd(lambda t: loss(t, k, v), q)
+    fk = _fd(lambda t: loss(q, t, v), k)
+    fv = _fd(lambda t: loss(q, k, t), v)
+    dq, dk, dv = oracle.attention_grad(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32),
+                                       dout.astype(np.float32), scale, causal)
+    assert rel_max_err(dq, fq) < 2e-5
+    assert rel_max_err(dk, fk) < 2e-5
+    assert rel_max_err(dv, fv) < 2e-5
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_lse_vs_fp64(oracle, causal):
+    r = _rng(31)
+    q = r.normal(size=(2, 2, 9, 8)).astype(np.float32)
+    k = r.normal(size=(2, 2, 6, 8)).astype(np.float32)
+    s = np.einsum("bhmk,bhnk->bhmn", q.astype(np.float64), k.astype(np.float64)) * 0.5
+    if causal:
+        s = np.where(np.arange(6)[None, :] <= np.arange(9)[:, None] + (6 - 9), s, -np.inf)
+    with np.errstate(divide="ignore"):
+        want = np.log(np.exp(s).sum(axis=-1))
+    got = oracle.attention_lse(q, k, 0.5, causal)
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isfinite(got), fin)
+    assert np.max(np.abs(got[fin] - want[fin])) < 1e-5
