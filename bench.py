@@ -252,6 +252,72 @@ def cpu_baseline_c2(seed, reps):
     }
 
 
+def regress_json(args):
+    """The reference's CPU bench workload (bench/bench_cpu.c: ramp inputs
+    x[i][j] = (i*cols + j + 1) * scale, fp32 matmul without epilogue,
+    softmax, RMSNorm with gamma = 1 and eps 1e-5, `iters` back-to-back calls)
+    run through libbwpp_hip, written in the reference's JSON layout
+    (bench_cpu.c:142-157, read by bench/bench_regress.py:93-111): time_s is
+    the wall time of all iterations.  Each group also carries the GPU rate,
+    its roofline fraction and the oracle's time on one core (cpu_time_s)."""
+    import torch
+    import bwpp
+    from bwpp import synth
+    be = bwpp.HipBackend(0)
+    be.set_stream(torch.cuda.current_stream())
+    M, N, K, rows, cols, iters = args.m, args.n, args.k, args.rows, args.cols, args.iters
+    a = torch.from_numpy(synth.ramp(M, K, 0.01)).cuda()
+    b = torch.from_numpy(synth.ramp(K, N, 0.02)).cuda()
+    c = torch.empty((M, N), device="cuda")
+    x = torch.from_numpy(synth.ramp(rows, cols, 0.01)).cuda()
+    y = torch.empty_like(x)
+    z = torch.empty_like(x)
+    gamma = torch.ones(cols, device="cuda")
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    mp = bwpp.MatmulParams(M, N, K, K, N, N)
+    sp = bwpp.SoftmaxParams(rows, cols, cols)
+    rp = bwpp.RmsnormParams(rows, cols, cols, 1e-5)
+    t_mm = timed(lambda: be.dispatch_matmul(a, b, c, None, mp))
+    t_sm = timed(lambda: be.dispatch_softmax(x, y, sp))
+    t_rn = timed(lambda: be.dispatch_rmsnorm(x, gamma, None, z, rp))
+    be.close()
+    flops = 2.0 * M * N * K * iters
+    nb = 2.0 * rows * cols * 4 * iters
+    out = {
+        "matmul": {"M": M, "N": N, "K": K, "iters": iters, "time_s": round(t_mm, 9),
+                   "gflops": round(flops / t_mm / 1e9, 3),
+                   "gpu_frac_f32_peak": round(flops / t_mm / 1e12 / F32_PEAK_TFLOPS, 5)},
+        "softmax": {"rows": rows, "cols": cols, "iters": iters, "time_s": round(t_sm, 9),
+                    "gpu_GB_s": round(nb / t_sm / 1e9, 2), "gpu_frac_hbm_peak": round(nb / t_sm / 1e9 / HBM_PEAK_GBS, 5)},
+        "rmsnorm": {"rows": rows, "cols": cols, "iters": iters, "time_s": round(t_rn, 9),
+                    "gpu_GB_s": round(nb / t_rn / 1e9, 2), "gpu_frac_hbm_peak": round(nb / t_rn / 1e9 / HBM_PEAK_GBS, 5)},
+        "device": "MI355X (libbwpp_hip)",
+    }
+    if not args.no_cpu:
+        # CPU baseline: the oracle (bit-identical to the reference's C) on one core.
+        sys.path.insert(0, ROOT)
+        from oracle.oracle import Oracle
+        orc = Oracle()
+        ah, bh, xh = a.cpu().numpy(), b.cpu().numpy(), x.cpu().numpy()
+        gh = np.ones(cols, np.float32)
+        for key, fn in (("matmul", lambda: orc.matmul(ah, bh)), ("softmax", lambda: orc.softmax(xh)),
+                        ("rmsnorm", lambda: orc.rmsnorm(xh, gh, None, 1e-5))):
+            t0 = time.perf_counter()
+            for _ in range(iters):
+                fn()
+            out[key]["cpu_time_s"] = round(time.perf_counter() - t0, 9)
+    return out
+
+
 def _events_us(torch, fn, iters, warmup=3):
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
@@ -352,7 +418,43 @@ def extras(be, torch, seed, iters, with_cpu):
             entry["cpu"] = {"GFLOP_s": round(fl / (B * H) / dt / 1e9, 3), "cores": 1, "kind": "port",
                             "sample": "one (batch, head) slice (extrapolated rate)"}
         out["c4_attention_causal" if causal else "c4_attention"] = entry
+    del q, k, v, o
+    out["c5_block_train_f32"] = block_train(be, torch, seed, max(3, iters // 4))
     return out
+
+
+# FLOP of one C5 step: forward GEMMs 2*BT*D*(3D + D + 2F), backward twice
+# that; causal attention 4*B*H*T*T*dh/2 forward, twice that backward
+# (dV, dP, dQ, dK; the recomputed scores are not counted).
+def block_train_flop(B, T, D, H, F):
+    BT = B * T
+    gemm = 2.0 * BT * D * (3 * D + D + 2 * F)
+    attn = 4.0 * B * H * T * T * (D // H) / 2
+    return 3.0 * gemm + 3.0 * attn
+
+
+def block_train(be, torch, seed, iters, B=8, T=512, D=1024, H=16, F=4096):
+    """C5: one forward + backward step of the pre-norm transformer block
+    (bwpp_ir/compiler/transformer_block.py) in fp32, run by the launch-plan
+    executor from its plan file over one mem-planned device arena."""
+    from bwpp import plan
+    text = plan.load_text("transformer_block_train", B=B, T=T, D=D, H=H, F=F)
+    p = plan.Plan(be, text)
+    p.allocate()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    rnd = lambda *shape, std=0.02: torch.randn(*shape, generator=g, device="cuda") * std
+    tensors = {"x": rnd(B * T, D, std=1.0), "g1": 1.0 + rnd(D, std=0.1), "wqkv": rnd(D, 3 * D),
+               "wo": rnd(D, D), "g2": 1.0 + rnd(D, std=0.1), "w1": rnd(D, F), "w2": rnd(F, D)}
+    for name, t in tensors.items():
+        p.bind(name, t)
+    us = _events_us(torch, p.run, iters)
+    fl = block_train_flop(B, T, D, H, F)
+    res = {"workload": f"B{B} T{T} D{D} H{H} F{F} fp32 fwd+bwd", "us_per_step": round(us, 1),
+           "TFLOP_s": round(fl / us / 1e6, 1), "frac_f32_peak": round(fl / us / 1e6 / F32_PEAK_TFLOPS, 4),
+           "arena_bytes": p.arena_bytes, "ops_per_step": sum(1 for ln in text.splitlines() if ln.startswith("op "))}
+    p.close()
+    return res
 
 
 def main():
@@ -370,7 +472,23 @@ def main():
                     help="also run N plain copies of known size (for scaling --pmc byte counters)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="no GPU: turn two rocprofv3 --pmc output dirs into profiles/traffic.json")
+    ap.add_argument("--regress-json", metavar="PATH",
+                    help="run the reference bench workload (bench_cpu.c) and write its JSON layout to PATH")
+    ap.add_argument("--m", type=int, default=256)
+    ap.add_argument("--n", type=int, default=256)
+    ap.add_argument("--k", type=int, default=256)
+    ap.add_argument("--rows", type=int, default=256)
+    ap.add_argument("--cols", type=int, default=256)
+    ap.add_argument("--iters", type=int, default=10)
     args = ap.parse_args()
+
+    if args.regress_json:
+        out = regress_json(args)
+        with open(args.regress_json, "w") as f:
+            json.dump(out, f, indent=2)
+            f.write("\n")
+        print(json.dumps(out))
+        return
 
     if args.traffic_from:
         t = traffic_from_pmc(*args.traffic_from)

@@ -4,7 +4,7 @@ The compute path is the C library libbwpp_hip.so and its gfx950 code
 objects (lib/); this package only binds them.  There is no CPU fallback:
 if the library or a code object is missing, HipBackend() raises.
 """
-from . import _lib, synth
+from . import _lib, plan, synth
 from ._lib import (AttentionParams, DType, ElementwiseParams, Epilogue,
                    LibraryMissing, MatmulParams, ReduceParams, RmsnormParams,
                    SoftmaxParams, Status)
@@ -12,7 +12,7 @@ from .backend import BwppError, HipBackend
 
 __all__ = ["HipBackend", "BwppError", "LibraryMissing", "Status", "DType",
            "Epilogue", "MatmulParams", "SoftmaxParams", "RmsnormParams",
-           "AttentionParams", "ReduceParams", "ElementwiseParams", "synth",
+           "AttentionParams", "ReduceParams", "ElementwiseParams", "synth", "plan",
            "load_library"]
 
 

@@ -103,6 +103,15 @@ SIGNATURES = {
     "bwpp_hip_arena_destroy": (None, [POINTER(Arena)]),
     "bwpp_hip_copy_to_device": (c_int, [_P, _P, _P, c_size_t]),
     "bwpp_hip_copy_to_host": (c_int, [_P, _P, _P, c_size_t]),
+    "bwpp_hip_plan_create": (c_int, [_P, c_char_p, POINTER(c_void_p)]),
+    "bwpp_hip_plan_destroy": (None, [_P]),
+    "bwpp_hip_plan_last_error": (c_char_p, [_P]),
+    "bwpp_hip_plan_arena_bytes": (c_size_t, [_P]),
+    "bwpp_hip_plan_allocate": (c_int, [_P]),
+    "bwpp_hip_plan_bind": (c_int, [_P, c_char_p, _P]),
+    "bwpp_hip_plan_value_ptr": (_P, [_P, c_char_p]),
+    "bwpp_hip_plan_run": (c_int, [_P]),
+    "bwpp_hip_plan_report": (c_size_t, [_P, c_char_p, c_size_t]),
     "bwpp_hip_dispatch_matmul": (c_int, [_P, _P, _P, _P, _P, MatmulParams]),
     "bwpp_hip_dispatch_softmax": (c_int, [_P, _P, _P, SoftmaxParams]),
     "bwpp_hip_dispatch_rmsnorm": (c_int, [_P, _P, _P, _P, _P, RmsnormParams]),

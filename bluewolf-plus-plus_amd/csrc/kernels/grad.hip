@@ -169,6 +169,7 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_elementwise(const BwppGra
         case 1: v = ar[c] - bv; break;
         case 2: v = ar[c] * bv; break;
         case 3: v = ar[c] / bv; break;
+        case 5: v = bv / (1.0f + expf(-bv)); break;  // SiLU of b (bwpp_cpu_ref.c:4-6)
         default: v = bv; break;
       }
       orow[c] = v;

@@ -8,6 +8,7 @@
 // front, so a missing kernel is an error at bwpp_hip_create() and never a
 // silent no-op at dispatch time (dispatch_stub.m:94-98).
 #include "bwpp_hip.h"
+#include "internal.h"
 
 #include <hip/hip_runtime_api.h>
 
@@ -746,9 +747,28 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention_lse(BwppHip *h, const void 
   return attn_forward(h, q, k, v, o, lse, p);
 }
 
+namespace {
+BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const void *v, const void *o,
+                             const void *dout, const float *lse, void *dq, void *dk, void *dv,
+                             const BwppAttentionParams &p, bool check_alias);
+}  // namespace
+
 extern "C" BwppHipStatus bwpp_hip_dispatch_attention_grad(BwppHip *h, const void *q, const void *k, const void *v,
                                                           const void *o, const void *dout, const float *lse,
                                                           void *dq, void *dk, void *dv, BwppAttentionParams p) {
+  return attn_grad_impl(h, q, k, v, o, dout, lse, dq, dk, dv, p, true);
+}
+
+BwppHipStatus bwpp_hip_attention_grad_planned(BwppHip *h, const void *q, const void *k, const void *v,
+                                              const void *o, const void *dout, const float *lse, void *dq,
+                                              void *dk, void *dv, const BwppAttentionParams &p) {
+  return attn_grad_impl(h, q, k, v, o, dout, lse, dq, dk, dv, p, false);
+}
+
+namespace {
+BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const void *v, const void *o,
+                             const void *dout, const float *lse, void *dq, void *dk, void *dv,
+                             const BwppAttentionParams &p, bool check_alias) {
   BwppHipStatus s = enter(h);
   if (s != BWPP_HIP_OK) return s;
   if (!dout || !lse || !dq || !dk || !dv)
@@ -773,11 +793,13 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention_grad(BwppHip *h, const void
   const Extent edq = hull(dq, g.q_bs, g.q_hs, p.M, p.K, g.ldq), edk = hull(dk, g.k_bs, g.k_hs, p.N, p.K, g.ldk);
   const Extent edv = hull(dv, g.v_bs, g.v_hs, p.N, p.D, g.ldv);
   const Extent else_{(uintptr_t)lse, (uintptr_t)lse + slices * p.M * 4};
-  for (const Extent &out : {edq, edk, edv})
-    for (const Extent &in : {eq, ek, ev, eo, edo, else_})
-      if (overlaps(out, in)) return fail(h, BWPP_HIP_ERR_ALIAS, "attention_grad: an output overlaps an input");
-  if (overlaps(edq, edk) || overlaps(edq, edv) || overlaps(edk, edv))
-    return fail(h, BWPP_HIP_ERR_ALIAS, "attention_grad: dq, dk and dv overlap");
+  if (check_alias) {
+    for (const Extent &out : {edq, edk, edv})
+      for (const Extent &in : {eq, ek, ev, eo, edo, else_})
+        if (overlaps(out, in)) return fail(h, BWPP_HIP_ERR_ALIAS, "attention_grad: an output overlaps an input");
+    if (overlaps(edq, edk) || overlaps(edq, edv) || overlaps(edk, edv))
+      return fail(h, BWPP_HIP_ERR_ALIAS, "attention_grad: dq, dk and dv overlap");
+  }
   if ((s = ensure_ws(h, (size_t)slices * p.M * sizeof(float) + 4)) != BWPP_HIP_OK) return s;
   const int bf = p.dtype == BWPP_HIP_BF16 ? 1 : 0, causal = p.causal ? 1 : 0;
   g.scale_log2 = p.scale != 0.0f ? p.scale : 1.0f;
@@ -801,6 +823,7 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention_grad(BwppHip *h, const void
   }
   return BWPP_HIP_OK;
 }
+}  // namespace
 
 // ------------------------------------------------------------- grad ops
 
@@ -946,15 +969,16 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_elementwise(BwppHip *h, const float *
                                                        BwppElementwiseParams p) {
   BwppHipStatus s = enter(h);
   if (s != BWPP_HIP_OK) return s;
-  if (p.op > BWPP_HIP_OP_COPY || p.bmode > BWPP_HIP_BCAST_SCALAR)
+  if (p.op > BWPP_HIP_OP_SILU || p.bmode > BWPP_HIP_BCAST_SCALAR)
     return fail(h, BWPP_HIP_ERR_INVALID_ARG, "elementwise: bad op %u or broadcast %u", p.op, p.bmode);
-  if (!b || !out || (p.op != BWPP_HIP_OP_COPY && !a))
+  const bool unary = p.op == BWPP_HIP_OP_COPY || p.op == BWPP_HIP_OP_SILU;
+  if (!b || !out || (!unary && !a))
     return fail(h, BWPP_HIP_ERR_INVALID_ARG, "elementwise: NULL pointer");
   const uint32_t ld = eff_ld(p.ld, p.cols);
   if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
   if (p.rows == 0 || p.cols == 0) return BWPP_HIP_OK;
   BwppGradArgs g = {};
-  g.a = p.op == BWPP_HIP_OP_COPY ? nullptr : a;
+  g.a = unary ? nullptr : a;
   g.b = b;
   g.out = out;
   g.rows = p.rows;

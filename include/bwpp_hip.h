@@ -139,14 +139,16 @@ typedef struct {
 
 /* Elementwise glue of the autodiff graph (graph_ir.c:697-770, 1457-1470,
  * 1585-1654): out = a (op) b with b broadcast as selected; op COPY writes
- * the broadcast b (a unused).  rows x cols with leading dimension ld
- * (0 = cols) for a, out and a full b. */
+ * the broadcast b and op SILU its SiLU b / (1 + expf(-b)) (graph op
+ * BWPP_GOP_SILU, bwpp_cpu_ref.c:4-6; a unused for both).  rows x cols with
+ * leading dimension ld (0 = cols) for a, out and a full b. */
 typedef enum {
   BWPP_HIP_OP_ADD = 0,
   BWPP_HIP_OP_SUB = 1,
   BWPP_HIP_OP_MUL = 2,
   BWPP_HIP_OP_DIV = 3,
-  BWPP_HIP_OP_COPY = 4
+  BWPP_HIP_OP_COPY = 4,
+  BWPP_HIP_OP_SILU = 5
 } BwppHipElementwiseOp;
 typedef enum {
   BWPP_HIP_BCAST_FULL = 0,   /* b is rows x cols */
@@ -320,6 +322,37 @@ BwppHipStatus bwpp_hip_dispatch_reduce_sum(BwppHip *h, const float *x, float *ou
 /* add / sub / mul / div with broadcasting, and broadcast (op COPY). */
 BwppHipStatus bwpp_hip_dispatch_elementwise(BwppHip *h, const float *a, const float *b, float *out,
                                             BwppElementwiseParams params);
+
+/* ---- launch plans (compiled graphs) ----
+ *
+ * The executor for a lowered BW++ graph: `bwppc` hands its graph to the
+ * Metal codegen today (main.c:186, codegen_metal.h:7); a HIP target emits
+ * this text instead (format in csrc/runtime/bwpp_plan.cpp: dims, named
+ * values, strided views, ordered operator launches over the dispatch calls
+ * above).  Creation parses and builds the memory plan: liveness-based
+ * buffer reuse as compiler/mem_plan.c:43-146, with byte sizes from the
+ * bound dims and no operator ever given the buffer of one of its own
+ * inputs.  h may be NULL to parse and plan only (report, arena size).
+ * On failure *out still receives a plan whose last_error says why; destroy
+ * it. */
+typedef struct BwppHipPlan BwppHipPlan;
+BwppHipStatus bwpp_hip_plan_create(BwppHip *h, const char *text, BwppHipPlan **out);
+void bwpp_hip_plan_destroy(BwppHipPlan *plan);
+const char *bwpp_hip_plan_last_error(const BwppHipPlan *plan);
+/* Device bytes of all planned buffers (temps, outputs, consts). */
+size_t bwpp_hip_plan_arena_bytes(const BwppHipPlan *plan);
+/* One device arena (bwpp_hip_arena_init) holding every planned buffer;
+ * const values are filled. */
+BwppHipStatus bwpp_hip_plan_allocate(BwppHipPlan *plan);
+/* Caller memory for an input or param value. */
+BwppHipStatus bwpp_hip_plan_bind(BwppHipPlan *plan, const char *name, void *device_ptr);
+/* Device address of any value (NULL if unknown or not yet placed). */
+void *bwpp_hip_plan_value_ptr(const BwppHipPlan *plan, const char *name);
+/* Runs every launch in order on the handle's stream. */
+BwppHipStatus bwpp_hip_plan_run(BwppHipPlan *plan);
+/* Memory-plan report in mem_plan.c:176-193's layout plus byte sizes, arena
+ * offsets and the total; returns the bytes needed including the NUL. */
+size_t bwpp_hip_plan_report(const BwppHipPlan *plan, char *buf, size_t cap);
 
 /* ---- synthetic inputs (host memory, no device needed) ----
  * Counter-based: element i of (seed, stream) is a pure function of

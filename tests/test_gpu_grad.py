@@ -106,6 +106,18 @@ def test_elementwise(be, op, bmode):
     assert_bits_equal(host(out), want)
 
 
+@pytest.mark.parametrize("n", [1, 70, 4096 * 1024 + 3])
+def test_elementwise_silu(be, n):
+    """Op 5 (unary SiLU, the executor's forward activation when it is not
+    fused into a GEMM) of the b operand: b / (1 + exp(-b)) in fp32 against float64; the GPU
+    exp is not correctly rounded, so the bar is a few ulps, not bits."""
+    x = synth.normal((1, n), n, 0, 0.0, 4.0)
+    out = _torch().empty((1, n), device="cuda")
+    be.dispatch_elementwise(None, dev(x), out, bwpp.ElementwiseParams(1, n, n, 5, 0))
+    xd = x.astype(np.float64)
+    assert rel_max_err(host(out), xd / (1.0 + np.exp(-xd))) <= 1e-6
+
+
 def test_grad_invalid_args(be):
     torch = _torch()
     x = torch.zeros(8, device="cuda")

@@ -1,0 +1,71 @@
+"""Launch-plan parsing and memory planning (no GPU: the plan is created
+without a device handle).  The planner follows compiler/mem_plan.c:43-146
+(buffer reuse by liveness) but sizes buffers in bytes from the bound dims
+and never gives an operator the buffer of one of its own inputs -- the
+reference frees inputs before allocating the output (mem_plan.c:89-140)."""
+import re
+
+import pytest
+
+from bwpp import plan
+
+SMALL = dict(B=2, T=64, D=128, H=2, F=256)
+
+
+def _ops_and_views(text):
+    views, ops = {}, []
+    for line in text.splitlines():
+        t = line.split("#")[0].split()
+        if not t:
+            continue
+        if t[0] == "view":
+            views[t[1]] = dict(kv.split("=", 1) for kv in t[2:])["of"]
+        elif t[0] == "op":
+            kv = dict(x.split("=", 1) for x in t[2:] if "=" in x)
+            ops.append((t[1], kv["out"].split(","), kv.get("in", "").split(",")))
+    return ops, views
+
+
+def _buffers(report):
+    return {m.group(2): int(m.group(1)) for m in re.finditer(r"-> buffer(\d+)  # (\S+)", report)}
+
+
+@pytest.mark.parametrize("dims", [{}, SMALL])
+def test_block_plan_report_and_no_self_alias(dims):
+    text = plan.load_text("transformer_block_train", **dims)
+    p = plan.Plan(None, text)
+    rep = p.report()
+    head = rep.splitlines()[0]
+    assert re.fullmatch(r"buffers=\d+ values=\d+", head)
+    nbuf = int(head.split()[0].split("=")[1])
+    assert all(re.fullmatch(r"buffer\d+ f32 \[[^\]]*\] row_major bytes=\d+ offset=\d+", l)
+               for l in rep.splitlines()[1:1 + nbuf])
+    buf = _buffers(rep)
+    ops, views = _ops_and_views(text)
+    base = lambda n: views.get(n, n)
+    ntemps = sum(1 for l in text.splitlines() if l.split()[:1] == ["value"] and l.split()[-1] == "temp")
+    assert nbuf < ntemps + 12, "temps were not reused"
+    for kind, outs, ins in ops:
+        ob = {buf[base(o)] for o in outs if base(o) in buf}
+        ib = {buf[base(i)] for i in ins if base(i) in buf}
+        assert not (ob & ib), f"{kind}: output shares a buffer with an input"
+    assert p.arena_bytes == int(rep.strip().splitlines()[-1].split("=")[1])
+
+
+def test_block_plan_arena_fits_reuse():
+    """Full-size config 5: every temp of fwd + bwd in well under 1 GB."""
+    p = plan.Plan(None, plan.load_text("transformer_block_train"))
+    assert 0.3e9 < p.arena_bytes < 1.0e9
+
+
+@pytest.mark.parametrize("text,msg", [
+    ("dim B 2\n", "bwpp.plan 1"),
+    ("bwpp.plan 1\nvalue x f32 [Q,4] input\n", "unknown dim"),
+    ("bwpp.plan 1\nvalue x f32 [4,4] temp\nop softmax out=y in=x\n", "unknown value"),
+    ("bwpp.plan 1\nvalue x f32 [4,4] input\nview v of=x offset=8 ld=4 shape=[3,4]\n", "runs past"),
+    ("bwpp.plan 1\nvalue x f32 [4,4] temp\nvalue y f32 [4,4] output\nop softmax out=y in=x\n", "never written"),
+])
+def test_plan_errors(text, msg):
+    with pytest.raises(plan.PlanError) as e:
+        plan.Plan(None, text)
+    assert msg in str(e.value)
