@@ -42,6 +42,12 @@ typedef struct {
   uint32_t tiles_n;  /* ceil(N / BN) */
   uint32_t group_m;  /* tile-order group height (in tiles) */
   uint32_t vec_ok;   /* 1: rows are 16-byte aligned (edge kernels only) */
+  /* Split-K (fp32 full tiles): block b computes K range [s * kchunk, ..)
+   * of tile b % tiles for s = b / tiles into part[s] ([M][N] raw sums);
+   * bwpp_gemm_f32_splitk_reduce then applies the epilogue. */
+  uint32_t ksplit;
+  uint32_t kchunk;
+  float *part;
 } BwppGemmArgs;
 
 /* Attention: O = softmax(scale * Q K^T [causal]) V per (batch, head). */
@@ -69,6 +75,7 @@ typedef struct {
   void *dk;
   void *dv;
   float *dsum;
+  float scale; /* the plain score scale (fp32 MFMA path, which gets scale * log2(e) in scale_log2) */
 } BwppAttnArgs;
 
 /* Grad ops and elementwise glue (grad.hip). */

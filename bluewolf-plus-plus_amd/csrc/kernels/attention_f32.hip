@@ -1,0 +1,470 @@
+// Attention forward and backward on the fp32 matrix cores of gfx950
+// (v_mfma_f32_32x32x2_f32), fp32 storage, head dims K = D in {64, 128}:
+//   forward   O = softmax(scale Q K^T [causal]) V, plus the per-query
+//             natural-log log-sum-exp (lse) when requested;
+//   backward  with p = exp(scale q.k - lse) and D_m = rowsum(dO * O)[m]:
+//             dS = p (dO.v - D_m), dQ = scale dS K, dK = scale dS^T Q,
+//             dV = P^T dO.
+// Semantics: runtime/cpu/bwpp_cpu_ref.c:92-144 (row max, sum of exp,
+// inv = sum > 0 ? 1/sum : 0) generalised with a score scale and a
+// bottom-right aligned causal mask (key n visible to query m iff
+// n <= m + N - M); the backward is the closed form of the graph's
+// softmax_grad chain (compiler/graph_ir.c:1722-1733) fused per tile.
+//
+// Work layout.  A block is kW waves; each wave owns 32 rows (queries for
+// the forward and dQ kernels, keys for the dK/dV kernel) and the block
+// streams 32-row tiles of the other side through a two-stage LDS ring
+// (register prefetch of tile t+1 during tile t, one barrier per tile).
+// LDS rows are padded to D + 4 floats, so the 16-byte reads of eight
+// consecutive rows hit distinct banks.
+//
+// MFMA operand layout (32x32x2 fp32, pinned by tests/test_gpu_mfma_layout):
+// lane l supplies A[l % 32][l / 32] and B[l / 32][l % 32]; accumulator
+// register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+// A dot product over the head dim runs in D/2 steps; step s pairs d = s
+// (lanes 0-31) with d = D/2 + s (lanes 32-63), so each lane's operand is
+// a contiguous half row (16-byte LDS reads, 16-byte global loads).
+// A product over 32 rows of scores runs in 16 steps; step j pairs row
+// 8 (j / 4) + j % 4 (lanes 0-31) with that row + 4 (lanes 32-63), which is
+// exactly the row held by accumulator register j: probabilities and dS go
+// from the accumulator into the "B" operand without data movement.
+//
+// Softmax runs in base 2 on scores multiplied by scale * log2(e) (passed
+// as scale_log2; the plain scale is in scale).  A query's 32 scores of a
+// tile are split between lanes l and l ^ 32: one permlane32 swap combines
+// row maxima and the final row sums.
+#include "common.h"
+#include "../kargs.h"
+
+using namespace bwpp;
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr int kW = 2;   // waves per block
+constexpr int kR = 32;  // rows per wave and per streamed tile
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ f32x16 mfma(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Symmetric combines of lane l with lane l ^ 32.
+__device__ __forceinline__ float max32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Row of accumulator register r (and of score-pair step r) for lane half hi.
+__device__ __forceinline__ int acc_row(int r, int hi) { return 8 * (r >> 2) + 4 * hi + (r & 3); }
+
+// Block-wide copy of two [kR x D] fp32 tiles (rows r0.., zero past `rows`)
+// from global memory into registers, then into a padded LDS stage.
+template <int D>
+struct TilePair {
+  static constexpr int C4 = D / 4;                   // float4 per row
+  static constexpr int PER = kR * C4 / (64 * kW);    // float4 per thread per tile
+  static constexpr int ST = D + 4;                   // LDS row stride (floats)
+  f32x4 x[PER], y[PER];
+
+  __device__ __forceinline__ void fetch(const float *X, uint32_t ldx, const float *Y, uint32_t ldy, uint32_t r0,
+                                        uint32_t rows) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = (int)threadIdx.x + i * 64 * kW;
+      const int r = idx / C4, c = idx % C4;
+      const uint32_t row = r0 + (uint32_t)r;
+      if (row < rows) {
+        x[i] = *reinterpret_cast<const f32x4 *>(X + (size_t)row * ldx + 4 * c);
+        y[i] = *reinterpret_cast<const f32x4 *>(Y + (size_t)row * ldy + 4 * c);
+      } else {
+        x[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        y[i] = x[i];
+      }
+    }
+  }
+  __device__ __forceinline__ void stash(float *lx, float *ly) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = (int)threadIdx.x + i * 64 * kW;
+      const int r = idx / C4, c = idx % C4;
+      *reinterpret_cast<f32x4 *>(lx + r * ST + 4 * c) = x[i];
+      *reinterpret_cast<f32x4 *>(ly + r * ST + 4 * c) = y[i];
+    }
+  }
+};
+
+// Half row (D/2 floats at column hi * D/2) of a [rows x ld] matrix into
+// registers; zeros for rows past the end.
+template <int D>
+__device__ __forceinline__ void load_half_row(float (&dst)[D / 2], const float *X, uint32_t ld, uint32_t row,
+                                              uint32_t rows, int hi) {
+  if (row < rows) {
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(X + (size_t)row * ld + hi * (D / 2));
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+      const f32x4 v = src[i];
+      dst[4 * i] = v[0];
+      dst[4 * i + 1] = v[1];
+      dst[4 * i + 2] = v[2];
+      dst[4 * i + 3] = v[3];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < D / 2; ++i) dst[i] = 0.0f;
+  }
+}
+
+// acc += X_tile(rows li, half hi) . reg over the head dim: X_tile is an LDS
+// tile [kR][D + 4], reg the lane's half row of the other operand.
+template <int D>
+__device__ __forceinline__ f32x16 dot_tile(const float *tile, const float (&reg)[D / 2], int li, int hi) {
+  f32x16 acc = {};
+  const float *row = tile + li * (D + 4) + hi * (D / 2);
+#pragma unroll
+  for (int j = 0; j < D / 2; j += 4) {
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(row + j);
+    acc = mfma(v[0], reg[j], acc);
+    acc = mfma(v[1], reg[j + 1], acc);
+    acc = mfma(v[2], reg[j + 2], acc);
+    acc = mfma(v[3], reg[j + 3], acc);
+  }
+  return acc;
+}
+
+// out[blk] (transposed [d][row-of-other-side]) += tile^T . w over the 32
+// tile rows: tile [kR][D + 4] in LDS, w the 16 accumulator-layout weights.
+template <int D>
+__device__ __forceinline__ void acc_tile_t(f32x16 (&out)[D / 32], const float *tile, const f32x16 &w, int li,
+                                           int hi) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float *row = tile + acc_row(j, hi) * (D + 4) + li;
+#pragma unroll
+    for (int blk = 0; blk < D / 32; ++blk) out[blk] = mfma(row[32 * blk], w[j], out[blk]);
+  }
+}
+
+// Stores a transposed accumulator block set (out[blk] register r = element
+// [d = 32 blk + acc_row(r, hi)] of row `row`) as 16-byte pieces, times f.
+template <int D>
+__device__ __forceinline__ void store_t(float *X, uint32_t ld, uint32_t row, const f32x16 (&acc)[D / 32], float f,
+                                        int hi) {
+  float *dst = X + (size_t)row * ld + 4 * hi;
+#pragma unroll
+  for (int blk = 0; blk < D / 32; ++blk)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+      *reinterpret_cast<f32x4 *>(dst + 32 * blk + 8 * r4) =
+          f32x4{acc[blk][4 * r4] * f, acc[blk][4 * r4 + 1] * f, acc[blk][4 * r4 + 2] * f, acc[blk][4 * r4 + 3] * f};
+}
+
+struct Slice {
+  uint32_t bh, b, h;
+};
+
+__device__ __forceinline__ Slice slice_of(const BwppAttnArgs &a, uint32_t nbh) {
+  Slice s;
+  s.bh = blockIdx.x % nbh;
+  s.b = s.bh / a.heads;
+  s.h = s.bh % a.heads;
+  return s;
+}
+
+// ----------------------------------------------------------------- forward
+template <int D, bool CAUSAL>
+__device__ __forceinline__ void attn_fwd(const BwppAttnArgs &a) {
+  using Tiles = TilePair<D>;
+  constexpr int ST = Tiles::ST;
+  __shared__ __attribute__((aligned(16))) float lds[2][2][kR * ST];  // [stage][K, V]
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const int li = lane & 31, hi = lane >> 5;
+  const uint32_t nbh = gridDim.x / a.q_tiles;
+  const uint32_t qt = a.q_tiles - 1 - blockIdx.x / nbh;  // heaviest (causal) first
+  const Slice sl = slice_of(a, nbh);
+  const float *Q = static_cast<const float *>(a.q) + sl.b * a.q_bs + sl.h * a.q_hs;
+  const float *K = static_cast<const float *>(a.k) + sl.b * a.k_bs + sl.h * a.k_hs;
+  const float *V = static_cast<const float *>(a.v) + sl.b * a.v_bs + sl.h * a.v_hs;
+  float *O = static_cast<float *>(a.o) + sl.b * a.o_bs + sl.h * a.o_hs;
+  const int64_t diag = (int64_t)a.N - (int64_t)a.M;
+  const uint32_t qb = qt * (kW * kR), q0 = qb + (uint32_t)wave * kR, qi = q0 + (uint32_t)li;
+
+  uint32_t kend = a.N;
+  if (CAUSAL) {
+    const int64_t last = (int64_t)min(a.M, qb + kW * kR) - 1 + diag;
+    kend = last < 0 ? 0u : (uint32_t)min<int64_t>(last + 1, (int64_t)a.N);
+  }
+  const uint32_t nt = (kend + kR - 1) / kR;
+  const int64_t wlast = (int64_t)q0 + kR - 1 + diag;  // last key any query of the wave sees (causal)
+
+  float qreg[D / 2];
+  load_half_row<D>(qreg, Q, a.ldq, qi, a.M, hi);
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int blk = 0; blk < D / 32; ++blk) o[blk] = f32x16{};
+  float mrun = -INFINITY, lsum = 0.0f;
+  const float c = a.scale_log2;
+
+  Tiles pf;
+  if (nt > 0) {
+    pf.fetch(K, a.ldk, V, a.ldv, 0, a.N);
+    pf.stash(lds[0][0], lds[0][1]);
+  }
+  __syncthreads();
+  for (uint32_t t = 0; t < nt; ++t) {
+    const int st = (int)(t & 1);
+    const uint32_t k0 = t * kR;
+    if (t + 1 < nt) pf.fetch(K, a.ldk, V, a.ldv, k0 + kR, a.N);
+    if (!CAUSAL || (int64_t)k0 <= wlast) {  // wave-uniform
+      f32x16 s = dot_tile<D>(lds[st][0], qreg, li, hi);
+      const bool edge = k0 + kR > a.N || (CAUSAL && (int64_t)k0 + kR - 1 > (int64_t)q0 + diag);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float v = s[r] * c;
+        if (edge) {
+          const uint32_t key = k0 + (uint32_t)acc_row(r, hi);
+          if (key >= a.N || (CAUSAL && (int64_t)key > (int64_t)qi + diag)) v = -INFINITY;
+        }
+        s[r] = v;
+        mx = fmaxf(mx, v);
+      }
+      mx = max32(mx);
+      const float mnew = fmaxf(mrun, mx);
+      const float mu = mnew == -INFINITY ? 0.0f : mnew;
+      const float alpha = __builtin_amdgcn_exp2f(mrun - mu);
+      float ps = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = __builtin_amdgcn_exp2f(s[r] - mu);
+        ps += s[r];
+      }
+      lsum = lsum * alpha + ps;
+      mrun = mnew;
+#pragma unroll
+      for (int blk = 0; blk < D / 32; ++blk) o[blk] *= alpha;
+      acc_tile_t<D>(o, lds[st][1], s, li, hi);
+    }
+    if (t + 1 < nt) pf.stash(lds[st ^ 1][0], lds[st ^ 1][1]);
+    __syncthreads();
+  }
+  const float ltot = sum32(lsum);
+  if (qi < a.M) {
+    store_t<D>(O, a.ldo, qi, o, ltot > 0.0f ? 1.0f / ltot : 0.0f, hi);
+    if (a.lse && hi == 0) a.lse[(size_t)sl.bh * a.M + qi] = ltot > 0.0f ? (mrun + log2f(ltot)) * kLn2 : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------- backward
+// dQ pass: a wave owns 32 queries and streams K / V tiles; it also writes
+// D_m = rowsum(dO * O) for the dK / dV pass.
+template <int D, bool CAUSAL>
+__device__ __forceinline__ void attn_bwd_dq(const BwppAttnArgs &a) {
+  using Tiles = TilePair<D>;
+  constexpr int ST = Tiles::ST;
+  __shared__ __attribute__((aligned(16))) float lds[2][2][kR * ST];  // [stage][K, V]
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const int li = lane & 31, hi = lane >> 5;
+  const uint32_t nbh = gridDim.x / a.q_tiles;
+  const uint32_t qt = a.q_tiles - 1 - blockIdx.x / nbh;
+  const Slice sl = slice_of(a, nbh);
+  const float *Q = static_cast<const float *>(a.q) + sl.b * a.q_bs + sl.h * a.q_hs;
+  const float *K = static_cast<const float *>(a.k) + sl.b * a.k_bs + sl.h * a.k_hs;
+  const float *V = static_cast<const float *>(a.v) + sl.b * a.v_bs + sl.h * a.v_hs;
+  const float *O = static_cast<const float *>(a.o) + sl.b * a.o_bs + sl.h * a.o_hs;
+  const float *dO = static_cast<const float *>(a.dout) + sl.b * a.o_bs + sl.h * a.o_hs;
+  float *dQ = static_cast<float *>(a.dq) + sl.b * a.q_bs + sl.h * a.q_hs;
+  const int64_t diag = (int64_t)a.N - (int64_t)a.M;
+  const uint32_t qb = qt * (kW * kR), q0 = qb + (uint32_t)wave * kR, qi = q0 + (uint32_t)li;
+
+  uint32_t kend = a.N;
+  if (CAUSAL) {
+    const int64_t last = (int64_t)min(a.M, qb + kW * kR) - 1 + diag;
+    kend = last < 0 ? 0u : (uint32_t)min<int64_t>(last + 1, (int64_t)a.N);
+  }
+  const uint32_t nt = (kend + kR - 1) / kR;
+  const int64_t wlast = (int64_t)q0 + kR - 1 + diag;
+
+  float qreg[D / 2], greg[D / 2];
+  load_half_row<D>(qreg, Q, a.ldq, qi, a.M, hi);
+  load_half_row<D>(greg, dO, a.ldo, qi, a.M, hi);
+  float dsum;
+  {
+    float orow[D / 2];
+    load_half_row<D>(orow, O, a.ldo, qi, a.M, hi);
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < D / 2; ++i) part += greg[i] * orow[i];
+    dsum = sum32(part);
+  }
+  if (qi < a.M && hi == 0) a.dsum[(size_t)sl.bh * a.M + qi] = dsum;
+  // Queries past M: +inf makes every probability exp2(-inf) = 0.
+  const float lse2 = qi < a.M ? a.lse[(size_t)sl.bh * a.M + qi] * kLog2e : INFINITY;
+  const float c = a.scale_log2;
+
+  f32x16 dq[D / 32];
+#pragma unroll
+  for (int blk = 0; blk < D / 32; ++blk) dq[blk] = f32x16{};
+
+  Tiles pf;
+  if (nt > 0) {
+    pf.fetch(K, a.ldk, V, a.ldv, 0, a.N);
+    pf.stash(lds[0][0], lds[0][1]);
+  }
+  __syncthreads();
+  for (uint32_t t = 0; t < nt; ++t) {
+    const int st = (int)(t & 1);
+    const uint32_t k0 = t * kR;
+    if (t + 1 < nt) pf.fetch(K, a.ldk, V, a.ldv, k0 + kR, a.N);
+    if (!CAUSAL || (int64_t)k0 <= wlast) {
+      f32x16 s = dot_tile<D>(lds[st][0], qreg, li, hi);   // S^T [key][query]
+      const f32x16 dp = dot_tile<D>(lds[st][1], greg, li, hi);  // dP^T = V dO^T
+      const bool edge = k0 + kR > a.N || (CAUSAL && (int64_t)k0 + kR - 1 > (int64_t)q0 + diag);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = __builtin_amdgcn_exp2f(s[r] * c - lse2);
+        if (edge) {
+          const uint32_t key = k0 + (uint32_t)acc_row(r, hi);
+          if (key >= a.N || (CAUSAL && (int64_t)key > (int64_t)qi + diag)) p = 0.0f;
+        }
+        s[r] = p * (dp[r] - dsum);  // dS^T
+      }
+      acc_tile_t<D>(dq, lds[st][0], s, li, hi);  // dQ^T += K^T dS^T
+    }
+    if (t + 1 < nt) pf.stash(lds[st ^ 1][0], lds[st ^ 1][1]);
+    __syncthreads();
+  }
+  if (qi < a.M) store_t<D>(dQ, a.ldq, qi, dq, a.scale, hi);
+}
+
+// dK / dV pass: a wave owns 32 keys and streams Q / dO tiles with their
+// lse and D_m.
+template <int D, bool CAUSAL>
+__device__ __forceinline__ void attn_bwd_dkdv(const BwppAttnArgs &a) {
+  using Tiles = TilePair<D>;
+  constexpr int ST = Tiles::ST;
+  __shared__ __attribute__((aligned(16))) float lds[2][2][kR * ST];  // [stage][Q, dO]
+  __shared__ __attribute__((aligned(16))) float rowv[2][2][kR];      // [stage][lse2, D_m]
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const int li = lane & 31, hi = lane >> 5;
+  const uint32_t nbh = gridDim.x / a.q_tiles;  // q_tiles holds the key tiles here
+  const uint32_t kt = blockIdx.x / nbh;          // heaviest (causal) first
+  const Slice sl = slice_of(a, nbh);
+  const float *Q = static_cast<const float *>(a.q) + sl.b * a.q_bs + sl.h * a.q_hs;
+  const float *K = static_cast<const float *>(a.k) + sl.b * a.k_bs + sl.h * a.k_hs;
+  const float *V = static_cast<const float *>(a.v) + sl.b * a.v_bs + sl.h * a.v_hs;
+  const float *dO = static_cast<const float *>(a.dout) + sl.b * a.o_bs + sl.h * a.o_hs;
+  float *dK = static_cast<float *>(a.dk) + sl.b * a.k_bs + sl.h * a.k_hs;
+  float *dV = static_cast<float *>(a.dv) + sl.b * a.v_bs + sl.h * a.v_hs;
+  const float *lse = a.lse + (size_t)sl.bh * a.M;
+  const float *dsum = a.dsum + (size_t)sl.bh * a.M;
+  const int64_t diag = (int64_t)a.N - (int64_t)a.M;
+  const uint32_t kb = kt * (kW * kR), k0w = kb + (uint32_t)wave * kR, ni = k0w + (uint32_t)li;
+
+  // Queries that see a key n: m >= n - diag (causal).
+  uint32_t mbeg = 0;
+  if (CAUSAL) {
+    const int64_t first = (int64_t)kb - diag;
+    mbeg = first <= 0 ? 0u : (first >= (int64_t)a.M ? a.M : (uint32_t)first);
+    mbeg -= mbeg % kR;
+  }
+  const uint32_t nt = a.M > mbeg ? (a.M - mbeg + kR - 1) / kR : 0u;
+  const int64_t wfirst = (int64_t)k0w - diag;  // first query that sees any key of the wave
+
+  float kreg[D / 2], vreg[D / 2];
+  load_half_row<D>(kreg, K, a.ldk, ni, a.N, hi);
+  load_half_row<D>(vreg, V, a.ldv, ni, a.N, hi);
+  f32x16 dk[D / 32], dv[D / 32];
+#pragma unroll
+  for (int blk = 0; blk < D / 32; ++blk) dk[blk] = dv[blk] = f32x16{};
+  const float c = a.scale_log2;
+
+  Tiles pf;
+  float rl = INFINITY, rd = 0.0f;  // lse2 / D_m of row threadIdx.x (< kR)
+  auto fetch_rows = [&](uint32_t m0) {
+    if (threadIdx.x < (uint32_t)kR) {
+      const uint32_t m = m0 + threadIdx.x;
+      rl = m < a.M ? lse[m] * kLog2e : INFINITY;
+      rd = m < a.M ? dsum[m] : 0.0f;
+    }
+  };
+  auto stash_rows = [&](int st) {
+    if (threadIdx.x < (uint32_t)kR) {
+      rowv[st][0][threadIdx.x] = rl;
+      rowv[st][1][threadIdx.x] = rd;
+    }
+  };
+  if (nt > 0) {
+    pf.fetch(Q, a.ldq, dO, a.ldo, mbeg, a.M);
+    fetch_rows(mbeg);
+    pf.stash(lds[0][0], lds[0][1]);
+    stash_rows(0);
+  }
+  __syncthreads();
+  for (uint32_t t = 0; t < nt; ++t) {
+    const int st = (int)(t & 1);
+    const uint32_t m0 = mbeg + t * kR;
+    if (t + 1 < nt) {
+      pf.fetch(Q, a.ldq, dO, a.ldo, m0 + kR, a.M);
+      fetch_rows(m0 + kR);
+    }
+    if (!CAUSAL || (int64_t)m0 + kR - 1 >= wfirst) {
+      f32x16 s = dot_tile<D>(lds[st][0], kreg, li, hi);          // S [query][key]
+      const f32x16 dp = dot_tile<D>(lds[st][1], vreg, li, hi);   // dP = dO V^T
+      const bool edge = CAUSAL && (int64_t)m0 < wfirst + kR - 1;
+      f32x16 ds;
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int row = 8 * r4 + 4 * hi;
+        const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&rowv[st][0][row]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&rowv[st][1][row]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * r4 + e;
+          float p = __builtin_amdgcn_exp2f(s[r] * c - l4[e]);
+          if (edge && (int64_t)ni > (int64_t)(m0 + (uint32_t)(row + e)) + diag) p = 0.0f;
+          s[r] = p;
+          ds[r] = p * (dp[r] - d4[e]);
+        }
+      }
+      acc_tile_t<D>(dv, lds[st][1], s, li, hi);   // dV^T += dO^T P
+      acc_tile_t<D>(dk, lds[st][0], ds, li, hi);  // dK^T += Q^T dS
+    }
+    if (t + 1 < nt) {
+      pf.stash(lds[st ^ 1][0], lds[st ^ 1][1]);
+      stash_rows(st ^ 1);
+    }
+    __syncthreads();
+  }
+  if (ni < a.N) {
+    store_t<D>(dK, a.ldk, ni, dk, a.scale, hi);
+    store_t<D>(dV, a.ldv, ni, dv, 1.0f, hi);
+  }
+}
+
+}  // namespace
+
+#define BWPP_ATTN_F32(D, CAUSAL, SUFFIX)                                                                    \
+  extern "C" __global__ __launch_bounds__(64 * kW) void bwpp_attn_f32_mfma_d##D##SUFFIX(const BwppAttnArgs a) { \
+    attn_fwd<D, CAUSAL>(a);                                                                                 \
+  }                                                                                                         \
+  extern "C" __global__ __launch_bounds__(64 * kW) void bwpp_attn_bwd_f32_mfma_d##D##SUFFIX##_dq(           \
+      const BwppAttnArgs a) {                                                                               \
+    attn_bwd_dq<D, CAUSAL>(a);                                                                              \
+  }                                                                                                         \
+  extern "C" __global__ __launch_bounds__(64 * kW) void bwpp_attn_bwd_f32_mfma_d##D##SUFFIX##_dkdv(         \
+      const BwppAttnArgs a) {                                                                               \
+    attn_bwd_dkdv<D, CAUSAL>(a);                                                                            \
+  }
+
+BWPP_ATTN_F32(64, false, )
+BWPP_ATTN_F32(64, true, _causal)
+BWPP_ATTN_F32(128, false, )
+BWPP_ATTN_F32(128, true, _causal)

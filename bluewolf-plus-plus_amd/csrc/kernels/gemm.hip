@@ -44,9 +44,9 @@ namespace {
 
 constexpr uint32_t kEpiAdd = 1u, kEpiSilu = 2u;
 
-__device__ __forceinline__ void tile_coords(const BwppGemmArgs &a, uint32_t &tm, uint32_t &tn) {
+__device__ __forceinline__ void tile_coords(const BwppGemmArgs &a, uint32_t &tm, uint32_t &tn,
+                                            uint32_t b = blockIdx.x) {
   const uint32_t T = a.tiles_m * a.tiles_n;
-  uint32_t b = blockIdx.x;
   if ((T & 7u) == 0) b = (b & 7u) * (T >> 3) + (b >> 3);
   const uint32_t gm = a.group_m;
   const uint32_t per_group = gm * a.tiles_n;
@@ -668,7 +668,7 @@ struct StageF32 {
   static constexpr int kSize = MNC ? BK * (R + 32) : R * (BK + 2);
 };
 
-template <bool TA, bool TB, bool EDGE>
+template <bool TA, bool TB, bool EDGE, bool SPLIT = false>
 __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
   constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 2;
   constexpr int NT = 64 * WM * WN;
@@ -682,10 +682,21 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   uint32_t tm, tn;
-  tile_coords(a, tm, tn);
-  const uint32_t m0 = tm * BM, n0 = tn * BN;
   const float *A = static_cast<const float *>(a.a);
   const float *B = static_cast<const float *>(a.b);
+  uint32_t Klen = a.K, split = 0;
+  if constexpr (SPLIT) {
+    const uint32_t T = a.tiles_m * a.tiles_n;
+    split = blockIdx.x / T;
+    tile_coords(a, tm, tn, blockIdx.x - split * T);
+    const uint32_t kb = split * a.kchunk;
+    Klen = min(a.kchunk, a.K - kb);
+    A += TA ? (size_t)kb * a.lda : kb;
+    B += TB ? kb : (size_t)kb * a.ldb;
+  } else {
+    tile_coords(a, tm, tn);
+  }
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
   const bool vec = a.vec_ok != 0;
   SA sa;
   SB sb;
@@ -698,10 +709,10 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const uint32_t nk = (a.K + BK - 1) / BK;
+  const uint32_t nk = (Klen + BK - 1) / BK;
   if (nk > 0) {
-    sa.load(A, a.lda, m0, a.M, 0, a.K, vec, tid);
-    sb.load(B, a.ldb, n0, a.N, 0, a.K, vec, tid);
+    sa.load(A, a.lda, m0, a.M, 0, Klen, vec, tid);
+    sb.load(B, a.ldb, n0, a.N, 0, Klen, vec, tid);
     sa.store(smemf, tid);
     sb.store(smemf + SA::kSize, tid);
   }
@@ -710,8 +721,8 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
   const int lrow = lane & 31, lk = lane >> 5;
   for (uint32_t kt = 0; kt < nk; ++kt) {
     const uint32_t kn = (kt + 1 < nk ? kt + 1 : kt) * BK;
-    sa.load(A, a.lda, m0, a.M, kn, a.K, vec, tid);
-    sb.load(B, a.ldb, n0, a.N, kn, a.K, vec, tid);
+    sa.load(A, a.lda, m0, a.M, kn, Klen, vec, tid);
+    sb.load(B, a.ldb, n0, a.N, kn, Klen, vec, tid);
     const float *As = smemf + (kt & 1) * kBuf;
     const float *Bs = As + SA::kSize;
 #pragma unroll
@@ -737,9 +748,10 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
   // Epilogue through LDS as in the bf16 kernel: C tile [BM][BN + 4] fp32.
   constexpr int kCld = BN + 4;
   static_assert(BM * kCld <= 2 * kBuf, "epilogue tile must fit the operand buffers");
+  // Split-K blocks store raw sums; the reduce kernel applies the epilogue.
   const float *bias = static_cast<const float *>(a.bias);
-  const bool add = (a.epilogue & kEpiAdd) && bias;
-  const bool act = (a.epilogue & kEpiSilu) != 0;
+  const bool add = !SPLIT && (a.epilogue & kEpiAdd) && bias;
+  const bool act = !SPLIT && (a.epilogue & kEpiSilu) != 0;
   const int lhalf = lane >> 5;
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
@@ -762,7 +774,8 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
     }
   }
   __syncthreads();
-  float *C = static_cast<float *>(a.c);
+  float *C = SPLIT ? a.part + (size_t)split * a.M * a.N : static_cast<float *>(a.c);
+  const uint32_t ldc = SPLIT ? a.N : a.ldc;
   constexpr int kRowVecs = BN / 4;
 #pragma unroll 4
   for (int it = 0; it < BM * kRowVecs / NT; ++it) {
@@ -771,18 +784,56 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
     const uint32_t m = m0 + row, n = n0 + c * 4;
     const float4 v = *reinterpret_cast<const float4 *>(smemf + row * kCld + c * 4);
     if (!EDGE || (m < a.M && n + 4 <= a.N && vec)) {
-      *reinterpret_cast<float4 *>(C + (size_t)m * a.ldc + n) = v;
+      *reinterpret_cast<float4 *>(C + (size_t)m * ldc + n) = v;
     } else if (m < a.M) {
       const float *h = smemf + row * kCld + c * 4;
       for (int e = 0; e < 4; ++e)
-        if (n + e < a.N) C[(size_t)m * a.ldc + n + e] = h[e];
+        if (n + e < a.N) C[(size_t)m * ldc + n + e] = h[e];
     }
   }
 }
 
 }  // namespace
 
-// Entry points: bwpp_gemm_<bf16|f32>_t<TA><TB>_<f|e>  (f: no edges, aligned)
+// Split-K reduction: C[m][n..n+3] = epilogue(sum_s part[s][m][n..n+3]) in
+// split order, then bias and SiLU as the single-pass epilogue.  Needs N a
+// multiple of 4 and 16-byte aligned C rows (the full-tile conditions).
+extern "C" __global__ __launch_bounds__(256) void bwpp_gemm_f32_splitk_reduce(const BwppGemmArgs a) {
+  const uint32_t nv = a.N / 4;
+  const size_t total = (size_t)a.M * nv, plane = (size_t)a.M * a.N;
+  const float *bias = static_cast<const float *>(a.bias);
+  const bool add = (a.epilogue & kEpiAdd) && bias;
+  const bool act = (a.epilogue & kEpiSilu) != 0;
+  float *C = static_cast<float *>(a.c);
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+    const uint32_t m = (uint32_t)(i / nv), n = (uint32_t)(i % nv) * 4;
+    const float *p = a.part + (size_t)m * a.N + n;
+    float4 t = *reinterpret_cast<const float4 *>(p);
+    for (uint32_t s = 1; s < a.ksplit; ++s) {
+      const float4 u = *reinterpret_cast<const float4 *>(p + s * plane);
+      t.x += u.x;
+      t.y += u.y;
+      t.z += u.z;
+      t.w += u.w;
+    }
+    if (add) {
+      t.x += bias[n];
+      t.y += bias[n + 1];
+      t.z += bias[n + 2];
+      t.w += bias[n + 3];
+    }
+    if (act) {
+      t.x = silu(t.x);
+      t.y = silu(t.y);
+      t.z = silu(t.z);
+      t.w = silu(t.w);
+    }
+    *reinterpret_cast<float4 *>(C + (size_t)m * a.ldc + n) = t;
+  }
+}
+
+// Entry points: bwpp_gemm_<bf16|f32>_t<TA><TB>_<f|e|s>  (f: no edges,
+// aligned; s: f with split-K partials)
 #define BWPP_GEMM_BF16(TA, TB, EDGE, SUF)                                                  \
   extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(256, 256),            \
                                        amdgpu_waves_per_eu(1, 1))) void                  \
@@ -820,3 +871,12 @@ BWPP_GEMM_BF16_W8(0, 1)
 BWPP_GEMM_BF16_W8(1, 0)
 BWPP_GEMM_BF16_W8(1, 1)
 BWPP_GEMM_ALL(BWPP_GEMM_F32)
+#define BWPP_GEMM_F32_SPLIT(TA, TB)                                                        \
+  extern "C" __global__ __launch_bounds__(256) void bwpp_gemm_f32_t##TA##TB##_s(         \
+      const BwppGemmArgs a) {                                                             \
+    gemm_f32<TA, TB, false, true>(a);                                                     \
+  }
+BWPP_GEMM_F32_SPLIT(0, 0)
+BWPP_GEMM_F32_SPLIT(0, 1)
+BWPP_GEMM_F32_SPLIT(1, 0)
+BWPP_GEMM_F32_SPLIT(1, 1)

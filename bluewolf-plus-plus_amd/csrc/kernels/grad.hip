@@ -111,17 +111,32 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_rmsnorm_grad(const BwppGr
 }
 
 // out[c] = sum_p part[p][c] for the two partial arrays (dgamma, dbeta); the
-// outputs may be NULL.
+// outputs may be NULL.  A block owns 16 columns: thread (g, c) of 16 x 16
+// sums parts g, g + 16, ... of column c (16 consecutive columns = 64-byte
+// rows per part), then the 16 partial sums of each column are added in LDS
+// in a fixed order.
 extern "C" __global__ __launch_bounds__(256) void bwpp_col_partials_sum(const BwppGradArgs g) {
-  const uint32_t c = blockIdx.x * 256u + threadIdx.x;
-  if (c >= g.cols) return;
+  __shared__ float red[2][16][17];
+  const uint32_t cl = threadIdx.x & 15u, grp = threadIdx.x >> 4;
+  const uint32_t c = blockIdx.x * 16u + cl;
   float sg = 0.0f, sb = 0.0f;
-  for (uint32_t p = 0; p < g.nparts; ++p) {
-    sg += g.part_g[(size_t)p * g.cols + c];
-    sb += g.part_b[(size_t)p * g.cols + c];
+  if (c < g.cols) {
+    for (uint32_t p = grp; p < g.nparts; p += 16) {
+      sg += g.part_g[(size_t)p * g.cols + c];
+      sb += g.part_b[(size_t)p * g.cols + c];
+    }
   }
-  if (g.out) g.out[c] = sg;
-  if (g.out2) g.out2[c] = sb;
+  red[0][grp][cl] = sg;
+  red[1][grp][cl] = sb;
+  __syncthreads();
+  if (threadIdx.x < 32) {
+    const uint32_t which = threadIdx.x >> 4, col = blockIdx.x * 16u + cl;
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t += red[which][i][cl];
+    float *out = which ? g.out2 : g.out;
+    if (col < g.cols && out) out[col] = t;
+  }
 }
 
 // reduce_sum along each row (axis 1): one block per row.

@@ -14,11 +14,13 @@
 
 #include <dlfcn.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cmath>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 #include <vector>
 
@@ -29,7 +31,8 @@ namespace {
 thread_local std::string g_create_error;
 
 // Code objects built by the package Makefile, all required.
-const char *const kModules[] = {"bwpp_rowops.hsaco", "bwpp_gemm.hsaco", "bwpp_attention.hsaco", "bwpp_grad.hsaco"};
+const char *const kModules[] = {"bwpp_rowops.hsaco", "bwpp_gemm.hsaco", "bwpp_attention.hsaco",
+                                 "bwpp_attention_f32.hsaco", "bwpp_grad.hsaco"};
 
 // Row-op kernels: bwpp_row_<op>_v<VPT>_w<WPR>_<f|p>, see rowops.hip.
 enum RowOpId { ROW_SOFTMAX, ROW_RMSNORM, ROW_LAYERNORM, ROW_MAX, ROW_MAXGRAD, ROW_MASK, ROW_NOPS };
@@ -74,10 +77,14 @@ struct BwppHip {
   // bwpp_gemm_<bf16|f32>_t<TA><TB>_<e|f>: [dtype][ta][tb][full]
   hipFunction_t gemm[2][2][2][2] = {};
   hipFunction_t gemm_bf16_w8[2][2] = {};  // 8-wave full-tile bf16: [ta][tb]
+  hipFunction_t gemm_f32_split[2][2] = {};  // fp32 full tiles, split-K partials: [ta][tb]
+  hipFunction_t gemm_f32_reduce = nullptr;
   hipFunction_t attn_flash[2] = {};       // bf16, d = 128: [causal]
   hipFunction_t attn_generic[2][2] = {};  // [bf16][causal]
   hipFunction_t attn_bwd_dq[2][2] = {};   // [bf16][causal]
   hipFunction_t attn_bwd_dkdv[2][2] = {};
+  // fp32 MFMA attention, head dim 64 / 128: [d128][causal]
+  hipFunction_t attn_f32_fwd[2][2] = {}, attn_f32_dq[2][2] = {}, attn_f32_dkdv[2][2] = {};
   hipFunction_t silu_grad = nullptr, softmax_grad = nullptr, rmsnorm_grad = nullptr, col_partials_sum = nullptr,
                 reduce_sum_rows = nullptr, reduce_sum_cols = nullptr, elementwise = nullptr;
   // Library-owned device workspace (column partials), grown on demand and
@@ -87,6 +94,7 @@ struct BwppHip {
   size_t ws_bytes = 0;
   uint32_t gemm_group_m = 8;  // BWPP_GEMM_GROUP_M
   uint32_t gemm_waves = 8;    // BWPP_GEMM_WAVES: 4 or 8 waves for full bf16 tiles
+  uint32_t gemm_splitk = 1;   // BWPP_GEMM_SPLITK=0 turns fp32 split-K off
 };
 
 namespace {
@@ -142,7 +150,7 @@ BwppHipStatus resolve_all(BwppHip *h) {
       {"bwpp_silu_grad", &h->silu_grad},             {"bwpp_softmax_grad", &h->softmax_grad},
       {"bwpp_rmsnorm_grad", &h->rmsnorm_grad},       {"bwpp_col_partials_sum", &h->col_partials_sum},
       {"bwpp_reduce_sum_rows", &h->reduce_sum_rows}, {"bwpp_reduce_sum_cols", &h->reduce_sum_cols},
-      {"bwpp_elementwise", &h->elementwise},
+      {"bwpp_elementwise", &h->elementwise},         {"bwpp_gemm_f32_splitk_reduce", &h->gemm_f32_reduce},
   };
   for (auto &e : singles)
     if ((s = resolve(h, e.name, e.slot)) != BWPP_HIP_OK) return s;
@@ -158,6 +166,8 @@ BwppHipStatus resolve_all(BwppHip *h) {
     for (int tb = 0; tb < 2; ++tb) {
       const std::string n = "bwpp_gemm_bf16w8_t" + std::to_string(ta) + std::to_string(tb) + "_f";
       if ((s = resolve(h, n, &h->gemm_bf16_w8[ta][tb])) != BWPP_HIP_OK) return s;
+      const std::string ns = std::string("bwpp_gemm_f32_t") + char('0' + ta) + char('0' + tb) + "_s";
+      if ((s = resolve(h, ns, &h->gemm_f32_split[ta][tb])) != BWPP_HIP_OK) return s;
     }
   for (int causal = 0; causal < 2; ++causal) {
     const char *cs = causal ? "_causal" : "";
@@ -166,6 +176,15 @@ BwppHipStatus resolve_all(BwppHip *h) {
       return s;
     if ((s = resolve(h, std::string("bwpp_attn_generic_bf16") + cs, &h->attn_generic[1][causal])) != BWPP_HIP_OK)
       return s;
+    for (int d128 = 0; d128 < 2; ++d128) {
+      const std::string dn = std::string(d128 ? "128" : "64") + cs;
+      if ((s = resolve(h, "bwpp_attn_f32_mfma_d" + dn, &h->attn_f32_fwd[d128][causal])) != BWPP_HIP_OK) return s;
+      if ((s = resolve(h, "bwpp_attn_bwd_f32_mfma_d" + dn + "_dq", &h->attn_f32_dq[d128][causal])) != BWPP_HIP_OK)
+        return s;
+      if ((s = resolve(h, "bwpp_attn_bwd_f32_mfma_d" + dn + "_dkdv", &h->attn_f32_dkdv[d128][causal])) !=
+          BWPP_HIP_OK)
+        return s;
+    }
     for (int bf = 0; bf < 2; ++bf) {
       const std::string base = std::string("bwpp_attn_bwd_") + (bf ? "bf16" : "f32") + cs;
       if ((s = resolve(h, base + "_dq", &h->attn_bwd_dq[bf][causal])) != BWPP_HIP_OK) return s;
@@ -289,6 +308,7 @@ BwppHipStatus bwpp_hip_create(BwppHip **out, int device, const char *code_object
   if (const char *cfg = getenv("BWPP_ROW_CFG")) h->row_cfg_override = atoi(cfg);
   if (const char *gc = getenv("BWPP_ROW_GRID")) h->row_grid_cap = (uint32_t)strtoul(gc, nullptr, 10);
   if (const char *gw = getenv("BWPP_GEMM_WAVES")) h->gemm_waves = (uint32_t)strtoul(gw, nullptr, 10) == 4 ? 4 : 8;
+  if (const char *sk = getenv("BWPP_GEMM_SPLITK")) h->gemm_splitk = atoi(sk) != 0 ? 1u : 0u;
   if (const char *gm = getenv("BWPP_GEMM_GROUP_M")) {
     const uint32_t v = (uint32_t)strtoul(gm, nullptr, 10);
     if (v > 0) h->gemm_group_m = v;
@@ -568,6 +588,8 @@ Extent extent(const void *p, uint64_t rows, uint64_t cols, uint64_t ld, uint64_t
 }
 bool overlaps(const Extent &a, const Extent &b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; }
 
+BwppHipStatus ensure_ws(BwppHip *h, size_t bytes);
+
 }  // namespace
 
 extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, const void *b, void *c,
@@ -624,6 +646,27 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
   if (tiles > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "matmul: too many tiles");
   if (bf16 && full && h->gemm_waves == 8)
     return launch(h, h->gemm_bf16_w8[ta][tb], (uint32_t)tiles, 1, 1, 512, g);
+  // fp32 full tiles that leave the chip under-filled (fewer tiles than the
+  // two 128 x 128 blocks each CU holds) and have a long K: split K into S
+  // ranges of at least 512 (multiples of BK), raw partial tiles into the
+  // workspace, then one reduce pass adds them in order and applies the
+  // epilogue.
+  if (!bf16 && full && h->gemm_splitk && h->cus > 0 && p.K >= 1024) {
+    const uint64_t slots = 2ull * (uint64_t)h->cus;
+    uint64_t S = tiles < slots ? std::min<uint64_t>((slots + tiles - 1) / tiles, p.K / 512) : 1;
+    if (S > 1) {
+      const uint32_t kchunk = (uint32_t)(((p.K + S - 1) / S + BK - 1) / BK * BK);
+      S = (p.K + kchunk - 1) / kchunk;
+      if ((s = ensure_ws(h, (size_t)S * p.M * p.N * sizeof(float))) != BWPP_HIP_OK) return s;
+      g.ksplit = (uint32_t)S;
+      g.kchunk = kchunk;
+      g.part = static_cast<float *>(h->ws);
+      if ((s = launch(h, h->gemm_f32_split[ta][tb], (uint32_t)(tiles * S), 1, 1, 256, g)) != BWPP_HIP_OK) return s;
+      const uint64_t vecs = (uint64_t)p.M * (p.N / 4);
+      const uint64_t grid = std::min<uint64_t>((vecs + 255) / 256, 8ull * (uint64_t)h->cus);
+      return launch(h, h->gemm_f32_reduce, (uint32_t)grid, 1, 1, 256, g);
+    }
+  }
   return launch(h, h->gemm[bf16 ? 1 : 0][ta][tb][full ? 1 : 0], (uint32_t)tiles, 1, 1, 256, g);
 }
 
@@ -697,6 +740,23 @@ BwppHipStatus attn_prepare(BwppHip *h, const void *q, const void *k, const void 
   return BWPP_HIP_OK;
 }
 
+// Variant of the fp32 MFMA attention kernels for these arguments (0: head
+// dim 64, 1: 128), or -1 for the generic path: they need K = D in {64, 128},
+// a finite scale and 16-byte rows (pointers, leading dims and slice strides
+// in multiples of 4 floats).
+int attn_f32_variant(const BwppAttentionParams &p, const BwppAttnArgs &g, float scale,
+                     std::initializer_list<const void *> ptrs) {
+  if (p.dtype != BWPP_HIP_F32 || p.K != p.D || (p.K != 64 && p.K != 128) || !std::isfinite(scale)) return -1;
+  for (const void *x : ptrs)
+    if (!aligned16(x)) return -1;
+  for (uint64_t v : {(uint64_t)g.ldq, (uint64_t)g.ldk, (uint64_t)g.ldv, (uint64_t)g.ldo, g.q_bs, g.q_hs, g.k_bs,
+                     g.k_hs, g.v_bs, g.v_hs, g.o_bs, g.o_hs})
+    if (v % 4 != 0) return -1;
+  return p.K == 128 ? 1 : 0;
+}
+
+constexpr uint32_t kF32Rows = 64;  // queries (keys) per block of the fp32 MFMA kernels: 2 waves x 32
+
 BwppHipStatus attn_forward(BwppHip *h, const void *q, const void *k, const void *v, void *o, float *lse,
                            const BwppAttentionParams &p) {
   BwppHipStatus s = enter(h);
@@ -725,6 +785,16 @@ BwppHipStatus attn_forward(BwppHip *h, const void *q, const void *k, const void 
     const uint64_t grid = slices * g.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: grid too large");
     return launch(h, h->attn_flash[causal], (uint32_t)grid, 1, 1, 512, g);
+  }
+  const int f32v = attn_f32_variant(p, g, scale, {q, k, v, o});
+  if (f32v >= 0) {
+    g.scale = scale;
+    g.scale_log2 = scale * 1.4426950408889634f;
+    g.lse = lse;
+    g.q_tiles = (p.M + kF32Rows - 1) / kF32Rows;
+    const uint64_t grid = slices * g.q_tiles;
+    if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: grid too large");
+    return launch(h, h->attn_f32_fwd[f32v][causal], (uint32_t)grid, 1, 1, 2 * 64, g);
   }
   g.scale_log2 = scale;
   g.lse = lse;
@@ -802,13 +872,30 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   }
   if ((s = ensure_ws(h, (size_t)slices * p.M * sizeof(float) + 4)) != BWPP_HIP_OK) return s;
   const int bf = p.dtype == BWPP_HIP_BF16 ? 1 : 0, causal = p.causal ? 1 : 0;
-  g.scale_log2 = p.scale != 0.0f ? p.scale : 1.0f;
+  const float scale = p.scale != 0.0f ? p.scale : 1.0f;
+  g.scale_log2 = scale;
   g.lse = const_cast<float *>(lse);
   g.dout = dout;
   g.dq = dq;
   g.dk = dk;
   g.dv = dv;
   g.dsum = static_cast<float *>(h->ws);
+  const int f32v = attn_f32_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
+  if (f32v >= 0) {
+    // dQ pass (also writes D_m = rowsum(dO * O)), then the dK / dV pass.
+    g.scale = scale;
+    g.scale_log2 = scale * 1.4426950408889634f;
+    g.q_tiles = (p.M + kF32Rows - 1) / kF32Rows;
+    uint64_t grid = slices * g.q_tiles;
+    if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
+    if (p.M > 0 && (s = launch(h, h->attn_f32_dq[f32v][causal], (uint32_t)grid, 1, 1, 2 * 64, g)) != BWPP_HIP_OK)
+      return s;
+    g.q_tiles = (p.N + kF32Rows - 1) / kF32Rows;  // key tiles
+    grid = slices * g.q_tiles;
+    if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
+    if (p.N > 0) return launch(h, h->attn_f32_dkdv[f32v][causal], (uint32_t)grid, 1, 1, 2 * 64, g);
+    return BWPP_HIP_OK;
+  }
   if (p.M > 0) {
     g.q_tiles = (p.M + 15) / 16;
     const uint64_t grid = slices * g.q_tiles;
@@ -914,7 +1001,11 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad(BwppHip *h, const float 
   g.cols = p.cols;
   g.ld = ld;
   g.eps = p.eps;
-  const uint32_t grid = p.rows == 0 ? 1u : row_grid(h, p.rows);
+  // With column partials, at most kMaxParts blocks (each loops over its
+  // rows), which bounds the partial arrays to kMaxParts rows.
+  constexpr uint32_t kMaxParts = 512;
+  uint32_t grid = p.rows == 0 ? 1u : row_grid(h, p.rows);
+  if (parts && grid > kMaxParts) grid = kMaxParts;
   if (parts) {
     if ((s = ensure_ws(h, (size_t)2 * grid * p.cols * sizeof(float))) != BWPP_HIP_OK) return s;
     g.part_g = static_cast<float *>(h->ws);
@@ -932,7 +1023,7 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad(BwppHip *h, const float 
   r.out2 = dbeta;
   r.cols = p.cols;
   r.nparts = grid;
-  return launch(h, h->col_partials_sum, (p.cols + 255) / 256, 1, 1, 256, r);
+  return launch(h, h->col_partials_sum, (p.cols + 15) / 16, 1, 1, 256, r);
 }
 
 extern "C" BwppHipStatus bwpp_hip_dispatch_reduce_sum(BwppHip *h, const float *x, float *out, BwppReduceParams p) {
@@ -962,7 +1053,7 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_reduce_sum(BwppHip *h, const float *x
   r.out = out;
   r.cols = p.cols;
   r.nparts = bands;
-  return launch(h, h->col_partials_sum, (p.cols + 255) / 256, 1, 1, 256, r);
+  return launch(h, h->col_partials_sum, (p.cols + 15) / 16, 1, 1, 256, r);
 }
 
 extern "C" BwppHipStatus bwpp_hip_dispatch_elementwise(BwppHip *h, const float *a, const float *b, float *out,

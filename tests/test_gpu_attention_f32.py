@@ -1,0 +1,163 @@
+"""GPU parity of the fp32 matrix-core attention kernels (head dims 64 and
+128: forward with lse, dQ and dK/dV passes) against the oracle.  fp32 bar:
+1e-4 relative max-norm; lse 1e-4 absolute relative to max(1, |lse|).
+
+Shapes cover partial 32-row tiles on both sides, M > N (causal rows that
+see no key: O = 0, lse = -inf, dQ = 0), M < N, several slices, packed
+projections read through strides (the layout of config 5's qkv buffer),
+negative scales and the full config-5 shape (checked on two slices).
+A head dim or layout the kernels do not take runs the generic kernel,
+checked here too (d = 64 with a leading dimension that breaks 16-byte
+rows)."""
+import numpy as np
+import pytest
+
+import bwpp
+from bwpp import synth
+from conftest import rel_max_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def dev(x):
+    return _torch().from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+
+
+def host(t):
+    _torch().cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def _check_lse(got, want):
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isfinite(got), fin)
+    assert np.array_equal(got[~fin], want[~fin])
+    err = np.max(np.abs(got[fin] - want[fin]), initial=0.0)
+    assert err <= TOL * max(1.0, np.abs(want[fin]).max(initial=0.0))
+
+
+def _run_all(be, q, k, v, dout, scale, causal, prm):
+    torch = _torch()
+    B, H, M = q.shape[:3]
+    D = v.shape[3]
+    qd, kd, vd, dod = dev(q), dev(k), dev(v), dev(dout)
+    o = torch.full((B, H, M, D), 5.0, device="cuda")
+    lse = torch.full((B, H, M), 5.0, device="cuda")
+    be.dispatch_attention_lse(qd, kd, vd, o, lse, prm)
+    o2 = torch.full((B, H, M, D), 5.0, device="cuda")
+    be.dispatch_attention(qd, kd, vd, o2, prm)
+    dq, dk, dv = (torch.full_like(t, 7.0) for t in (qd, kd, vd))
+    be.dispatch_attention_grad(qd, kd, vd, o, dod, lse, dq, dk, dv, prm)
+    return host(o), host(o2), host(lse), host(dq), host(dk), host(dv)
+
+
+@pytest.mark.parametrize("B,H,M,N,D", [
+    (1, 1, 1, 1, 64), (1, 1, 31, 33, 64), (2, 3, 64, 64, 64), (1, 2, 97, 200, 64), (1, 1, 200, 97, 64),
+    (1, 1, 130, 130, 128), (2, 1, 65, 190, 128), (1, 1, 190, 65, 128)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_mfma_f32_fwd_bwd(be, oracle, B, H, M, N, D, causal):
+    seed = B * 1000 + M * 7 + N
+    q = synth.normal((B, H, M, D), seed, 0)
+    k = synth.normal((B, H, N, D), seed, 1)
+    v = synth.normal((B, H, N, D), seed, 2)
+    dout = synth.normal((B, H, M, D), seed, 3)
+    scale = 1.0 / np.sqrt(D)
+    prm = bwpp.AttentionParams(M=M, N=N, K=D, D=D, ldq=D, ldk=D, ldv=D, ldo=D, batch=B, heads=H,
+                               scale=scale, causal=int(causal), dtype=int(bwpp.DType.F32))
+    o, o2, lse, dq, dk, dv = _run_all(be, q, k, v, dout, scale, causal, prm)
+    want = oracle.attention_bh(q, k, v, scale, causal)
+    assert rel_max_err(o, want) <= TOL
+    assert rel_max_err(o2, want) <= TOL
+    _check_lse(lse, oracle.attention_lse(q, k, scale, causal))
+    wq, wk, wv = oracle.attention_grad(q, k, v, dout, scale, causal)
+    assert rel_max_err(dq, wq) <= TOL
+    assert rel_max_err(dk, wk) <= TOL
+    assert rel_max_err(dv, wv) <= TOL
+    if causal and M > N:  # rows that see no key
+        assert np.all(o[:, :, :M - N] == 0.0) and np.all(dq[:, :, :M - N] == 0.0)
+
+
+@pytest.mark.parametrize("scale", [-0.3, 2.0])
+def test_mfma_f32_scales(be, oracle, scale):
+    B, H, M, N, D = 1, 2, 100, 140, 64
+    q = synth.normal((B, H, M, D), 5, 0)
+    k = synth.normal((B, H, N, D), 5, 1)
+    v = synth.normal((B, H, N, D), 5, 2)
+    dout = synth.normal((B, H, M, D), 5, 3)
+    prm = bwpp.AttentionParams(M=M, N=N, K=D, D=D, ldq=D, ldk=D, ldv=D, ldo=D, batch=B, heads=H,
+                               scale=scale, causal=1, dtype=int(bwpp.DType.F32))
+    o, _, lse, dq, dk, dv = _run_all(be, q, k, v, dout, scale, True, prm)
+    assert rel_max_err(o, oracle.attention_bh(q, k, v, scale, True)) <= TOL
+    _check_lse(lse, oracle.attention_lse(q, k, scale, True))
+    for got, want in zip((dq, dk, dv), oracle.attention_grad(q, k, v, dout, scale, True)):
+        assert rel_max_err(got, want) <= TOL
+
+
+def _packed(B, T, H, dh, seed):
+    """qkv [B*T, 3*H*dh] and dout [B*T, H*dh] as config 5 lays them out."""
+    D = H * dh
+    qkv = synth.normal((B * T, 3 * D), seed, 0)
+    dout = synth.normal((B * T, D), seed, 1)
+    return qkv, dout
+
+
+def _unpack(qkv, B, T, H, dh, part):
+    D = H * dh
+    x = qkv[:, part * D:(part + 1) * D].reshape(B, T, H, dh)
+    return np.ascontiguousarray(x.transpose(0, 2, 1, 3))
+
+
+@pytest.mark.parametrize("B,T,H,dh,ld_pad,check", [(2, 96, 3, 64, 0, None), (8, 512, 16, 64, 0, [(0, 0), (7, 15)]),
+                                                   (1, 70, 2, 64, 1, None)])
+def test_packed_views(be, oracle, B, T, H, dh, ld_pad, check):
+    """Q, K, V as column blocks of one [B*T, 3*H*dh] buffer (head stride dh,
+    batch stride T*ld), O / dO as [B*T, H*dh]; causal, scale 1/8.  ld_pad = 1
+    makes rows 4-byte aligned only, so the generic kernel runs."""
+    torch = _torch()
+    D = H * dh
+    qkv, dout = _packed(B, T, H, dh, B * T + H)
+    ld = 3 * D + ld_pad
+    buf = np.zeros((B * T, ld), np.float32)
+    buf[:, :3 * D] = qkv
+    dbuf = dev(buf)
+    flat = dbuf.view(-1)
+    qd, kd, vd = flat[0:], flat[D:], flat[2 * D:]
+    ldo = D + ld_pad
+    obuf = np.zeros((B * T, ldo), np.float32)
+    obuf[:, :D] = dout
+    dod = dev(obuf)
+    o = torch.zeros((B * T, ldo), device="cuda")
+    lse = torch.zeros((B, H, T), device="cuda")
+    scale = 0.125
+    prm = bwpp.AttentionParams(M=T, N=T, K=dh, D=dh, ldq=ld, ldk=ld, ldv=ld, ldo=ldo, batch=B, heads=H,
+                               q_batch_stride=T * ld, q_head_stride=dh, k_batch_stride=T * ld, k_head_stride=dh,
+                               v_batch_stride=T * ld, v_head_stride=dh, o_batch_stride=T * ldo, o_head_stride=dh,
+                               scale=scale, causal=1, dtype=int(bwpp.DType.F32))
+    be.dispatch_attention_lse(qd, kd, vd, o, lse, prm)
+    # dQ / dK / dV take the strides of Q / K / V, each in a buffer of its own
+    # (the public entry point rejects outputs whose byte ranges interleave).
+    gbufs = [torch.zeros((B * T, ld), device="cuda") for _ in range(3)]
+    be.dispatch_attention_grad(qd, kd, vd, o, dod, lse, *(gb.view(-1)[i * D:] for i, gb in enumerate(gbufs)), prm)
+    q, k, v = (_unpack(qkv, B, T, H, dh, i) for i in range(3))
+    g = np.ascontiguousarray(dout.reshape(B, T, H, dh).transpose(0, 2, 1, 3))
+    oh = host(o)[:, :D].reshape(B, T, H, dh).transpose(0, 2, 1, 3)
+    gq, gk, gv = (_unpack(host(gb), B, T, H, dh, i) for i, gb in enumerate(gbufs))
+    for i, gb in enumerate(host(gb) for gb in gbufs):  # outside its column block: untouched
+        rest = np.delete(gb, np.s_[i * D:(i + 1) * D], axis=1)
+        assert np.all(rest == 0.0)
+    lh = host(lse)
+    for (b, h) in (check or [(b, h) for b in range(B) for h in range(H)]):
+        sl = lambda t: t[b:b + 1, h:h + 1]
+        assert rel_max_err(oh[b, h], oracle.attention_bh(sl(q), sl(k), sl(v), scale, True)[0, 0]) <= TOL
+        _check_lse(lh[b, h], oracle.attention_lse(sl(q), sl(k), scale, True)[0, 0])
+        wq, wk, wv = oracle.attention_grad(sl(q), sl(k), sl(v), sl(g), scale, True)
+        assert rel_max_err(gq[b, h], wq[0, 0]) <= TOL
+        assert rel_max_err(gk[b, h], wk[0, 0]) <= TOL
+        assert rel_max_err(gv[b, h], wv[0, 0]) <= TOL

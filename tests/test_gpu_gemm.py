@@ -223,3 +223,35 @@ def test_full_tile_kernels(oracle, monkeypatch, ta, tb, waves):
         assert rel_max_err(bf16_host(c), want) <= BF16_TOL
     finally:
         be.close()
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb", [(128, 128, 4096, 1, 0), (256, 384, 2048, 0, 0), (128, 256, 4000, 0, 1),
+                                         (384, 128, 1056, 1, 1), (1024, 1024, 4096, 1, 0)])
+@pytest.mark.parametrize("epi,silu,add", [(0, False, False), (3, True, True)])
+def test_f32_split_k(be, oracle, M, N, K, ta, tb, epi, silu, add):
+    """fp32 full tiles with fewer tiles than the chip holds and K >= 1024 run
+    split-K (partial tiles, then an in-order reduce with the epilogue);
+    K = 4000 and 1056 leave a shorter last range.  The same GEMM with
+    split-K turned off must agree to the fp32 bar as well."""
+    a = synth.uniform((M, K), M + K, 0, -1, 1)
+    b = synth.uniform((K, N), M + K, 1, -1, 1)
+    bias = synth.uniform((N,), M + K, 2, -1, 1)
+    ad, bd = f32_dev(stored(a, ta)), f32_dev(stored(b, tb))
+    c = run(be, bwpp.DType.F32, ad, bd, f32_dev(bias), M, N, K, epi, ta, tb)
+    want = oracle.matmul(a, b, bias, apply_silu=silu, apply_bias=add)
+    assert rel_max_err(f32_host(c), want) <= F32_TOL
+
+
+def test_f32_split_k_off_matches(oracle, monkeypatch):
+    torch = _torch()
+    monkeypatch.setenv("BWPP_GEMM_SPLITK", "0")
+    be = bwpp.HipBackend(0)
+    be.set_stream(torch.cuda.current_stream())
+    try:
+        M, N, K = 256, 128, 2048
+        a = synth.uniform((M, K), 3, 0, -1, 1)
+        b = synth.uniform((K, N), 3, 1, -1, 1)
+        c = run(be, bwpp.DType.F32, f32_dev(a), f32_dev(b), None, M, N, K, 0)
+        assert rel_max_err(f32_host(c), oracle.matmul(a, b)) <= F32_TOL
+    finally:
+        be.close()
