@@ -111,6 +111,7 @@ struct BwppHipPlan {
   size_t arena_bytes = 0;
   BwppHipArena arena{};
   bool allocated = false;
+  bool check_only = false;  // run_op validates arguments and launches nothing
   std::string err;
 };
 
@@ -381,6 +382,10 @@ BwppHipStatus plan_memory(BwppHipPlan &p) {
 
 }  // namespace
 
+namespace {
+BwppHipStatus run_op(BwppHipPlan &p, const Op &op);
+}  // namespace
+
 extern "C" BwppHipStatus bwpp_hip_plan_create(BwppHip *h, const char *text, BwppHipPlan **out) {
   if (!out) return BWPP_HIP_ERR_INVALID_ARG;
   *out = nullptr;
@@ -389,6 +394,10 @@ extern "C" BwppHipStatus bwpp_hip_plan_create(BwppHip *h, const char *text, Bwpp
   p->h = h;
   BwppHipStatus s = parse(*p, text);
   if (s == BWPP_HIP_OK) s = plan_memory(*p);
+  // Every op checks its arguments once here, so a bad plan fails at creation.
+  p->check_only = true;
+  for (size_t i = 0; s == BWPP_HIP_OK && i < p->ops.size(); ++i) s = run_op(*p, p->ops[i]);
+  p->check_only = false;
   *out = p;  // returned even on failure so that the caller can read the error
   return s;
 }
@@ -457,6 +466,10 @@ std::string attr(const Op &op, const char *k, const char *dflt) {
   return it == op.attrs.end() ? std::string(dflt) : it->second;
 }
 
+// In check-only mode (plan creation) each op validates its arguments and
+// shapes and launches nothing.
+#define BWPP_PLAN_CALL(expr) (p.check_only ? BWPP_HIP_OK : (expr))
+
 BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
   BwppHip *h = p.h;
   auto val = [&](int i) -> const Value & { return p.values[i]; };
@@ -486,25 +499,27 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
     if ((ta ? A.cols() : A.rows()) != M || (tb ? B.cols() : B.rows()) != K || (tb ? B.rows() : B.cols()) != N)
       return bad("operand shapes do not match");
     const std::string e = attr(op, "epi", "none");
+    if (e != "none" && e != "add" && e != "silu" && e != "add_silu")
+      return bad("epi must be none, add, silu or add_silu");
     uint32_t epi = e == "add" ? BWPP_HIP_EPILOGUE_ADD : e == "silu" ? BWPP_HIP_EPILOGUE_SILU
                    : e == "add_silu" ? BWPP_HIP_EPILOGUE_ADD_SILU : BWPP_HIP_EPILOGUE_NONE;
     BwppMatmulParams mp = {(uint32_t)M, (uint32_t)N, (uint32_t)K, (uint32_t)A.row_stride(), (uint32_t)B.row_stride(),
                            (uint32_t)C.row_stride(), C.dtype, epi, ta, tb};
-    s = bwpp_hip_dispatch_matmul(h, ptr(op.ins[0]), ptr(op.ins[1]), ptr(op.outs[0]),
-                                 op.ins.size() > 2 ? ptr(op.ins[2]) : nullptr, mp);
+    s = BWPP_PLAN_CALL(bwpp_hip_dispatch_matmul(h, ptr(op.ins[0]), ptr(op.ins[1]), ptr(op.outs[0]),
+                                 op.ins.size() > 2 ? ptr(op.ins[2]) : nullptr, mp));
   } else if (k == "softmax" || k == "rmsnorm" || k == "layernorm") {
     if (!need(1, 1)) return bad("in=X[,gamma[,beta]] out=Y");
     const Value &X = val(op.ins[0]);
     const float eps = (float)num("eps", 1e-5);
     if (k == "softmax") {
       BwppSoftmaxParams sp = {(uint32_t)X.rows(), (uint32_t)X.cols(), (uint32_t)X.row_stride()};
-      s = bwpp_hip_dispatch_softmax(h, f32(op.ins[0]), f32(op.outs[0]), sp);
+      s = BWPP_PLAN_CALL(bwpp_hip_dispatch_softmax(h, f32(op.ins[0]), f32(op.outs[0]), sp));
     } else {
       BwppRmsnormParams rp = {(uint32_t)X.rows(), (uint32_t)X.cols(), (uint32_t)X.row_stride(), eps};
       const float *g = op.ins.size() > 1 ? f32(op.ins[1]) : nullptr;
       const float *bt = op.ins.size() > 2 ? f32(op.ins[2]) : nullptr;
-      s = k == "rmsnorm" ? bwpp_hip_dispatch_rmsnorm(h, f32(op.ins[0]), g, bt, f32(op.outs[0]), rp)
-                         : bwpp_hip_dispatch_layernorm(h, f32(op.ins[0]), g, bt, f32(op.outs[0]), rp);
+      s = BWPP_PLAN_CALL(k == "rmsnorm" ? bwpp_hip_dispatch_rmsnorm(h, f32(op.ins[0]), g, bt, f32(op.outs[0]), rp)
+                         : bwpp_hip_dispatch_layernorm(h, f32(op.ins[0]), g, bt, f32(op.outs[0]), rp));
     }
   } else if (k == "add" || k == "sub" || k == "mul" || k == "div" || k == "copy" || k == "silu") {
     const bool unary = k == "copy" || k == "silu";
@@ -512,6 +527,8 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
     const Value &C = val(op.outs[0]);
     const int bi = op.ins[unary ? 0 : 1];
     const std::string bm = attr(op, "bcast", "full");
+    if (bm != "full" && bm != "row" && bm != "col" && bm != "scalar")
+      return bad("bcast must be full, row, col or scalar");
     const uint32_t bmode = bm == "row" ? BWPP_HIP_BCAST_ROW : bm == "col" ? BWPP_HIP_BCAST_COL
                            : bm == "scalar" ? BWPP_HIP_BCAST_SCALAR : BWPP_HIP_BCAST_FULL;
     const uint32_t opc = k == "add" ? BWPP_HIP_OP_ADD : k == "sub" ? BWPP_HIP_OP_SUB : k == "mul" ? BWPP_HIP_OP_MUL
@@ -519,28 +536,30 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
     if (bmode == BWPP_HIP_BCAST_FULL && val(bi).row_stride() != C.row_stride()) return bad("full b needs C's stride");
     if (!unary && val(op.ins[0]).row_stride() != C.row_stride()) return bad("a needs C's stride");
     BwppElementwiseParams ep = {(uint32_t)C.rows(), (uint32_t)C.cols(), (uint32_t)C.row_stride(), opc, bmode};
-    s = bwpp_hip_dispatch_elementwise(h, unary ? nullptr : f32(op.ins[0]), f32(bi), f32(op.outs[0]), ep);
+    s = BWPP_PLAN_CALL(
+        bwpp_hip_dispatch_elementwise(h, unary ? nullptr : f32(op.ins[0]), f32(bi), f32(op.outs[0]), ep));
   } else if (k == "reduce_sum") {
     if (!need(1, 1)) return bad("in=X out=Y");
     const Value &X = val(op.ins[0]);
     BwppReduceParams rp = {(uint32_t)X.rows(), (uint32_t)X.cols(), (uint32_t)X.row_stride(),
                            (int32_t)num("axis", 1)};
-    s = bwpp_hip_dispatch_reduce_sum(h, f32(op.ins[0]), f32(op.outs[0]), rp);
+    s = BWPP_PLAN_CALL(bwpp_hip_dispatch_reduce_sum(h, f32(op.ins[0]), f32(op.outs[0]), rp));
   } else if (k == "silu_grad") {
     if (!need(2, 1)) return bad("in=X,dY out=dX");
-    s = bwpp_hip_dispatch_silu_grad(h, f32(op.ins[0]), f32(op.ins[1]), f32(op.outs[0]), val(op.ins[0]).elems());
+    s = BWPP_PLAN_CALL(
+        bwpp_hip_dispatch_silu_grad(h, f32(op.ins[0]), f32(op.ins[1]), f32(op.outs[0]), val(op.ins[0]).elems()));
   } else if (k == "softmax_grad") {
     if (!need(2, 1)) return bad("in=Y,dY out=dX");
     const Value &Y = val(op.ins[0]);
     BwppSoftmaxParams sp = {(uint32_t)Y.rows(), (uint32_t)Y.cols(), (uint32_t)Y.row_stride()};
-    s = bwpp_hip_dispatch_softmax_grad(h, f32(op.ins[0]), f32(op.ins[1]), f32(op.outs[0]), sp);
+    s = BWPP_PLAN_CALL(bwpp_hip_dispatch_softmax_grad(h, f32(op.ins[0]), f32(op.ins[1]), f32(op.outs[0]), sp));
   } else if (k == "rmsnorm_grad") {
     if (!need(3, 1)) return bad("in=X,gamma,dY out=dX[,dgamma[,dbeta]]");
     const Value &X = val(op.ins[0]);
     BwppRmsnormParams rp = {(uint32_t)X.rows(), (uint32_t)X.cols(), (uint32_t)X.row_stride(), (float)num("eps", 1e-5)};
-    s = bwpp_hip_dispatch_rmsnorm_grad(h, f32(op.ins[0]), f32(op.ins[1]), f32(op.ins[2]), f32(op.outs[0]),
+    s = BWPP_PLAN_CALL(bwpp_hip_dispatch_rmsnorm_grad(h, f32(op.ins[0]), f32(op.ins[1]), f32(op.ins[2]), f32(op.outs[0]),
                                        op.outs.size() > 1 ? f32(op.outs[1]) : nullptr,
-                                       op.outs.size() > 2 ? f32(op.outs[2]) : nullptr, rp);
+                                       op.outs.size() > 2 ? f32(op.outs[2]) : nullptr, rp));
   } else if (k == "attention" || k == "attention_grad") {
     // q / k / v (and o, do, dq, dk, dv) are [batch*seq, heads*dim] row
     // blocks: head h of a row starts at column h*dim.
@@ -578,13 +597,13 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
       // A second output receives the per-query log-sum-exp ([batch, heads, seq]).
       float *lse = op.outs.size() > 1 ? f32(op.outs[1]) : nullptr;
       if (lse && val(op.outs[1]).elems() != B * H * M) return bad("lse needs batch*heads*seq elements");
-      s = lse ? bwpp_hip_dispatch_attention_lse(h, ptr(op.ins[0]), ptr(op.ins[1]), ptr(op.ins[2]), ptr(op.outs[0]),
+      s = BWPP_PLAN_CALL(lse ? bwpp_hip_dispatch_attention_lse(h, ptr(op.ins[0]), ptr(op.ins[1]), ptr(op.ins[2]), ptr(op.outs[0]),
                                                 lse, ap)
-              : bwpp_hip_dispatch_attention(h, ptr(op.ins[0]), ptr(op.ins[1]), ptr(op.ins[2]), ptr(op.outs[0]), ap);
+              : bwpp_hip_dispatch_attention(h, ptr(op.ins[0]), ptr(op.ins[1]), ptr(op.ins[2]), ptr(op.outs[0]), ap));
     } else {
-      s = bwpp_hip_attention_grad_planned(h, ptr(op.ins[0]), ptr(op.ins[1]), ptr(op.ins[2]), ptr(op.ins[3]),
+      s = BWPP_PLAN_CALL(bwpp_hip_attention_grad_planned(h, ptr(op.ins[0]), ptr(op.ins[1]), ptr(op.ins[2]), ptr(op.ins[3]),
                                           ptr(op.ins[4]), f32(op.ins[5]), ptr(op.outs[0]), ptr(op.outs[1]),
-                                          ptr(op.outs[2]), ap);
+                                          ptr(op.outs[2]), ap));
     }
   } else {
     return bad("unknown op");

@@ -58,12 +58,22 @@ def test_block_plan_arena_fits_reuse():
     assert 0.3e9 < p.arena_bytes < 1.0e9
 
 
+_IO = "bwpp.plan 1\nvalue a f32 [4,4] input\nvalue b f32 [4,4] input\nvalue y f32 [4,4] output\n"
+
+
 @pytest.mark.parametrize("text,msg", [
     ("dim B 2\n", "bwpp.plan 1"),
     ("bwpp.plan 1\nvalue x f32 [Q,4] input\n", "unknown dim"),
     ("bwpp.plan 1\nvalue x f32 [4,4] temp\nop softmax out=y in=x\n", "unknown value"),
     ("bwpp.plan 1\nvalue x f32 [4,4] input\nview v of=x offset=8 ld=4 shape=[3,4]\n", "runs past"),
     ("bwpp.plan 1\nvalue x f32 [4,4] temp\nvalue y f32 [4,4] output\nop softmax out=y in=x\n", "never written"),
+    # Op arguments are checked when the plan is created, not when it runs.
+    (_IO + "op matmul out=y in=a,b epi=gelu\n", "epi must be"),
+    (_IO + "op add out=y in=a,b bcast=diag\n", "bcast must be"),
+    (_IO + "op frobnicate out=y in=a\n", "unknown op"),
+    ("bwpp.plan 1\nvalue a f32 [4,3] input\nvalue b f32 [4,4] input\nvalue y f32 [4,4] output\n"
+     "op matmul out=y in=a,b\n", "operand shapes do not match"),
+    (_IO + "op attention out=y in=a,b,b heads=3\n", "bad batch / heads"),
 ])
 def test_plan_errors(text, msg):
     with pytest.raises(plan.PlanError) as e:
