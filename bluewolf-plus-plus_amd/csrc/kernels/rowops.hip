@@ -346,24 +346,33 @@ __device__ __forceinline__ void row_reg(const BwppRowArgs &a) {
   };
 
   // Group loop, two groups per trip so the prefetch buffers alternate
-  // without copies; every trip count is block-uniform.
+  // without copies; every trip count is block-uniform.  The last group of a
+  // block is processed on a path of its own, so inside the loop the
+  // next-group loads are issued unconditionally: the compiler's vmcnt
+  // waits then count them as younger than the current group's loads (with
+  // a conditional prefetch it merges both paths and waits for the prefetch
+  // too, which serialises the rows).
   uint32_t grp = blockIdx.x;
   if (grp >= ngroups) return;  // block-uniform
   float4 va[VPT], vb[VPT];
   load_row(grp, va);
   for (;;) {
     uint32_t next = grp + gridDim.x;
-    bool has_next = next < ngroups;
-    if (kPrefetch && has_next) load_row(next, vb);
+    if (next >= ngroups) {
+      process(va, grp);
+      break;
+    }
+    if (kPrefetch) load_row(next, vb);
     process(va, grp);
-    if (!has_next) break;
     if (!kPrefetch) load_row(next, vb);
     grp = next;
     next = grp + gridDim.x;
-    has_next = next < ngroups;
-    if (kPrefetch && has_next) load_row(next, va);
+    if (next >= ngroups) {
+      process(vb, grp);
+      break;
+    }
+    if (kPrefetch) load_row(next, va);
     process(vb, grp);
-    if (!has_next) break;
     if (!kPrefetch) load_row(next, va);
     grp = next;
   }
