@@ -599,74 +599,96 @@ __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
 
 // ---------------------------------------------------------------- fp32
 
-template <int R, int BK, int NT, bool MNC, bool EDGE>
-struct StageF32 {
-  // MNC: tile kept [BK][R + 32]; else [R][BK + 2].
-  static constexpr int kLd = MNC ? R + 32 : BK + 2;
-  static constexpr int kVecs = R * BK / 4 / NT;
-  float4 r[kVecs];
+// LDS tiles hold both operands K-contiguous: [R rows][32 k] fp32, 128-byte
+// rows of eight 16-byte chunks, chunk q of row r stored at chunk
+// q ^ swz(r), swz(r) = (r & 7) ^ ((r >> 3) & 3).  Eight consecutive rows at
+// one chunk (the MFMA operand reads) and rows 4t + c, t = 0..7, at one
+// chunk (the transposing stores below) both map to eight distinct chunk
+// positions, i.e. distinct bank groups.
+__device__ __forceinline__ uint32_t f32_swz(uint32_t r) { return (r & 7u) ^ ((r >> 3) & 3u); }
+__device__ __forceinline__ uint32_t f32_off(uint32_t r, uint32_t q) { return r * 32u + ((q ^ f32_swz(r)) << 2); }
 
-  __device__ __forceinline__ void load(const float *g, uint32_t ld, uint32_t r0, uint32_t rows,
-                                       uint32_t k0, uint32_t K, bool vec, int tid) {
+// Register staging of one operand tile (R rows x 32 k) for NT threads.
+// K-contiguous in memory (KC): thread t copies chunk t % 8 of rows
+// t / 8 + (NT / 8) i.  MN-contiguous (the transpose of what LDS holds):
+// thread t loads a 4 (k) x 4 (mn) block with four 16-byte loads along mn
+// and writes its four columns as 16-byte k-runs (the 4 x 4 transpose is a
+// register renaming).
+template <int R, int NT, bool KC, bool EDGE>
+struct TileF32 {
+  static constexpr int kVecs = R * 32 / 4 / NT;
+  static_assert(KC ? (NT % 8 == 0 && R % (NT / 8) == 0) : (R % 4 == 0 && NT % (R / 4) == 0), "tile shape");
+  float4 v[kVecs];
+
+  // g: operand base, ld its leading dimension; r0 the first tile row (m or
+  // n), rows the operand's extent there; k0 the first k, K the k extent.
+  __device__ __forceinline__ void load(const float *g, uint32_t ld, uint32_t r0, uint32_t rows, uint32_t k0,
+                                       uint32_t K, bool vec, int tid) {
+    if constexpr (KC) {
 #pragma unroll
-    for (int i = 0; i < kVecs; ++i) {
-      const int q = tid + i * NT;
-      uint32_t grow, gcol, lim_row, lim_col;
-      if constexpr (MNC) {  // memory rows are k, columns mn
-        const int k = q / (R / 4), c = q % (R / 4);
-        grow = k0 + k;
-        gcol = r0 + c * 4;
-        lim_row = K;
-        lim_col = rows;
-      } else {  // memory rows are mn, columns k
-        const int row = q / (BK / 4), c = q % (BK / 4);
-        grow = r0 + row;
-        gcol = k0 + c * 4;
-        lim_row = rows;
-        lim_col = K;
+      for (int i = 0; i < kVecs; ++i) {
+        const uint32_t row = (uint32_t)(tid / 8 + (NT / 8) * i), gk = k0 + 4u * (uint32_t)(tid % 8);
+        v[i] = ld4<EDGE>(g, ld, r0 + row, rows, gk, K, vec);
       }
-      const float *p = g + (size_t)grow * ld + gcol;
-      if (!EDGE) {
-        r[i] = *reinterpret_cast<const float4 *>(p);
-      } else {
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (grow < lim_row) {
-          if (vec && gcol + 4 <= lim_col) {
-            v = *reinterpret_cast<const float4 *>(p);
-          } else {
-            if (gcol + 0 < lim_col) v.x = p[0];
-            if (gcol + 1 < lim_col) v.y = p[1];
-            if (gcol + 2 < lim_col) v.z = p[2];
-            if (gcol + 3 < lim_col) v.w = p[3];
-          }
-        }
-        r[i] = v;
+    } else {
+      constexpr int kPer = R / 4;  // threads across one k row
+      const uint32_t mn = 4u * (uint32_t)(tid % kPer);
+#pragma unroll
+      for (int b = 0; b < kVecs / 4; ++b) {
+        const uint32_t kk = k0 + 4u * (uint32_t)(tid / kPer + (NT / kPer) * b);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * b + e] = ld4<EDGE>(g, ld, kk + e, K, r0 + mn, rows, vec);
       }
     }
   }
 
   __device__ __forceinline__ void store(float *s, int tid) const {
+    if constexpr (KC) {
 #pragma unroll
-    for (int i = 0; i < kVecs; ++i) {
-      const int q = tid + i * NT;
-      if constexpr (MNC) {
-        const int k = q / (R / 4), c = q % (R / 4);
-        *reinterpret_cast<float4 *>(s + k * kLd + c * 4) = r[i];
-      } else {
-        const int row = q / (BK / 4), c = q % (BK / 4);
-        float2 *d = reinterpret_cast<float2 *>(s + row * kLd + c * 4);
-        d[0] = make_float2(r[i].x, r[i].y);
-        d[1] = make_float2(r[i].z, r[i].w);
+      for (int i = 0; i < kVecs; ++i) {
+        const uint32_t row = (uint32_t)(tid / 8 + (NT / 8) * i);
+        *reinterpret_cast<float4 *>(s + f32_off(row, (uint32_t)(tid % 8))) = v[i];
+      }
+    } else {
+      constexpr int kPer = R / 4;
+      const uint32_t mn = 4u * (uint32_t)(tid % kPer);
+#pragma unroll
+      for (int b = 0; b < kVecs / 4; ++b) {
+        const uint32_t q = (uint32_t)(tid / kPer + (NT / kPer) * b);  // k chunk
+        const float4 &x0 = v[4 * b], &x1 = v[4 * b + 1], &x2 = v[4 * b + 2], &x3 = v[4 * b + 3];
+        *reinterpret_cast<float4 *>(s + f32_off(mn + 0, q)) = make_float4(x0.x, x1.x, x2.x, x3.x);
+        *reinterpret_cast<float4 *>(s + f32_off(mn + 1, q)) = make_float4(x0.y, x1.y, x2.y, x3.y);
+        *reinterpret_cast<float4 *>(s + f32_off(mn + 2, q)) = make_float4(x0.z, x1.z, x2.z, x3.z);
+        *reinterpret_cast<float4 *>(s + f32_off(mn + 3, q)) = make_float4(x0.w, x1.w, x2.w, x3.w);
       }
     }
   }
 
-  // Element (k, mn) of the tile.
-  __device__ __forceinline__ static float at(const float *s, int k, int mn) {
-    return MNC ? s[k * kLd + mn] : s[mn * kLd + k];
+  // 16 bytes at (row, col..col+3) of a [rows x cols] matrix with leading
+  // dimension ld; zeros outside (EDGE), element-wise when not 16-byte rows.
+  template <bool E>
+  __device__ __forceinline__ static float4 ld4(const float *g, uint32_t ld, uint32_t row, uint32_t nrows,
+                                               uint32_t col, uint32_t ncols, bool vec) {
+    const float *p = g + (size_t)row * ld + col;
+    if (!E) return *reinterpret_cast<const float4 *>(p);
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row < nrows) {
+      if (vec && col + 4 <= ncols) {
+        x = *reinterpret_cast<const float4 *>(p);
+      } else {
+        if (col + 0 < ncols) x.x = p[0];
+        if (col + 1 < ncols) x.y = p[1];
+        if (col + 2 < ncols) x.z = p[2];
+        if (col + 3 < ncols) x.w = p[3];
+      }
+    }
+    return x;
   }
-  static constexpr int kSize = MNC ? BK * (R + 32) : R * (BK + 2);
 };
+
+#ifndef BWPP_F32_STORE_AFTER
+#define BWPP_F32_STORE_AFTER 0
+#endif
 
 template <bool TA, bool TB, bool EDGE, bool SPLIT = false>
 __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
@@ -674,10 +696,13 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
   constexpr int NT = 64 * WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
-  using SA = StageF32<BM, BK, NT, TA, EDGE>;   // A MN-contiguous when transposed
-  using SB = StageF32<BN, BK, NT, !TB, EDGE>;  // B MN-contiguous when not transposed
-  constexpr int kBuf = SA::kSize + SB::kSize;
-  __shared__ __attribute__((aligned(16))) float smemf[2 * kBuf];
+  using SA = TileF32<BM, NT, !TA, EDGE>;  // A K-contiguous unless transposed
+  using SB = TileF32<BN, NT, TB, EDGE>;   // B K-contiguous only when transposed
+  constexpr int kTileA = BM * BK, kTileB = BN * BK;
+  constexpr int kBuf = kTileA + kTileB;
+  constexpr int kCld = BN + 4;  // epilogue C tile [BM][BN + 4], reusing the operand buffers
+  constexpr int kSmem = 2 * kBuf > BM * kCld ? 2 * kBuf : BM * kCld;
+  __shared__ __attribute__((aligned(16))) float smemf[kSmem];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -714,40 +739,66 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
     sa.load(A, a.lda, m0, a.M, 0, Klen, vec, tid);
     sb.load(B, a.ldb, n0, a.N, 0, Klen, vec, tid);
     sa.store(smemf, tid);
-    sb.store(smemf + SA::kSize, tid);
+    sb.store(smemf + kTileA, tid);
   }
   __syncthreads();
 
-  const int lrow = lane & 31, lk = lane >> 5;
+  // Operand reads: lane l takes row l % 32 of its 32-row block and, for the
+  // 8-k chunk j, the 16-byte k-run 8j + 4 (l / 32) .. +3; MFMA step s of
+  // the chunk pairs k = 8j + s (lanes 0-31) with 8j + 4 + s (lanes 32-63).
+  const uint32_t lrow = (uint32_t)(lane & 31), lhi = (uint32_t)(lane >> 5);
+  constexpr uint32_t kStoreAfter = BWPP_F32_STORE_AFTER;
   for (uint32_t kt = 0; kt < nk; ++kt) {
     const uint32_t kn = (kt + 1 < nk ? kt + 1 : kt) * BK;
     sa.load(A, a.lda, m0, a.M, kn, Klen, vec, tid);
     sb.load(B, a.ldb, n0, a.N, kn, Klen, vec, tid);
+    // Keep the next tile's loads here, ahead of the MFMAs: left alone, the
+    // scheduler sinks them to the LDS stores at the end of the iteration
+    // and the full memory latency is exposed once per K tile.
+    __builtin_amdgcn_sched_barrier(0);
     const float *As = smemf + (kt & 1) * kBuf;
-    const float *Bs = As + SA::kSize;
+    const float *Bs = As + kTileA;
+    // Operands of chunk j + 1 are read while chunk j's MFMAs issue.
+    float4 af[2][FM], bf[2][FN];
+    auto read_chunk = [&](uint32_t j, float4(&ar)[FM], float4(&br)[FN]) {
 #pragma unroll
-    for (int ks = 0; ks < BK / 2; ++ks) {
-      const int k = 2 * ks + lk;
-      float af[FM], bf[FN];
+      for (int f = 0; f < FM; ++f)
+        ar[f] = *reinterpret_cast<const float4 *>(As + f32_off((uint32_t)(wm * TM + f * 32) + lrow, 2 * j + lhi));
 #pragma unroll
-      for (int j = 0; j < FM; ++j) af[j] = SA::at(As, k, wm * TM + j * 32 + lrow);
+      for (int f = 0; f < FN; ++f)
+        br[f] = *reinterpret_cast<const float4 *>(Bs + f32_off((uint32_t)(wn * TN + f * 32) + lrow, 2 * j + lhi));
+    };
+    read_chunk(0, af[0], bf[0]);
 #pragma unroll
-      for (int i = 0; i < FN; ++i) bf[i] = SB::at(Bs, k, wn * TN + i * 32 + lrow);
+    for (uint32_t j = 0; j < BK / 8; ++j) {
+      if (j + 1 < BK / 8) read_chunk(j + 1, af[(j + 1) & 1], bf[(j + 1) & 1]);
+      const float4(&ac)[FM] = af[j & 1];
+      const float4(&bc)[FN] = bf[j & 1];
 #pragma unroll
-      for (int i = 0; i < FN; ++i)
+      for (int st = 0; st < 4; ++st)
 #pragma unroll
-        for (int j = 0; j < FM; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[i], af[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int jj = 0; jj < FM; ++jj) {
+            const float x = st == 0 ? bc[i].x : st == 1 ? bc[i].y : st == 2 ? bc[i].z : bc[i].w;
+            const float y = st == 0 ? ac[jj].x : st == 1 ? ac[jj].y : st == 2 ? ac[jj].z : ac[jj].w;
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc[i][jj], 0, 0, 0);
+          }
+      if (j == kStoreAfter) {
+        // The next tile goes into the other buffer part way through the
+        // MFMAs (nobody reads that buffer during this tile), so the wait for
+        // its loads and the LDS writes overlap the remaining MFMAs.
+        __builtin_amdgcn_sched_barrier(0);
+        float *nxt = smemf + ((kt + 1) & 1) * kBuf;
+        sa.store(nxt, tid);
+        sb.store(nxt + kTileA, tid);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    float *nxt = smemf + ((kt + 1) & 1) * kBuf;
-    sa.store(nxt, tid);
-    sb.store(nxt + SA::kSize, tid);
     __syncthreads();
   }
 
   // Epilogue through LDS as in the bf16 kernel: C tile [BM][BN + 4] fp32.
-  constexpr int kCld = BN + 4;
-  static_assert(BM * kCld <= 2 * kBuf, "epilogue tile must fit the operand buffers");
   // Split-K blocks store raw sums; the reduce kernel applies the epilogue.
   const float *bias = static_cast<const float *>(a.bias);
   const bool add = !SPLIT && (a.epilogue & kEpiAdd) && bias;
