@@ -110,6 +110,107 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_rmsnorm_grad(const BwppGr
   }
 }
 
+// rmsnorm_grad for 16-byte rows of at most 256 * VPT columns: one wave per
+// row (lane l owns float4 chunks l, l + 64, ...), so the two row sums are
+// wave reductions with no block barrier inside the row loop; the block's 4
+// waves stride over rows, each keeping its dgamma / dbeta column sums in
+// registers, and combine them once through LDS at the end into the block's
+// partial row (summed by bwpp_col_partials_sum).  Same arithmetic as
+// bwpp_rmsnorm_grad.
+template <int VPT>
+__device__ __forceinline__ void rmsnorm_grad_wave(const BwppGradArgs &g) {
+  extern __shared__ float colacc[];  // [4 waves][2][cols] when partials are requested
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const uint32_t cols = g.cols;
+  const bool parts = g.part_g != nullptr;
+  float4 gm[VPT], ag[VPT], ab[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const uint32_t c = 4u * (uint32_t)(lane + 64 * j);
+    gm[j] = make_float4(1.f, 1.f, 1.f, 1.f);
+    if (g.gamma && c < cols) gm[j] = *reinterpret_cast<const float4 *>(g.gamma + c);
+    ag[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    ab[j] = ag[j];
+  }
+  for (uint32_t r = blockIdx.x * 4u + (uint32_t)wave; r < g.rows; r += gridDim.x * 4u) {
+    const float *x = g.a + (size_t)r * g.ld;
+    const float *dy = g.b + (size_t)r * g.ld;
+    float *dx = g.out + (size_t)r * g.ld;
+    float4 xv[VPT], dv[VPT];
+    float ss = 0.0f, t = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const uint32_t c = 4u * (uint32_t)(lane + 64 * j);
+      xv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      dv[j] = xv[j];
+      if (c < cols) {
+        xv[j] = *reinterpret_cast<const float4 *>(x + c);
+        dv[j] = *reinterpret_cast<const float4 *>(dy + c);
+      }
+      ss += (xv[j].x * xv[j].x + xv[j].y * xv[j].y) + (xv[j].z * xv[j].z + xv[j].w * xv[j].w);
+      t += (xv[j].x * gm[j].x * dv[j].x + xv[j].y * gm[j].y * dv[j].y) +
+           (xv[j].z * gm[j].z * dv[j].z + xv[j].w * gm[j].w * dv[j].w);
+    }
+    ss = wave_sum(ss);
+    t = wave_sum(t);
+    const float inv = 1.0f / sqrtf(ss / (float)cols + g.eps);
+    const float mdot = inv * t / (float)cols;  // mean(xhat * gamma * dy)
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const uint32_t c = 4u * (uint32_t)(lane + 64 * j);
+      if (c >= cols) continue;
+      float4 h, o;
+      h.x = xv[j].x * inv;
+      h.y = xv[j].y * inv;
+      h.z = xv[j].z * inv;
+      h.w = xv[j].w * inv;
+      o.x = inv * (gm[j].x * dv[j].x - h.x * mdot);
+      o.y = inv * (gm[j].y * dv[j].y - h.y * mdot);
+      o.z = inv * (gm[j].z * dv[j].z - h.z * mdot);
+      o.w = inv * (gm[j].w * dv[j].w - h.w * mdot);
+      *reinterpret_cast<float4 *>(dx + c) = o;
+      ag[j].x += dv[j].x * h.x;
+      ag[j].y += dv[j].y * h.y;
+      ag[j].z += dv[j].z * h.z;
+      ag[j].w += dv[j].w * h.w;
+      ab[j].x += dv[j].x;
+      ab[j].y += dv[j].y;
+      ab[j].z += dv[j].z;
+      ab[j].w += dv[j].w;
+    }
+  }
+  if (!parts) return;  // block-uniform
+  float *mine = colacc + (size_t)wave * 2 * cols;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const uint32_t c = 4u * (uint32_t)(lane + 64 * j);
+    if (c < cols) {
+      *reinterpret_cast<float4 *>(mine + c) = ag[j];
+      *reinterpret_cast<float4 *>(mine + cols + c) = ab[j];
+    }
+  }
+  __syncthreads();
+  for (uint32_t c = threadIdx.x; c < cols; c += 256) {
+    float sg = 0.0f, sb = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      sg += colacc[(size_t)w * 2 * cols + c];
+      sb += colacc[(size_t)w * 2 * cols + cols + c];
+    }
+    g.part_g[(size_t)blockIdx.x * cols + c] = sg;
+    g.part_b[(size_t)blockIdx.x * cols + c] = sb;
+  }
+}
+
+#define BWPP_RMSNORM_GRAD_WAVE(VPT)                                                                 \
+  extern "C" __global__ __launch_bounds__(256) void bwpp_rmsnorm_grad_w##VPT(const BwppGradArgs g) { \
+    rmsnorm_grad_wave<VPT>(g);                                                                      \
+  }
+BWPP_RMSNORM_GRAD_WAVE(1)
+BWPP_RMSNORM_GRAD_WAVE(2)
+BWPP_RMSNORM_GRAD_WAVE(4)
+BWPP_RMSNORM_GRAD_WAVE(8)
+
 // out[c] = sum_p part[p][c] for the two partial arrays (dgamma, dbeta); the
 // outputs may be NULL.  A block owns 16 columns: thread (g, c) of 16 x 16
 // sums parts g, g + 16, ... of column c (16 consecutive columns = 64-byte

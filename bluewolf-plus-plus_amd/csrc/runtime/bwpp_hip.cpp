@@ -85,6 +85,7 @@ struct BwppHip {
   hipFunction_t attn_bwd_dkdv[2][2] = {};
   // fp32 MFMA attention, head dim 64 / 128: [d128][causal]
   hipFunction_t attn_f32_fwd[2][2] = {}, attn_f32_dq[2][2] = {}, attn_f32_dkdv[2][2] = {};
+  hipFunction_t rmsnorm_grad_w[4] = {};  // wave-per-row rmsnorm_grad, 256 / 512 / 1024 / 2048 columns
   hipFunction_t silu_grad = nullptr, softmax_grad = nullptr, rmsnorm_grad = nullptr, col_partials_sum = nullptr,
                 reduce_sum_rows = nullptr, reduce_sum_cols = nullptr, elementwise = nullptr;
   // Library-owned device workspace (column partials), grown on demand and
@@ -151,6 +152,8 @@ BwppHipStatus resolve_all(BwppHip *h) {
       {"bwpp_rmsnorm_grad", &h->rmsnorm_grad},       {"bwpp_col_partials_sum", &h->col_partials_sum},
       {"bwpp_reduce_sum_rows", &h->reduce_sum_rows}, {"bwpp_reduce_sum_cols", &h->reduce_sum_cols},
       {"bwpp_elementwise", &h->elementwise},         {"bwpp_gemm_f32_splitk_reduce", &h->gemm_f32_reduce},
+      {"bwpp_rmsnorm_grad_w1", &h->rmsnorm_grad_w[0]}, {"bwpp_rmsnorm_grad_w2", &h->rmsnorm_grad_w[1]},
+      {"bwpp_rmsnorm_grad_w4", &h->rmsnorm_grad_w[2]}, {"bwpp_rmsnorm_grad_w8", &h->rmsnorm_grad_w[3]},
   };
   for (auto &e : singles)
     if ((s = resolve(h, e.name, e.slot)) != BWPP_HIP_OK) return s;
@@ -646,22 +649,44 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
   if (tiles > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "matmul: too many tiles");
   if (bf16 && full && h->gemm_waves == 8)
     return launch(h, h->gemm_bf16_w8[ta][tb], (uint32_t)tiles, 1, 1, 512, g);
-  // fp32 full tiles that leave the chip under-filled (fewer tiles than the
-  // two 128 x 128 blocks each CU holds) and have a long K: split K into S
-  // ranges of at least 512 (multiples of BK), raw partial tiles into the
-  // workspace, then one reduce pass adds them in order and applies the
-  // epilogue.
-  if (!bf16 && full && h->gemm_splitk && h->cus > 0 && p.K >= 1024) {
+  // fp32 full tiles: split K into S ranges (multiples of BK, at least 256
+  // long) when that fills the chip better.  Each CU holds two 128 x 128
+  // blocks, so a launch of b blocks runs in ceil(b / slots) waves of blocks
+  // that each take time proportional to their K range; splitting adds a
+  // reduce pass over S + 1 planes of M x N floats.  S minimises
+  //   waves(S) * (K / S) * t_k + (S + 1) * M * N * 4 / bw + t_launch
+  // with t_k = 0.13 us per k of one block (measured: a 128 x 128 x 1024
+  // block takes ~134 us with two blocks per CU), bw = 5 TB/s, t_launch =
+  // 5 us.  The blocks write raw partial tiles into the workspace and the
+  // reduce pass adds them in order and applies the epilogue.
+  if (!bf16 && full && h->gemm_splitk && h->cus > 0 && p.K >= 512) {
     const uint64_t slots = 2ull * (uint64_t)h->cus;
-    uint64_t S = tiles < slots ? std::min<uint64_t>((slots + tiles - 1) / tiles, p.K / 512) : 1;
-    if (S > 1) {
+    auto cost = [&](uint64_t S, uint32_t kchunk) {
+      const double waves = (double)((tiles * S + slots - 1) / slots);
+      double t = waves * kchunk * 0.13;
+      if (S > 1) t += (double)(S + 1) * p.M * p.N * 4.0 / 5e6 + 5.0;
+      return t;
+    };
+    uint64_t bestS = 1;
+    uint32_t bestChunk = p.K;
+    double best = cost(1, p.K);
+    for (uint64_t S = 2; S <= 16 && p.K / S >= 256; ++S) {
       const uint32_t kchunk = (uint32_t)(((p.K + S - 1) / S + BK - 1) / BK * BK);
-      S = (p.K + kchunk - 1) / kchunk;
-      if ((s = ensure_ws(h, (size_t)S * p.M * p.N * sizeof(float))) != BWPP_HIP_OK) return s;
-      g.ksplit = (uint32_t)S;
-      g.kchunk = kchunk;
+      const uint64_t Se = (p.K + kchunk - 1) / kchunk;
+      const double c = cost(Se, kchunk);
+      if (c < 0.95 * best) {  // split only for a clear gain
+        best = c;
+        bestS = Se;
+        bestChunk = kchunk;
+      }
+    }
+    if (bestS > 1) {
+      if ((s = ensure_ws(h, (size_t)bestS * p.M * p.N * sizeof(float))) != BWPP_HIP_OK) return s;
+      g.ksplit = (uint32_t)bestS;
+      g.kchunk = bestChunk;
       g.part = static_cast<float *>(h->ws);
-      if ((s = launch(h, h->gemm_f32_split[ta][tb], (uint32_t)(tiles * S), 1, 1, 256, g)) != BWPP_HIP_OK) return s;
+      if ((s = launch(h, h->gemm_f32_split[ta][tb], (uint32_t)(tiles * bestS), 1, 1, 256, g)) != BWPP_HIP_OK)
+        return s;
       const uint64_t vecs = (uint64_t)p.M * (p.N / 4);
       const uint64_t grid = std::min<uint64_t>((vecs + 255) / 256, 8ull * (uint64_t)h->cus);
       return launch(h, h->gemm_f32_reduce, (uint32_t)grid, 1, 1, 256, g);
@@ -1004,16 +1029,29 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad(BwppHip *h, const float 
   // With column partials, at most kMaxParts blocks (each loops over its
   // rows), which bounds the partial arrays to kMaxParts rows.
   constexpr uint32_t kMaxParts = 512;
-  uint32_t grid = p.rows == 0 ? 1u : row_grid(h, p.rows);
-  if (parts && grid > kMaxParts) grid = kMaxParts;
+  // 16-byte rows of at most 2048 columns: one wave per row (no block
+  // barriers in the row loop), 4 rows per block per trip.
+  int wv = -1;
+  if (p.cols <= 2048 && p.cols % 4 == 0 && ld % 4 == 0 && aligned16(x) && aligned16(dy) && aligned16(dx) &&
+      (!gamma || aligned16(gamma)))
+    wv = p.cols <= 256 ? 0 : p.cols <= 512 ? 1 : p.cols <= 1024 ? 2 : 3;
+  uint32_t grid;
+  if (wv >= 0) {
+    const uint32_t cap = parts ? kMaxParts : (h->cus > 0 ? 8u * (uint32_t)h->cus : 2048u);
+    grid = p.rows == 0 ? 1u : std::min<uint32_t>((p.rows + 3) / 4, cap);
+  } else {
+    grid = p.rows == 0 ? 1u : row_grid(h, p.rows);
+    if (parts && grid > kMaxParts) grid = kMaxParts;
+  }
   if (parts) {
     if ((s = ensure_ws(h, (size_t)2 * grid * p.cols * sizeof(float))) != BWPP_HIP_OK) return s;
     g.part_g = static_cast<float *>(h->ws);
     g.part_b = g.part_g + (size_t)grid * p.cols;
   }
   if (p.rows > 0 || parts) {
-    if ((s = launch(h, h->rmsnorm_grad, grid, 1, 1, 256, g, parts ? 2u * p.cols * 4u : 0u)) != BWPP_HIP_OK)
-      return s;
+    s = wv >= 0 ? launch(h, h->rmsnorm_grad_w[wv], grid, 1, 1, 256, g, parts ? 8u * p.cols * 4u : 0u)
+                : launch(h, h->rmsnorm_grad, grid, 1, 1, 256, g, parts ? 2u * p.cols * 4u : 0u);
+    if (s != BWPP_HIP_OK) return s;
   }
   if (!parts) return BWPP_HIP_OK;
   BwppGradArgs r = {};

@@ -80,6 +80,28 @@ def test_rmsnorm_grad(be, oracle, rows, cols, with_gamma):
     assert rel_max_err(host(dx2), wdx) <= TOL
 
 
+@pytest.mark.parametrize("rows,cols,ld", [(3, 2048, 2048), (1029, 512, 516), (2, 256, 256), (7, 1996, 2000),
+                                         (2049, 20, 24)])
+def test_rmsnorm_grad_wave_rows(be, oracle, rows, cols, ld):
+    """The wave-per-row kernel (16-byte rows, <= 2048 columns): row counts
+    that leave blocks partly empty, padded rows, partial float4 lanes."""
+    torch = _torch()
+    x = synth.normal((rows, cols), rows, 0)
+    g = synth.uniform((cols,), cols, 1, 0.5, 1.5)
+    dy = synth.normal((rows, cols), rows, 2)
+    pad = lambda a: np.pad(a, ((0, 0), (0, ld - cols)))
+    dx = torch.full((rows, ld), 5.0, device="cuda")
+    dg = torch.zeros(cols, device="cuda")
+    db = torch.zeros(cols, device="cuda")
+    be.dispatch_rmsnorm_grad(dev(pad(x)), dev(g), dev(pad(dy)), dx, dg, db, bwpp.RmsnormParams(rows, cols, ld, 1e-5))
+    wdx, wdg, wdb = oracle.rmsnorm_grad(x, g, dy, 1e-5)
+    out = host(dx)
+    assert rel_max_err(out[:, :cols], wdx) <= TOL
+    assert np.all(out[:, cols:] == 5.0)
+    assert rel_max_err(host(dg), wdg) <= TOL
+    assert rel_max_err(host(db), wdb) <= TOL
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 1), (7, 300), (4096, 1024), (1000, 3)])
 @pytest.mark.parametrize("axis", [0, 1])
 def test_reduce_sum(be, oracle, rows, cols, axis):
