@@ -154,6 +154,9 @@ def time_c2(bench, steps, warmup):
     return wall, s.elapsed_time(e) * 1e-3
 
 
+WARM_MS = 40.0  # sustained work before any extras timing starts
+
+
 def time_c2_ops(bench, reps):
     """Average launch duration per operator: `reps` back-to-back launches
     over the rotating buffer sets, between two events on the launch stream."""
@@ -318,9 +321,21 @@ def regress_json(args):
     return out
 
 
-def _events_us(torch, fn, iters, warmup=3):
+def _events_us(torch, fn, iters, warm_ms=WARM_MS):
+    """Average launch time of fn over `iters` back-to-back launches, after
+    at least warm_ms of the same work: the MI355X clock ramps up over the
+    first ~35 ms of sustained matrix work (a C3 GEMM goes from ~1035 to
+    ~1180 TFLOP/s), and the figure wanted is the steady state."""
     stream = torch.cuda.current_stream()
-    for _ in range(warmup):
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(3):
+        fn()
+    e.record(stream)
+    torch.cuda.synchronize()
+    est_us = max(s.elapsed_time(e) / 3 * 1e3, 1.0)
+    for _ in range(min(4000, int(warm_ms * 1e3 / est_us) + 1)):
         fn()
     torch.cuda.synchronize()
     s = torch.cuda.Event(enable_timing=True)
@@ -464,7 +479,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=100,
+                    help="untimed C2 steps first (~20 ms: the clock ramps up under sustained load)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--nbuf", type=int, default=3, help="rotating input/output buffer sets")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -569,7 +585,7 @@ def main():
     del bench
     if not args.no_extras:
         torch.cuda.empty_cache()
-        out["extras"] = extras(be, torch, args.seed, 20, not args.no_cpu)
+        out["extras"] = extras(be, torch, args.seed, 30, not args.no_cpu)
     be.close()
     print(json.dumps(out))
 

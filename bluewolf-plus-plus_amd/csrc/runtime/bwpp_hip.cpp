@@ -649,8 +649,8 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
   if (tiles > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "matmul: too many tiles");
   if (bf16 && full && h->gemm_waves == 8)
     return launch(h, h->gemm_bf16_w8[ta][tb], (uint32_t)tiles, 1, 1, 512, g);
-  // fp32 full tiles: split K into S ranges (multiples of BK, at least 256
-  // long) when that fills the chip better.  Each CU holds two 128 x 128
+  // fp32 full tiles: split K into S ranges (multiples of BK) when that fills
+  // the chip better.  Each CU holds two 128 x 128
   // blocks, so a launch of b blocks runs in ceil(b / slots) waves of blocks
   // that each take time proportional to their K range; splitting adds a
   // reduce pass over S + 1 planes of M x N floats.  S minimises
@@ -659,7 +659,7 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
   // block takes ~134 us with two blocks per CU), bw = 5 TB/s, t_launch =
   // 5 us.  The blocks write raw partial tiles into the workspace and the
   // reduce pass adds them in order and applies the epilogue.
-  if (!bf16 && full && h->gemm_splitk && h->cus > 0 && p.K >= 512) {
+  if (!bf16 && full && h->gemm_splitk && h->cus > 0 && p.K >= 2 * BK) {
     const uint64_t slots = 2ull * (uint64_t)h->cus;
     auto cost = [&](uint64_t S, uint32_t kchunk) {
       const double waves = (double)((tiles * S + slots - 1) / slots);
@@ -670,7 +670,7 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
     uint64_t bestS = 1;
     uint32_t bestChunk = p.K;
     double best = cost(1, p.K);
-    for (uint64_t S = 2; S <= 16 && p.K / S >= 256; ++S) {
+    for (uint64_t S = 2; S <= 16 && p.K / S >= BK; ++S) {
       const uint32_t kchunk = (uint32_t)(((p.K + S - 1) / S + BK - 1) / BK * BK);
       const uint64_t Se = (p.K + kchunk - 1) / kchunk;
       const double c = cost(Se, kchunk);
