@@ -111,6 +111,47 @@ __device__ __forceinline__ void row_chan(float &n, float &mu, float &m2, float *
   }
 }
 
+// row_chan for equal per-thread counts n (full rows): the same statistics
+// with the equal-weight form of the merge; WPR waves' (mean, M2) combine as
+// mean = average of the means, M2 = sum of M2 + n_wave * sum (mean_i - mean)^2.
+template <int WPR>
+__device__ __forceinline__ void row_chan_equal(float &n, float &mu, float &m2, float *red) {
+  auto merge = [&](float mu2, float m22) {
+    const float d = mu2 - mu;
+    mu = mu + 0.5f * d;
+    m2 = m2 + m22 + d * d * (0.5f * n);
+    n = 2.0f * n;
+  };
+  merge(dpp_f32<kDppQuadXor1>(mu), dpp_f32<kDppQuadXor1>(m2));
+  merge(dpp_f32<kDppQuadXor2>(mu), dpp_f32<kDppQuadXor2>(m2));
+  merge(dpp_f32<kDppRowHalfMirror>(mu), dpp_f32<kDppRowHalfMirror>(m2));
+  merge(dpp_f32<kDppRowMirror>(mu), dpp_f32<kDppRowMirror>(m2));
+  merge(xor_f32(mu, 16), xor_f32(m2, 16));
+  merge(xor_f32(mu, 32), xor_f32(m2, 32));
+  if constexpr (WPR > 1) {
+    const int w = threadIdx.x >> 6, w0 = (w / WPR) * WPR;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+      red[2 * w] = mu;
+      red[2 * w + 1] = m2;
+    }
+    __syncthreads();
+    float smu = 0.0f;
+#pragma unroll
+    for (int i = 0; i < WPR; ++i) smu += red[2 * (w0 + i)];
+    const float gmu = smu * (1.0f / (float)WPR);
+    float sm2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < WPR; ++i) {
+      const float d = red[2 * (w0 + i)] - gmu;
+      sm2 += red[2 * (w0 + i) + 1] + d * d * n;
+    }
+    mu = gmu;
+    m2 = sm2;
+    n = n * (float)WPR;
+  }
+}
+
 template <int WPR>
 struct RowGeom {
   static constexpr int kBlock = WPR >= 4 ? 64 * WPR : 256;  // threads per block
@@ -270,7 +311,14 @@ __device__ __forceinline__ void row_reg(const BwppRowArgs &a) {
             }
           }
         }
-        row_chan<WPR>(n, mu, m2, redf);
+        if constexpr (FULL) {
+          // Full rows: every thread holds 4 VPT values, so every merge step
+          // joins equal counts n and Chan's update needs no division:
+          // mu = (mu_a + mu_b) / 2, M2 = M2_a + M2_b + (mu_b - mu_a)^2 n / 2.
+          row_chan_equal<WPR>(n, mu, m2, redf);
+        } else {
+          row_chan<WPR>(n, mu, m2, redf);
+        }
         mean = mu;
         ss = m2;
       } else {

@@ -250,8 +250,9 @@ int pick_row_cfg(const BwppHip *h, RowOpId op, uint32_t cols, bool vec_ok) {
 }
 
 // Launches one row-wise (axis = last) operator.  The norms run a persistent
-// grid of 4 blocks per CU so each block reuses its gamma/beta registers over
-// several rows; the others launch one block per row group.
+// grid of 2 blocks per CU (measured best of 1 / 2 / 4 / one per row) so each
+// block reuses its gamma/beta registers over several rows; the others launch
+// one block per row group.
 BwppHipStatus row_dispatch(BwppHip *h, RowOpId op, const BwppRowArgs &a, bool vec_ok) {
   const int c = pick_row_cfg(h, op, a.cols, vec_ok);
   if (c < 0) return launch(h, h->row_gen[op], a.rows, 1, 1, 256, a);
@@ -260,7 +261,7 @@ BwppHipStatus row_dispatch(BwppHip *h, RowOpId op, const BwppRowArgs &a, bool ve
   const uint32_t rpb = row_rows_per_block(cfg);
   uint32_t grid = (a.rows + rpb - 1) / rpb;
   uint32_t cap = h->row_grid_cap;
-  if (cap == 0 && (op == ROW_RMSNORM || op == ROW_LAYERNORM) && h->cus > 0) cap = 4u * (uint32_t)h->cus;
+  if (cap == 0 && (op == ROW_RMSNORM || op == ROW_LAYERNORM) && h->cus > 0) cap = 2u * (uint32_t)h->cus;
   if (cap && grid > cap) grid = cap;
   return launch(h, h->row_reg[op][c][full], grid, 1, 1, row_block(cfg), a);
 }
