@@ -78,6 +78,18 @@ typedef struct {
   float scale; /* the plain score scale (fp32 MFMA path, which gets scale * log2(e) in scale_log2) */
 } BwppAttnArgs;
 
+/* Attention operand copies between the caller's strided bf16 layout
+ * ([batch][head] slices of rows x cols, leading dimension ld) and
+ * contiguous fp32 [batch * heads][rows][cols] (attention_f32.hip). */
+typedef struct {
+  const void *src;
+  void *dst;
+  uint64_t bs, hs;   /* batch / head strides of the bf16 side (elements) */
+  uint32_t rows, cols, ld, heads;
+  uint32_t slices;   /* batch * heads */
+  uint32_t vec;      /* 1: bf16 rows are 16-byte aligned (8-element loads / stores) */
+} BwppConvArgs;
+
 /* Grad ops and elementwise glue (grad.hip). */
 typedef struct {
   const float *a;   /* x, y or the left operand */

@@ -349,6 +349,11 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
   // O = O^T / l, staged through LDS ([query][d] bf16 per wave), then stored
   // with 16-byte row chunks.
   uint16_t *os = reinterpret_cast<uint16_t *>(smem) + (size_t)wave * kQW * D;
+  // Natural-log log-sum-exp of the scaled scores when asked for: the sum of
+  // exp(scale s) is 2^mrow * lrow (mrow in log2 units).
+  if (a.lse && lh == 0 && qi < a.M)
+    a.lse[(size_t)bh * a.M + qi] =
+        lrow > 0.0f ? ((mrow == -INFINITY ? 0.0f : mrow) + log2f(lrow)) * 0.69314718055994531f : -INFINITY;
   {
     const float inv = lrow > 0.0f ? 1.0f / lrow : 0.0f;
 #pragma unroll

@@ -468,3 +468,65 @@ BWPP_ATTN_F32(64, false, )
 BWPP_ATTN_F32(64, true, _causal)
 BWPP_ATTN_F32(128, false, )
 BWPP_ATTN_F32(128, true, _causal)
+
+// bf16 <-> fp32 operand copies for running bf16 attention backward on the
+// fp32 kernels above: element (slice, r, c) of the strided bf16 tensor <->
+// element [(slice * rows + r) * cols + c] of the fp32 buffer.  Eight columns
+// per thread (cols is a multiple of 8 here); fp32 -> bf16 rounds to nearest
+// even.
+__device__ __forceinline__ size_t conv_src(const BwppConvArgs &a, uint32_t sl, uint32_t r, uint32_t c) {
+  return (size_t)(sl / a.heads) * a.bs + (size_t)(sl % a.heads) * a.hs + (size_t)r * a.ld + c;
+}
+
+extern "C" __global__ __launch_bounds__(256) void bwpp_attn_conv_bf16_to_f32(const BwppConvArgs a) {
+  const uint32_t c8 = a.cols / 8;
+  const size_t total = (size_t)a.slices * a.rows * c8;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+    const uint32_t c = (uint32_t)(i % c8) * 8;
+    const size_t sr = i / c8;
+    const uint32_t r = (uint32_t)(sr % a.rows), sl = (uint32_t)(sr / a.rows);
+    const uint16_t *src = static_cast<const uint16_t *>(a.src) + conv_src(a, sl, r, c);
+    float4 lo, hi;
+    if (a.vec) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(src);
+      lo = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+                       __uint_as_float(v.y & 0xffff0000u));
+      hi = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u), __uint_as_float(v.w << 16),
+                       __uint_as_float(v.w & 0xffff0000u));
+    } else {
+      lo = make_float4(bf16_bits_to_f32(src[0]), bf16_bits_to_f32(src[1]), bf16_bits_to_f32(src[2]),
+                       bf16_bits_to_f32(src[3]));
+      hi = make_float4(bf16_bits_to_f32(src[4]), bf16_bits_to_f32(src[5]), bf16_bits_to_f32(src[6]),
+                       bf16_bits_to_f32(src[7]));
+    }
+    float *dst = static_cast<float *>(a.dst) + sr * a.cols + c;
+    *reinterpret_cast<float4 *>(dst) = lo;
+    *reinterpret_cast<float4 *>(dst + 4) = hi;
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void bwpp_attn_conv_f32_to_bf16(const BwppConvArgs a) {
+  const uint32_t c8 = a.cols / 8;
+  const size_t total = (size_t)a.slices * a.rows * c8;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+    const uint32_t c = (uint32_t)(i % c8) * 8;
+    const size_t sr = i / c8;
+    const uint32_t r = (uint32_t)(sr % a.rows), sl = (uint32_t)(sr / a.rows);
+    const float *src = static_cast<const float *>(a.src) + sr * a.cols + c;
+    const float4 lo = *reinterpret_cast<const float4 *>(src);
+    const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+    const uint4 w = make_uint4(pack_bf16x2(lo.x, lo.y), pack_bf16x2(lo.z, lo.w), pack_bf16x2(hi.x, hi.y),
+                               pack_bf16x2(hi.z, hi.w));
+    uint16_t *dst = static_cast<uint16_t *>(a.dst) + conv_src(a, sl, r, c);
+    if (a.vec) {
+      *reinterpret_cast<uint4 *>(dst) = w;
+    } else {
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        dst[2 * e] = (uint16_t)(ws[e] & 0xffffu);
+        dst[2 * e + 1] = (uint16_t)(ws[e] >> 16);
+      }
+    }
+  }
+}

@@ -85,6 +85,7 @@ struct BwppHip {
   hipFunction_t attn_bwd_dkdv[2][2] = {};
   // fp32 MFMA attention, head dim 64 / 128: [d128][causal]
   hipFunction_t attn_f32_fwd[2][2] = {}, attn_f32_dq[2][2] = {}, attn_f32_dkdv[2][2] = {};
+  hipFunction_t attn_conv_to_f32 = nullptr, attn_conv_to_bf16 = nullptr;  // bf16 <-> fp32 operand copies
   hipFunction_t rmsnorm_grad_w[4] = {};  // wave-per-row rmsnorm_grad, 256 / 512 / 1024 / 2048 columns
   hipFunction_t silu_grad = nullptr, softmax_grad = nullptr, rmsnorm_grad = nullptr, col_partials_sum = nullptr,
                 reduce_sum_rows = nullptr, reduce_sum_cols = nullptr, elementwise = nullptr;
@@ -154,6 +155,7 @@ BwppHipStatus resolve_all(BwppHip *h) {
       {"bwpp_elementwise", &h->elementwise},         {"bwpp_gemm_f32_splitk_reduce", &h->gemm_f32_reduce},
       {"bwpp_rmsnorm_grad_w1", &h->rmsnorm_grad_w[0]}, {"bwpp_rmsnorm_grad_w2", &h->rmsnorm_grad_w[1]},
       {"bwpp_rmsnorm_grad_w4", &h->rmsnorm_grad_w[2]}, {"bwpp_rmsnorm_grad_w8", &h->rmsnorm_grad_w[3]},
+      {"bwpp_attn_conv_bf16_to_f32", &h->attn_conv_to_f32}, {"bwpp_attn_conv_f32_to_bf16", &h->attn_conv_to_bf16},
   };
   for (auto &e : singles)
     if ((s = resolve(h, e.name, e.slot)) != BWPP_HIP_OK) return s;
@@ -795,9 +797,8 @@ BwppHipStatus attn_forward(BwppHip *h, const void *q, const void *k, const void 
   const int causal = p.causal ? 1 : 0;
   const bool bf16 = p.dtype == BWPP_HIP_BF16;
   // The flash kernel takes the row maximum of the raw scores and scales it
-  // afterwards, which needs a positive scale (finite: NaN / inf go generic);
-  // it does not write the log-sum-exp.
-  const bool flash = !lse && bf16 && p.K == 128 && p.D == 128 && p.N > 0 && scale > 0.0f && scale < INFINITY &&
+  // afterwards, which needs a positive scale (finite: NaN / inf go generic).
+  const bool flash = bf16 && p.K == 128 && p.D == 128 && p.N > 0 && scale > 0.0f && scale < INFINITY &&
                      aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) && g.ldq % 8 == 0 &&
                      g.ldk % 8 == 0 && g.ldv % 8 == 0 && g.ldo % 8 == 0 && g.q_bs % 8 == 0 && g.q_hs % 8 == 0 &&
                      g.k_bs % 8 == 0 && g.k_hs % 8 == 0 && g.v_bs % 8 == 0 && g.v_hs % 8 == 0 &&
@@ -807,6 +808,7 @@ BwppHipStatus attn_forward(BwppHip *h, const void *q, const void *k, const void 
                      (uint64_t)(p.N - 1) * g.ldv + p.D < (1ull << 31);
   if (flash) {
     g.scale_log2 = scale * 1.4426950408889634f;
+    g.lse = lse;
     g.q_tiles = (p.M + 255) / 256;
     const uint64_t grid = slices * g.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: grid too large");
@@ -906,21 +908,78 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   g.dk = dk;
   g.dv = dv;
   g.dsum = static_cast<float *>(h->ws);
-  const int f32v = attn_f32_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
-  if (f32v >= 0) {
-    // dQ pass (also writes D_m = rowsum(dO * O)), then the dK / dV pass.
-    g.scale = scale;
-    g.scale_log2 = scale * 1.4426950408889634f;
-    g.q_tiles = (p.M + kF32Rows - 1) / kF32Rows;
-    uint64_t grid = slices * g.q_tiles;
+  // fp32 matrix-core passes: dQ (also writes D_m = rowsum(dO * O)), then
+  // dK / dV.
+  auto run_f32 = [&](BwppAttnArgs f, int variant) -> BwppHipStatus {
+    f.scale = scale;
+    f.scale_log2 = scale * 1.4426950408889634f;
+    f.q_tiles = (p.M + kF32Rows - 1) / kF32Rows;
+    uint64_t grid = slices * f.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
-    if (p.M > 0 && (s = launch(h, h->attn_f32_dq[f32v][causal], (uint32_t)grid, 1, 1, 2 * 64, g)) != BWPP_HIP_OK)
-      return s;
-    g.q_tiles = (p.N + kF32Rows - 1) / kF32Rows;  // key tiles
-    grid = slices * g.q_tiles;
+    BwppHipStatus st;
+    if (p.M > 0 && (st = launch(h, h->attn_f32_dq[variant][causal], (uint32_t)grid, 1, 1, 2 * 64, f)) != BWPP_HIP_OK)
+      return st;
+    f.q_tiles = (p.N + kF32Rows - 1) / kF32Rows;  // key tiles
+    grid = slices * f.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
-    if (p.N > 0) return launch(h, h->attn_f32_dkdv[f32v][causal], (uint32_t)grid, 1, 1, 2 * 64, g);
+    if (p.N > 0) return launch(h, h->attn_f32_dkdv[variant][causal], (uint32_t)grid, 1, 1, 2 * 64, f);
     return BWPP_HIP_OK;
+  };
+  const int f32v = attn_f32_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
+  if (f32v >= 0) return run_f32(g, f32v);
+  if (bf && p.K == p.D && (p.K == 64 || p.K == 128) && std::isfinite(scale)) {
+    // bf16 with head dim 64 / 128: fp32 copies of Q, K, V, O, dO in the
+    // workspace go through the fp32 matrix-core passes, and dQ, dK, dV are
+    // rounded back into the caller's bf16 layout.
+    const uint64_t D = p.D, nq = slices * p.M * D, nk = slices * p.N * D;
+    if ((s = ensure_ws(h, (4 * nq + 4 * nk + slices * p.M) * sizeof(float))) != BWPP_HIP_OK) return s;
+    float *w = static_cast<float *>(h->ws);
+    float *q32 = w, *o32 = q32 + nq, *do32 = o32 + nq, *dq32 = do32 + nq;
+    float *k32 = dq32 + nq, *v32 = k32 + nk, *dk32 = v32 + nk, *dv32 = dk32 + nk, *ds32 = dv32 + nk;
+    auto conv = [&](const void *src, void *dst, uint32_t rows, uint32_t ld, uint64_t bs, uint64_t hs,
+                    bool to_bf16) -> BwppHipStatus {
+      if (rows == 0) return BWPP_HIP_OK;
+      BwppConvArgs c = {};
+      c.src = src;
+      c.dst = dst;
+      c.bs = bs;
+      c.hs = hs;
+      c.rows = rows;
+      c.cols = (uint32_t)D;
+      c.ld = ld;
+      c.heads = H;
+      c.slices = (uint32_t)slices;
+      c.vec = (aligned16(to_bf16 ? dst : src) && ld % 8 == 0 && bs % 8 == 0 && hs % 8 == 0) ? 1u : 0u;
+      const uint64_t total = slices * rows * (D / 8);
+      const uint64_t grid = std::min<uint64_t>((total + 255) / 256, h->cus > 0 ? 8ull * (uint64_t)h->cus : 2048ull);
+      return launch(h, to_bf16 ? h->attn_conv_to_bf16 : h->attn_conv_to_f32, (uint32_t)grid, 1, 1, 256, c);
+    };
+    if ((s = conv(q, q32, p.M, g.ldq, g.q_bs, g.q_hs, false)) != BWPP_HIP_OK ||
+        (s = conv(k, k32, p.N, g.ldk, g.k_bs, g.k_hs, false)) != BWPP_HIP_OK ||
+        (s = conv(v, v32, p.N, g.ldv, g.v_bs, g.v_hs, false)) != BWPP_HIP_OK ||
+        (s = conv(o, o32, p.M, g.ldo, g.o_bs, g.o_hs, false)) != BWPP_HIP_OK ||
+        (s = conv(dout, do32, p.M, g.ldo, g.o_bs, g.o_hs, false)) != BWPP_HIP_OK)
+      return s;
+    BwppAttnArgs f = g;
+    f.q = q32;
+    f.k = k32;
+    f.v = v32;
+    f.o = o32;
+    f.dout = do32;
+    f.dq = dq32;
+    f.dk = dk32;
+    f.dv = dv32;
+    f.dsum = ds32;
+    f.ldq = f.ldk = f.ldv = f.ldo = (uint32_t)D;
+    f.q_hs = f.o_hs = p.M * D;
+    f.q_bs = f.o_bs = (uint64_t)H * p.M * D;
+    f.k_hs = f.v_hs = p.N * D;
+    f.k_bs = f.v_bs = (uint64_t)H * p.N * D;
+    if ((s = run_f32(f, D == 128 ? 1 : 0)) != BWPP_HIP_OK) return s;
+    if ((s = conv(dq32, dq, p.M, g.ldq, g.q_bs, g.q_hs, true)) != BWPP_HIP_OK ||
+        (s = conv(dk32, dk, p.N, g.ldk, g.k_bs, g.k_hs, true)) != BWPP_HIP_OK)
+      return s;
+    return conv(dv32, dv, p.N, g.ldv, g.v_bs, g.v_hs, true);
   }
   if (p.M > 0) {
     g.q_tiles = (p.M + 15) / 16;

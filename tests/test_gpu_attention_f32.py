@@ -161,3 +161,42 @@ def test_packed_views(be, oracle, B, T, H, dh, ld_pad, check):
         assert rel_max_err(gq[b, h], wq[0, 0]) <= TOL
         assert rel_max_err(gk[b, h], wk[0, 0]) <= TOL
         assert rel_max_err(gv[b, h], wv[0, 0]) <= TOL
+
+
+def _bf16_dev(x):
+    torch = _torch()
+    bits = synth.to_bf16_bits(np.ascontiguousarray(x, np.float32))
+    return torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16), synth.bf16_bits_to_f32(bits)
+
+
+def _bf16_host(t):
+    torch = _torch()
+    torch.cuda.synchronize()
+    return synth.bf16_bits_to_f32(t.view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+@pytest.mark.parametrize("B,H,M,N,D", [(1, 2, 97, 200, 64), (2, 1, 130, 130, 128), (1, 1, 190, 65, 128),
+                                       (1, 2, 256, 256, 128)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_grad_through_f32_passes(be, oracle, B, H, M, N, D, causal):
+    """bf16 storage, head dim 64 / 128: the forward saves lse (the flash
+    kernel at d = 128), the backward runs the fp32 matrix-core passes on
+    fp32 copies and rounds dQ, dK, dV to bf16.  Bar 2e-2 against the
+    oracle on the exact bf16 input values."""
+    torch = _torch()
+    seed = B * 100 + M + N
+    (qd, q), (kd, k), (vd, v) = (_bf16_dev(synth.normal(s, seed, i)) for i, s in
+                                 enumerate([(B, H, M, D), (B, H, N, D), (B, H, N, D)]))
+    dod, dout = _bf16_dev(synth.normal((B, H, M, D), seed, 3))
+    scale = 1.0 / np.sqrt(D)
+    prm = bwpp.AttentionParams(M=M, N=N, K=D, D=D, ldq=D, ldk=D, ldv=D, ldo=D, batch=B, heads=H,
+                               scale=scale, causal=int(causal), dtype=int(bwpp.DType.BF16))
+    o = torch.empty((B, H, M, D), dtype=torch.bfloat16, device="cuda")
+    lse = torch.full((B, H, M), 5.0, device="cuda")
+    be.dispatch_attention_lse(qd, kd, vd, o, lse, prm)
+    _check_lse(host(lse), oracle.attention_lse(q, k, scale, causal))
+    assert rel_max_err(_bf16_host(o), oracle.attention_bh(q, k, v, scale, causal)) <= 2e-2
+    dq, dk, dv = (torch.full_like(t, 7.0) for t in (qd, kd, vd))
+    be.dispatch_attention_grad(qd, kd, vd, o, dod, lse, dq, dk, dv, prm)
+    for got, want in zip((dq, dk, dv), oracle.attention_grad(q, k, v, dout, scale, causal)):
+        assert rel_max_err(_bf16_host(got), want) <= 2e-2
