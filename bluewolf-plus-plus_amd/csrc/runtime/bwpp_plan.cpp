@@ -315,10 +315,13 @@ bool planned(Kind k) { return k == Kind::kTemp || k == Kind::kOutput || k == Kin
 // buffers; temps reuse a released buffer of the same dtype and byte size.
 BwppHipStatus plan_memory(BwppHipPlan &p) {
   const int nops = (int)p.ops.size();
+  std::vector<int> first_read(p.values.size(), -1);
   for (int i = 0; i < nops; ++i) {
     for (int v : p.ops[i].ins) {
-      Value &o = p.values[owner(p, v)];
+      const int oi = owner(p, v);
+      Value &o = p.values[oi];
       o.last_use = i;
+      if (first_read[oi] < 0) first_read[oi] = i;
     }
     for (int v : p.ops[i].outs) {
       Value &o = p.values[owner(p, v)];
@@ -332,6 +335,9 @@ BwppHipStatus plan_memory(BwppHipPlan &p) {
     const Value &v = p.values[i];
     if (v.kind == Kind::kTemp && v.first_def < 0 && v.last_use >= 0)
       return perr(&p, BWPP_HIP_ERR_INVALID_ARG, "'%s' is read but never written", v.name.c_str());
+    if ((v.kind == Kind::kTemp || v.kind == Kind::kOutput) && first_read[i] >= 0 && first_read[i] < v.first_def)
+      return perr(&p, BWPP_HIP_ERR_INVALID_ARG, "'%s' is read (line %d) before it is written", v.name.c_str(),
+                  p.ops[first_read[i]].line);
   }
   std::vector<int> free_list;
   auto bytes_of = [](const Value &v) { return v.elems() * (v.dtype == BWPP_HIP_BF16 ? 2 : 4); };
@@ -362,13 +368,17 @@ BwppHipStatus plan_memory(BwppHipPlan &p) {
       const int o = owner(p, v);
       if (planned(p.values[o].kind)) take(o);
     }
-    for (int v : p.ops[i].ins) {
-      const int o = owner(p, v);
-      Value &val = p.values[o];
-      if (val.kind == Kind::kTemp && val.last_use == i && val.buffer >= 0 &&
-          std::find(free_list.begin(), free_list.end(), val.buffer) == free_list.end())
-        free_list.push_back(val.buffer);
-    }
+    // Release temps whose last use is this op: inputs read for the last
+    // time, and outputs nothing reads later (after this op's outputs have
+    // their buffers, so none of them shares a buffer with its own inputs).
+    for (const std::vector<int> *list : {&p.ops[i].ins, &p.ops[i].outs})
+      for (int v : *list) {
+        const int o = owner(p, v);
+        Value &val = p.values[o];
+        if (val.kind == Kind::kTemp && val.last_use == i && val.buffer >= 0 &&
+            std::find(free_list.begin(), free_list.end(), val.buffer) == free_list.end())
+          free_list.push_back(val.buffer);
+      }
   }
   size_t off = 0;
   for (Buffer &b : p.buffers) {
@@ -490,6 +500,26 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
   };
   const std::string &k = op.kind;
   BwppHipStatus s = BWPP_HIP_OK;
+  // dtypes: matmul and attention take f32 or bf16 operands of one dtype
+  // (lse is f32); every other operator is f32 only.
+  {
+    auto dt = [&](int i) { return val(i).dtype; };
+    if (k == "matmul" || k == "attention" || k == "attention_grad") {
+      const uint32_t d0 = dt(op.ins[0]);
+      const bool att = k != "matmul";
+      for (size_t j = 0; j < op.ins.size(); ++j)
+        if (!(k == "attention_grad" && j == 5) && dt(op.ins[j]) != d0) return bad("operands of different dtypes");
+      for (size_t j = 0; j < op.outs.size(); ++j) {
+        const bool lse = att && k == "attention" && j == 1;
+        if (dt(op.outs[j]) != (lse ? (uint32_t)BWPP_HIP_F32 : d0)) return bad("output dtype does not match");
+      }
+      if (k == "attention_grad" && op.ins.size() > 5 && dt(op.ins[5]) != BWPP_HIP_F32) return bad("lse must be f32");
+    } else {
+      for (const std::vector<int> *list : {&op.ins, &op.outs})
+        for (int v : *list)
+          if (dt(v) != BWPP_HIP_F32) return bad("this operator takes f32 values only");
+    }
+  }
   if (k == "matmul") {
     if (!need(2, 1)) return bad("in=A,B[,bias] out=C");
     const Value &A = val(op.ins[0]), &B = val(op.ins[1]), &C = val(op.outs[0]);

@@ -87,3 +87,49 @@ def test_plan_unbound_input_is_an_error(be):
         p.run()
     assert "not bound" in str(e.value)
     p.close()
+
+
+def test_bf16_projection_attention_plan(be, oracle):
+    """A bf16 plan: qkv = x W (bf16 GEMM), causal attention on its column
+    views with the lse saved; against the oracle on the exact bf16 values
+    (qkv rounded to bf16 as the GEMM stores it).  Bar 2e-2."""
+    import torch
+    B, T, H, dh = 2, 96, 2, 128
+    D = H * dh
+    text = f"""bwpp.plan 1
+dim BT {B * T}
+dim D {D}
+dim D3 {3 * D}
+value x bf16 [BT,D] input
+value w bf16 [D,D3] param
+value qkv bf16 [BT,D3] temp
+op matmul out=qkv in=x,w
+view q of=qkv offset=0 ld=D3 shape=[BT,D]
+view k of=qkv offset=D ld=D3 shape=[BT,D]
+view v of=qkv offset=2*D ld=D3 shape=[BT,D]
+value o bf16 [BT,D] output
+value lse f32 [{B},{H},{T}] output
+op attention out=o,lse in=q,k,v batch={B} heads={H} causal=1 scale=0.125
+"""
+    x = synth.normal((B * T, D), 3, 0)
+    w = synth.normal((D, 3 * D), 3, 1, 0.0, 0.05)
+    xb, wb = synth.to_bf16_bits(x), synth.to_bf16_bits(w)
+    p = plan.Plan(be, text)
+    p.allocate()
+    xd = torch.from_numpy(xb.view(np.int16)).cuda()
+    wd = torch.from_numpy(wb.view(np.int16)).cuda()
+    p.bind("x", xd)
+    p.bind("w", wd)
+    p.run()
+    o = synth.bf16_bits_to_f32(p.host("o", (B * T, D), np.uint16))
+    lse = p.host("lse", (B, H, T))
+    qkv = synth.bf16_bits_to_f32(synth.to_bf16_bits(oracle.matmul(synth.bf16_bits_to_f32(xb),
+                                                                  synth.bf16_bits_to_f32(wb))))
+    heads = lambda part: np.ascontiguousarray(
+        qkv[:, part * D:(part + 1) * D].reshape(B, T, H, dh).transpose(0, 2, 1, 3))
+    q, k, v = heads(0), heads(1), heads(2)
+    want = oracle.attention_bh(q, k, v, 0.125, True).transpose(0, 2, 1, 3).reshape(B * T, D)
+    assert rel_max_err(o, want) <= 2e-2
+    wl = oracle.attention_lse(q, k, 0.125, True)
+    assert np.max(np.abs(lse - wl)) <= 2e-2 * max(1.0, np.abs(wl).max())
+    p.close()

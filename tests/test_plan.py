@@ -67,6 +67,11 @@ _IO = "bwpp.plan 1\nvalue a f32 [4,4] input\nvalue b f32 [4,4] input\nvalue y f3
     ("bwpp.plan 1\nvalue x f32 [4,4] temp\nop softmax out=y in=x\n", "unknown value"),
     ("bwpp.plan 1\nvalue x f32 [4,4] input\nview v of=x offset=8 ld=4 shape=[3,4]\n", "runs past"),
     ("bwpp.plan 1\nvalue x f32 [4,4] temp\nvalue y f32 [4,4] output\nop softmax out=y in=x\n", "never written"),
+    ("bwpp.plan 1\nvalue x f32 [4,4] input\nvalue t f32 [4,4] temp\nvalue y f32 [4,4] output\n"
+     "op softmax out=y in=t\nop softmax out=t in=x\n", "before it is written"),
+    ("bwpp.plan 1\nvalue x bf16 [4,4] input\nvalue y f32 [4,4] output\nop softmax out=y in=x\n", "f32 values only"),
+    ("bwpp.plan 1\nvalue a bf16 [4,4] input\nvalue b f32 [4,4] input\nvalue y bf16 [4,4] output\n"
+     "op matmul out=y in=a,b\n", "different dtypes"),
     # Op arguments are checked when the plan is created, not when it runs.
     (_IO + "op matmul out=y in=a,b epi=gelu\n", "epi must be"),
     (_IO + "op add out=y in=a,b bcast=diag\n", "bcast must be"),
@@ -79,3 +84,12 @@ def test_plan_errors(text, msg):
     with pytest.raises(plan.PlanError) as e:
         plan.Plan(None, text)
     assert msg in str(e.value)
+
+
+def test_dead_temp_buffer_is_reused():
+    """A temp written but never read gives its buffer back after its op."""
+    text = ("bwpp.plan 1\nvalue x f32 [8,8] input\nvalue dead f32 [8,8] temp\nvalue t f32 [8,8] temp\n"
+            "value y f32 [8,8] output\nop softmax out=dead in=x\nop softmax out=t in=x\nop softmax out=y in=t\n")
+    rep = plan.Plan(None, text).report()
+    buf = _buffers(rep)
+    assert buf["dead"] == buf["t"]
