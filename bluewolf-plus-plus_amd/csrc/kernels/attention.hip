@@ -6,8 +6,9 @@
 // a bottom-right aligned causal mask (keys n > m + N - M excluded); the MSL
 // kernel it replaces is codegen_metal.c:435-556.
 //
-// Layout of the work: a block of 8 waves (two per SIMD) owns 256 queries of
-// one (batch, head); each wave owns 32 queries.  Keys stream through LDS in
+// Layout of the work: a block of 8 waves (two per SIMD) owns a tile of 256
+// queries of one (batch, head) (causal: two such tiles, one after the
+// other); each wave owns 32 queries of the tile.  Keys stream through LDS in
 // tiles of 64 (K and V, 16 KiB each for d = 128) in a 4-stage ring filled
 // by global -> LDS DMA.  Two waves per SIMD let one wave's softmax (VALU)
 // run while the other's MFMAs issue; 32 queries per wave keep the
@@ -78,8 +79,9 @@ __device__ __forceinline__ void g2lds16_so(const void *sbase, uint32_t voff, uin
 __device__ __forceinline__ uint32_t k_off(uint32_t r, uint32_t c) { return r * 256u + 16u * (c ^ (r & 15u)); }
 __device__ __forceinline__ uint32_t v_off(uint32_t r, uint32_t c) { return r * 256u + 16u * (c ^ (4u * (r & 3u))); }
 
+// One query tile (256 queries) of one (batch, head) slice.
 template <bool CAUSAL>
-__device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
+__device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const uint32_t bh, const uint32_t qt) {
   constexpr int D = 128;
   constexpr int KS = D / 16;  // k-steps of S over d
   constexpr int DB = D / 32;  // 32-wide d blocks of O^T
@@ -92,9 +94,6 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t nbh = gridDim.x / a.q_tiles;
-  const uint32_t qt = a.q_tiles - 1 - blockIdx.x / nbh;  // heaviest query tiles first
-  const uint32_t bh = blockIdx.x % nbh;
   const uint32_t b = bh / a.heads, h = bh % a.heads;
   const uint16_t *Q = static_cast<const uint16_t *>(a.q) + b * a.q_bs + h * a.q_hs;
   const uint16_t *K = static_cast<const uint16_t *>(a.k) + b * a.k_bs + h * a.k_hs;
@@ -377,6 +376,29 @@ __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
     if (qo < a.M)
       *reinterpret_cast<uint4 *>(O + (size_t)qo * a.ldo + 8u * cc) =
           *reinterpret_cast<const uint4 *>(os + ql * D + 8u * cc);
+  }
+  __syncthreads();  // the block's next tile reuses smem
+}
+
+// Work per block.  Blocks are dispatched round-robin over the 8 XCDs; the
+// renumbering below gives each XCD a contiguous run of (batch, head) slices
+// with all of their query tiles, so the blocks that stream the same K / V
+// run together on one L2.  Unmasked: one query tile per block.  Causal: a
+// block takes query tiles QT - 1 - p and p of one slice, whose visible key
+// counts add up to the same total for every p, so all blocks carry equal
+// work (the runtime launches slices * ceil(QT / 2) blocks).
+template <bool CAUSAL>
+__device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
+  const uint32_t G = gridDim.x, QT = a.q_tiles;
+  const uint32_t lb = G % 8u == 0 ? (blockIdx.x % 8u) * (G / 8u) + blockIdx.x / 8u : blockIdx.x;
+  if (!CAUSAL) {
+    attn_bf16_d128_tile<CAUSAL>(a, lb / QT, QT - 1 - lb % QT);
+    return;
+  }
+  const uint32_t P = (QT + 1) / 2, bh = lb / P, pi = lb % P;
+  for (uint32_t i = 0; i < 2; ++i) {
+    if (i == 1 && QT - 1 - pi == pi) break;
+    attn_bf16_d128_tile<CAUSAL>(a, bh, i == 0 ? QT - 1 - pi : pi);
   }
 }
 

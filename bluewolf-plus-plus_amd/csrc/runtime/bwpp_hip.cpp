@@ -810,7 +810,8 @@ BwppHipStatus attn_forward(BwppHip *h, const void *q, const void *k, const void 
     g.scale_log2 = scale * 1.4426950408889634f;
     g.lse = lse;
     g.q_tiles = (p.M + 255) / 256;
-    const uint64_t grid = slices * g.q_tiles;
+    // Causal blocks take two query tiles each (the longest with the shortest).
+    const uint64_t grid = slices * (causal ? (g.q_tiles + 1) / 2 : g.q_tiles);
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: grid too large");
     return launch(h, h->attn_flash[causal], (uint32_t)grid, 1, 1, 512, g);
   }

@@ -98,7 +98,10 @@ def test_generic_bf16(be, oracle, B, H, M, N, D, causal):
 
 
 @pytest.mark.parametrize("B,H,M,N", [(1, 2, 256, 256), (1, 1, 300, 300), (2, 2, 200, 513), (1, 1, 513, 200),
-                                     (1, 1, 64, 1000), (1, 3, 1024, 1024), (1, 1, 1, 1)])
+                                     (1, 1, 64, 1000), (1, 3, 1024, 1024), (1, 1, 1, 1),
+                                     # odd query-tile count (causal blocks pair tiles 4+0, 3+1, 2 alone);
+                                     # grids that are / are not multiples of the 8 XCDs
+                                     (1, 5, 1280, 1280), (2, 4, 2048, 2048), (1, 1, 1100, 1300)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_flash_bf16_d128(be, oracle, B, H, M, N, causal):
     (qd, kd, vd), (q, k, v) = inputs(B, H, M, N, 128, 128, B * 1000 + M + N, True)
