@@ -436,7 +436,24 @@ def extras(be, torch, seed, iters, with_cpu):
             entry["cpu"] = {"GFLOP_s": round(fl / (B * H) / dt / 1e9, 3), "cores": 1, "kind": "port",
                             "sample": "one (batch, head) slice (extrapolated rate)"}
         out["c4_attention_causal" if causal else "c4_attention"] = entry
-    del q, k, v, o
+    # Attention backward at the C4 shape (bf16 matrix-core dQ and dK/dV
+    # passes after a forward that saves lse): 5 products of 2*S*S*d per
+    # slice (S and dP recomputed, dV, dQ, dK) = 2.5x the forward FLOP.
+    dout = _bf16(torch, synth.normal((B, H, S, d), seed, 3))
+    lse = torch.empty((B, H, S), device="cuda")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    for causal in (0, 1):
+        p = bwpp.AttentionParams(M=S, N=S, K=d, D=d, ldq=d, ldk=d, ldv=d, ldo=d, batch=B, heads=H,
+                                 scale=d ** -0.5, causal=causal, dtype=int(bwpp.DType.BF16))
+        be.dispatch_attention_lse(q, k, v, o, lse, p)
+        us = _events_us(torch, lambda: be.dispatch_attention_grad(q, k, v, o, dout, lse, dq, dk, dv, p),
+                        max(3, iters // 3))
+        fl = 2.5 * (full / 2 if causal else full)
+        out["c4_attention_grad_bf16" + ("_causal" if causal else "")] = {
+            "kernel": "bwpp_attn_bwd_bf16_mfma_d128" + ("_causal" if causal else "") + "_{dq,dkdv}",
+            "us_per_launch": round(us, 1), "TFLOP_s": round(fl / us / 1e6, 1),
+            "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    del q, k, v, o, dout, dq, dk, dv
     out["c5_block_train_f32"] = block_train(be, torch, seed, max(3, iters // 4))
     return out
 

@@ -1,0 +1,424 @@
+// Attention backward on the bf16 matrix cores of gfx950
+// (v_mfma_f32_32x32x16_bf16): bf16 Q, K, V, O, dO and dQ, dK, dV; fp32
+// lse, D_m, softmax and accumulation; head dims K = D in {64, 128}.
+//   p = exp(scale q.k - lse),  D_m = rowsum(dO * O)[m],
+//   dS = p (dO.v - D_m),  dQ = scale dS K,  dK = scale dS^T Q,  dV = P^T dO,
+// with P and dS rounded to bf16 where they enter an MFMA as an operand.
+// Semantics: the closed form of the graph's softmax_grad chain
+// (compiler/graph_ir.c:1722-1733) applied to the attention of
+// runtime/cpu/bwpp_cpu_ref.c:92-144, generalised with a score scale and a
+// bottom-right aligned causal mask (key n visible to query m iff
+// n <= m + N - M).
+//
+// Work layout as in the fp32 kernels: a block is 2 waves, each wave owns
+// 32 rows (queries in the dQ pass, keys in the dK/dV pass) and the block
+// streams 32-row tiles of the other side through a two-stage LDS ring
+// (register prefetch of tile t+1 during tile t, one barrier per tile).
+//
+// MFMA operands (32x32x16 bf16): lane l supplies A[l % 32][8 (l / 32) ..
+// +7] and B[8 (l / 32) .. +7][l % 32]; accumulator register r of lane l is
+// C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+//  - Products over the head dim (S, dP) take the streamed tile's rows as A
+//    (one 16-byte LDS read per lane per k-step) and the wave's own rows as
+//    B, held in registers (query or key l % 32, d = 16 ks + 8 (l / 32)).
+//    The accumulator then gives lane l one row of the wave (l % 32) and 16
+//    rows of the tile: row-wise softmax terms are lane-local.
+//  - Products over the tile's rows (dQ, dK, dV) are computed transposed,
+//    X^T W: W (the probabilities or dS) goes from the accumulator straight
+//    into the B operand, lane half h taking tile rows 4h..4h+3 and
+//    8+4h..8+4h+3 of each 16, and X^T is read from the row-major tile with
+//    ds_read_b64_tr_b16 at exactly those rows.
+// LDS tiles are [32 rows][D] bf16 with 16-byte chunk c of row r stored at
+// chunk c ^ swz(r); swz is a permutation on any 16 consecutive rows (the
+// row reads) and keeps the two chunks of the four rows that a 16-lane
+// group of a transposing read touches apart.
+#include "common.h"
+#include "../kargs.h"
+
+using namespace bwpp;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef short v8s_t __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
+
+namespace {
+
+constexpr int kW = 2;   // waves per block
+constexpr int kR = 32;  // rows per wave and per streamed tile
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ f32x16_t mfma16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float sum32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Tile row of accumulator register r for lane half hi.
+__device__ __forceinline__ int acc_row(int r, int hi) { return 8 * (r >> 2) + 4 * hi + (r & 3); }
+
+template <int D>
+__device__ __forceinline__ uint32_t swz(uint32_t r) {
+  if constexpr (D == 128)
+    return ((r & 3u) << 1) | ((r >> 2) & 1u) | (r & 8u);  // 16 chunks per 256-byte row
+  else
+    return (((r >> 1) & 1u) << 1) | ((r >> 2) & 1u) | (((r >> 3) & 1u) << 2);  // 8 chunks per 128-byte row
+}
+template <int D>
+__device__ __forceinline__ uint32_t toff(uint32_t r, uint32_t c) {
+  return r * (uint32_t)(D * 2) + 16u * (c ^ swz<D>(r));
+}
+
+// Two [kR x D] bf16 tiles (rows r0.., zeros past `rows`) copied by the
+// block from global memory into registers, then into an LDS stage.
+template <int D>
+struct TilePairB {
+  static constexpr int CH = D / 8;                 // 16-byte chunks per row
+  static constexpr int PER = kR * CH / (64 * kW);  // chunks per thread per tile
+  u32x4_t x[PER], y[PER];
+
+  // rows >= 1.  Rows past the end load row rows - 1 and are then zeroed:
+  // no branch around the loads, so they stay in flight across the tile.
+  __device__ __forceinline__ void fetch(const uint16_t *X, uint32_t ldx, const uint16_t *Y, uint32_t ldy,
+                                        uint32_t r0, uint32_t rows) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = (int)threadIdx.x + i * 64 * kW;
+      const uint32_t row = r0 + (uint32_t)(idx / CH), c = (uint32_t)(idx % CH);
+      const uint32_t rr = row < rows ? row : rows - 1;
+      x[i] = *reinterpret_cast<const u32x4_t *>(X + (size_t)rr * ldx + 8u * c);
+      y[i] = *reinterpret_cast<const u32x4_t *>(Y + (size_t)rr * ldy + 8u * c);
+      if (row >= rows) x[i] = y[i] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+  __device__ __forceinline__ void stash(unsigned char *lx, unsigned char *ly) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = (int)threadIdx.x + i * 64 * kW;
+      const uint32_t off = toff<D>((uint32_t)(idx / CH), (uint32_t)(idx % CH));
+      *reinterpret_cast<u32x4_t *>(lx + off) = x[i];
+      *reinterpret_cast<u32x4_t *>(ly + off) = y[i];
+    }
+  }
+};
+
+// The lane's 16-byte pieces of a row: d = 16 ks + 8 hi .. +7, ks < D / 16
+// (zeros past the end; a row past the end loads row rows - 1, when there
+// is one, and discards it).
+template <int D>
+__device__ __forceinline__ void load_row(bf16x8_t (&dst)[D / 16], const uint16_t *X, uint32_t ld, uint32_t row,
+                                         uint32_t rows, int hi) {
+  const uint32_t rr = row < rows ? row : (rows > 0 ? rows - 1 : 0);
+  const bool in = row < rows;
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) {
+    u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+    if (rows > 0) v = *reinterpret_cast<const u32x4_t *>(X + (size_t)rr * ld + 16 * ks + 8 * hi);
+    if (!in) v = u32x4_t{0u, 0u, 0u, 0u};
+    dst[ks] = __builtin_bit_cast(bf16x8_t, v);
+  }
+}
+
+// Per-lane LDS offsets: row reads (tile row li, k-step ks) and the two
+// transposing reads (tile rows 0-7 / 8-15 of a 16-row step) of d block blk.
+template <int D>
+struct Offsets {
+  uint32_t row[D / 16], tlo[D / 32], thi[D / 32];
+  __device__ __forceinline__ Offsets(int lane) {
+    const uint32_t li = (uint32_t)(lane & 31), hi = (uint32_t)(lane >> 5);
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) row[ks] = toff<D>(li, 2u * ks + hi);
+    const uint32_t grp = (uint32_t)((lane >> 4) & 3), L = (uint32_t)(lane & 15);
+    const uint32_t rb = 4u * (grp >> 1) + (L >> 2);
+#pragma unroll
+    for (int blk = 0; blk < D / 32; ++blk) {
+      const uint32_t col = 32u * blk + 16u * (grp & 1u) + 4u * (L & 3u);
+      tlo[blk] = toff<D>(rb, col >> 3) + (col & 7u) * 2u;
+      thi[blk] = toff<D>(rb + 8u, col >> 3) + (col & 7u) * 2u;
+    }
+  }
+};
+
+// A operand X^T (d block blk, tile rows 16 kq .. +15 in the accumulator's
+// row order) from a row-major LDS tile.  16 rows keep swz (it depends on
+// the row's low four bits only).
+template <int D>
+__device__ __forceinline__ bf16x8_t tr_operand(const unsigned char *tile, const Offsets<D> &o, int blk, int kq) {
+  const uint32_t step = (uint32_t)kq * 16u * (uint32_t)(D * 2);
+  const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(tile + o.tlo[blk] + step));
+  const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(tile + o.thi[blk] + step));
+  const v8s_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// B operand from accumulator registers 8 kq .. 8 kq + 7 (rounded to bf16).
+__device__ __forceinline__ bf16x8_t acc_operand(const f32x16_t &w, int kq) {
+  const int r0 = 8 * kq;
+  uint4 u;
+  u.x = pack_bf16x2(w[r0 + 0], w[r0 + 1]);
+  u.y = pack_bf16x2(w[r0 + 2], w[r0 + 3]);
+  u.z = pack_bf16x2(w[r0 + 4], w[r0 + 5]);
+  u.w = pack_bf16x2(w[r0 + 6], w[r0 + 7]);
+  return __builtin_bit_cast(bf16x8_t, u);
+}
+
+// acc = X_tile(rows) . W^T over the head dim: X_tile rows from LDS, W the
+// lane's register pieces.
+template <int D>
+__device__ __forceinline__ f32x16_t dot_rows(const unsigned char *tile, const Offsets<D> &o,
+                                             const bf16x8_t (&w)[D / 16]) {
+  f32x16_t acc = {};
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+    acc = mfma16(__builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(tile + o.row[ks])), w[ks], acc);
+  return acc;
+}
+
+// Stores a transposed accumulator set (register r of out[blk] = element
+// d = 32 blk + acc_row(r, hi) of row `row`) as bf16, times f, 8 bytes a piece.
+template <int D>
+__device__ __forceinline__ void store_t(uint16_t *X, uint32_t ld, uint32_t row, const f32x16_t (&acc)[D / 32],
+                                        float f, int hi) {
+  uint16_t *dst = X + (size_t)row * ld + 4 * hi;
+#pragma unroll
+  for (int blk = 0; blk < D / 32; ++blk)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      uint2 u;
+      u.x = pack_bf16x2(acc[blk][4 * r4] * f, acc[blk][4 * r4 + 1] * f);
+      u.y = pack_bf16x2(acc[blk][4 * r4 + 2] * f, acc[blk][4 * r4 + 3] * f);
+      *reinterpret_cast<uint2 *>(dst + 32 * blk + 8 * r4) = u;
+    }
+}
+
+struct SliceB {
+  uint32_t bh, b, h;
+};
+__device__ __forceinline__ SliceB slice_b(const BwppAttnArgs &a, uint32_t nbh) {
+  SliceB s;
+  s.bh = blockIdx.x % nbh;
+  s.b = s.bh / a.heads;
+  s.h = s.bh % a.heads;
+  return s;
+}
+
+// dQ pass: a wave owns 32 queries and streams K / V tiles; also writes
+// D_m = rowsum(dO * O) for the dK / dV pass.
+template <int D, bool CAUSAL>
+__device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
+  constexpr int DB = D / 32, TB = kR * D * 2;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2][2][TB];  // [stage][K, V]
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const int li = lane & 31, hi = lane >> 5;
+  const uint32_t nbh = gridDim.x / a.q_tiles;
+  const uint32_t qt = a.q_tiles - 1 - blockIdx.x / nbh;  // heaviest (causal) first
+  const SliceB sl = slice_b(a, nbh);
+  const uint16_t *Q = static_cast<const uint16_t *>(a.q) + sl.b * a.q_bs + sl.h * a.q_hs;
+  const uint16_t *K = static_cast<const uint16_t *>(a.k) + sl.b * a.k_bs + sl.h * a.k_hs;
+  const uint16_t *V = static_cast<const uint16_t *>(a.v) + sl.b * a.v_bs + sl.h * a.v_hs;
+  const uint16_t *O = static_cast<const uint16_t *>(a.o) + sl.b * a.o_bs + sl.h * a.o_hs;
+  const uint16_t *dO = static_cast<const uint16_t *>(a.dout) + sl.b * a.o_bs + sl.h * a.o_hs;
+  uint16_t *dQ = static_cast<uint16_t *>(a.dq) + sl.b * a.q_bs + sl.h * a.q_hs;
+  const int64_t diag = (int64_t)a.N - (int64_t)a.M;
+  const uint32_t qb = qt * (kW * kR), q0 = qb + (uint32_t)wave * kR, qi = q0 + (uint32_t)li;
+
+  uint32_t kend = a.N;
+  if (CAUSAL) {
+    const int64_t last = (int64_t)min(a.M, qb + kW * kR) - 1 + diag;
+    kend = last < 0 ? 0u : (uint32_t)min<int64_t>(last + 1, (int64_t)a.N);
+  }
+  const uint32_t nt = (kend + kR - 1) / kR;
+  const int64_t wlast = (int64_t)q0 + kR - 1 + diag;
+
+  bf16x8_t qf[D / 16], gf[D / 16];
+  load_row<D>(qf, Q, a.ldq, qi, a.M, hi);
+  load_row<D>(gf, dO, a.ldo, qi, a.M, hi);
+  float dsum;
+  {
+    bf16x8_t of[D / 16];
+    load_row<D>(of, O, a.ldo, qi, a.M, hi);
+    float part = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part += (float)gf[ks][e] * (float)of[ks][e];
+    dsum = sum32(part);
+  }
+  if (qi < a.M && hi == 0) a.dsum[(size_t)sl.bh * a.M + qi] = dsum;
+  // Queries past M: +inf makes every probability exp2(-inf) = 0.
+  const float lse2 = qi < a.M ? a.lse[(size_t)sl.bh * a.M + qi] * kLog2e : INFINITY;
+  const float c = a.scale_log2;
+  const Offsets<D> off(lane);
+
+  f32x16_t dq[DB];
+#pragma unroll
+  for (int blk = 0; blk < DB; ++blk) dq[blk] = f32x16_t{};
+
+  TilePairB<D> pf;
+  if (nt > 0) {
+    pf.fetch(K, a.ldk, V, a.ldv, 0, a.N);
+    pf.stash(lds[0][0], lds[0][1]);
+  }
+  __syncthreads();
+  for (uint32_t t = 0; t < nt; ++t) {
+    const int st = (int)(t & 1);
+    const uint32_t k0 = t * kR;
+    if (t + 1 < nt) pf.fetch(K, a.ldk, V, a.ldv, k0 + kR, a.N);
+    if (!CAUSAL || (int64_t)k0 <= wlast) {
+      f32x16_t s = dot_rows<D>(lds[st][0], off, qf);         // S^T [key][query]
+      const f32x16_t dp = dot_rows<D>(lds[st][1], off, gf);  // dP^T = V dO^T
+      const bool edge = k0 + kR > a.N || (CAUSAL && (int64_t)k0 + kR - 1 > (int64_t)q0 + diag);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = __builtin_amdgcn_exp2f(s[r] * c - lse2);
+        if (edge) {
+          const uint32_t key = k0 + (uint32_t)acc_row(r, hi);
+          if (key >= a.N || (CAUSAL && (int64_t)key > (int64_t)qi + diag)) p = 0.0f;
+        }
+        s[r] = p * (dp[r] - dsum);  // dS^T
+      }
+#pragma unroll
+      for (int kq = 0; kq < 2; ++kq) {
+        const bf16x8_t w = acc_operand(s, kq);
+#pragma unroll
+        for (int blk = 0; blk < DB; ++blk) dq[blk] = mfma16(tr_operand<D>(lds[st][0], off, blk, kq), w, dq[blk]);
+      }
+    }
+    if (t + 1 < nt) pf.stash(lds[st ^ 1][0], lds[st ^ 1][1]);
+    __syncthreads();
+  }
+  if (qi < a.M) store_t<D>(dQ, a.ldq, qi, dq, a.scale, hi);
+}
+
+// dK / dV pass: a wave owns 32 keys and streams Q / dO tiles with their
+// lse and D_m.
+template <int D, bool CAUSAL>
+__device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
+  constexpr int DB = D / 32, TB = kR * D * 2;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2][2][TB];  // [stage][Q, dO]
+  __shared__ __attribute__((aligned(16))) float rowv[2][2][kR];          // [stage][lse2, D_m]
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const int li = lane & 31, hi = lane >> 5;
+  const uint32_t nbh = gridDim.x / a.q_tiles;  // q_tiles holds the key tiles here
+  const uint32_t kt = blockIdx.x / nbh;          // heaviest (causal) first
+  const SliceB sl = slice_b(a, nbh);
+  const uint16_t *Q = static_cast<const uint16_t *>(a.q) + sl.b * a.q_bs + sl.h * a.q_hs;
+  const uint16_t *K = static_cast<const uint16_t *>(a.k) + sl.b * a.k_bs + sl.h * a.k_hs;
+  const uint16_t *V = static_cast<const uint16_t *>(a.v) + sl.b * a.v_bs + sl.h * a.v_hs;
+  const uint16_t *dO = static_cast<const uint16_t *>(a.dout) + sl.b * a.o_bs + sl.h * a.o_hs;
+  uint16_t *dK = static_cast<uint16_t *>(a.dk) + sl.b * a.k_bs + sl.h * a.k_hs;
+  uint16_t *dV = static_cast<uint16_t *>(a.dv) + sl.b * a.v_bs + sl.h * a.v_hs;
+  const float *lse = a.lse + (size_t)sl.bh * a.M;
+  const float *dsum = a.dsum + (size_t)sl.bh * a.M;
+  const int64_t diag = (int64_t)a.N - (int64_t)a.M;
+  const uint32_t kb = kt * (kW * kR), k0w = kb + (uint32_t)wave * kR, ni = k0w + (uint32_t)li;
+
+  // Queries that see a key n: m >= n - diag (causal).
+  uint32_t mbeg = 0;
+  if (CAUSAL) {
+    const int64_t first = (int64_t)kb - diag;
+    mbeg = first <= 0 ? 0u : (first >= (int64_t)a.M ? a.M : (uint32_t)first);
+    mbeg -= mbeg % kR;
+  }
+  const uint32_t nt = a.M > mbeg ? (a.M - mbeg + kR - 1) / kR : 0u;
+  const int64_t wfirst = (int64_t)k0w - diag;  // first query that sees any key of the wave
+
+  bf16x8_t kf[D / 16], vf[D / 16];
+  load_row<D>(kf, K, a.ldk, ni, a.N, hi);
+  load_row<D>(vf, V, a.ldv, ni, a.N, hi);
+  f32x16_t dk[DB], dv[DB];
+#pragma unroll
+  for (int blk = 0; blk < DB; ++blk) dk[blk] = dv[blk] = f32x16_t{};
+  const float c = a.scale_log2;
+  const Offsets<D> off(lane);
+
+  TilePairB<D> pf;
+  float rl = INFINITY, rd = 0.0f;  // lse2 / D_m of row threadIdx.x (< kR)
+  auto fetch_rows = [&](uint32_t m0) {
+    if (threadIdx.x < (uint32_t)kR) {
+      const uint32_t m = m0 + threadIdx.x;
+      rl = m < a.M ? lse[m] * kLog2e : INFINITY;
+      rd = m < a.M ? dsum[m] : 0.0f;
+    }
+  };
+  auto stash_rows = [&](int st) {
+    if (threadIdx.x < (uint32_t)kR) {
+      rowv[st][0][threadIdx.x] = rl;
+      rowv[st][1][threadIdx.x] = rd;
+    }
+  };
+  if (nt > 0) {
+    pf.fetch(Q, a.ldq, dO, a.ldo, mbeg, a.M);
+    fetch_rows(mbeg);
+    pf.stash(lds[0][0], lds[0][1]);
+    stash_rows(0);
+  }
+  __syncthreads();
+  for (uint32_t t = 0; t < nt; ++t) {
+    const int st = (int)(t & 1);
+    const uint32_t m0 = mbeg + t * kR;
+    if (t + 1 < nt) {
+      pf.fetch(Q, a.ldq, dO, a.ldo, m0 + kR, a.M);
+      fetch_rows(m0 + kR);
+    }
+    if (!CAUSAL || (int64_t)m0 + kR - 1 >= wfirst) {
+      f32x16_t s = dot_rows<D>(lds[st][0], off, kf);         // S [query][key]
+      const f32x16_t dp = dot_rows<D>(lds[st][1], off, vf);  // dP = dO V^T
+      const bool edge = CAUSAL && (int64_t)m0 < wfirst + kR - 1;
+      f32x16_t ds;
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int row = 8 * r4 + 4 * hi;
+        const f32x4_t l4 = *reinterpret_cast<const f32x4_t *>(&rowv[st][0][row]);
+        const f32x4_t d4 = *reinterpret_cast<const f32x4_t *>(&rowv[st][1][row]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * r4 + e;
+          float p = __builtin_amdgcn_exp2f(s[r] * c - l4[e]);
+          if (edge && (int64_t)ni > (int64_t)(m0 + (uint32_t)(row + e)) + diag) p = 0.0f;
+          s[r] = p;
+          ds[r] = p * (dp[r] - d4[e]);
+        }
+      }
+#pragma unroll
+      for (int kq = 0; kq < 2; ++kq) {
+        const bf16x8_t wp = acc_operand(s, kq), wd = acc_operand(ds, kq);
+#pragma unroll
+        for (int blk = 0; blk < DB; ++blk) {
+          dv[blk] = mfma16(tr_operand<D>(lds[st][1], off, blk, kq), wp, dv[blk]);  // dV^T += dO^T P
+          dk[blk] = mfma16(tr_operand<D>(lds[st][0], off, blk, kq), wd, dk[blk]);  // dK^T += Q^T dS
+        }
+      }
+    }
+    if (t + 1 < nt) {
+      pf.stash(lds[st ^ 1][0], lds[st ^ 1][1]);
+      stash_rows(st ^ 1);
+    }
+    __syncthreads();
+  }
+  if (ni < a.N) {
+    store_t<D>(dK, a.ldk, ni, dk, a.scale, hi);
+    store_t<D>(dV, a.ldv, ni, dv, 1.0f, hi);
+  }
+}
+
+}  // namespace
+
+#define BWPP_ATTN_BWD_BF16(D, CAUSAL, SUFFIX)                                                   \
+  extern "C" __global__ __launch_bounds__(64 * kW) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dq( \
+      const BwppAttnArgs a) {                                                                   \
+    bwd_dq<D, CAUSAL>(a);                                                                       \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(64 * kW) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dkdv( \
+      const BwppAttnArgs a) {                                                                   \
+    bwd_dkdv<D, CAUSAL>(a);                                                                     \
+  }
+
+BWPP_ATTN_BWD_BF16(64, false, )
+BWPP_ATTN_BWD_BF16(64, true, _causal)
+BWPP_ATTN_BWD_BF16(128, false, )
+BWPP_ATTN_BWD_BF16(128, true, _causal)

@@ -32,7 +32,7 @@ thread_local std::string g_create_error;
 
 // Code objects built by the package Makefile, all required.
 const char *const kModules[] = {"bwpp_rowops.hsaco", "bwpp_gemm.hsaco", "bwpp_attention.hsaco",
-                                 "bwpp_attention_f32.hsaco", "bwpp_grad.hsaco"};
+                                 "bwpp_attention_f32.hsaco", "bwpp_attention_bwd.hsaco", "bwpp_grad.hsaco"};
 
 // Row-op kernels: bwpp_row_<op>_v<VPT>_w<WPR>_<f|p>, see rowops.hip.
 enum RowOpId { ROW_SOFTMAX, ROW_RMSNORM, ROW_LAYERNORM, ROW_MAX, ROW_MAXGRAD, ROW_MASK, ROW_NOPS };
@@ -85,6 +85,8 @@ struct BwppHip {
   hipFunction_t attn_bwd_dkdv[2][2] = {};
   // fp32 MFMA attention, head dim 64 / 128: [d128][causal]
   hipFunction_t attn_f32_fwd[2][2] = {}, attn_f32_dq[2][2] = {}, attn_f32_dkdv[2][2] = {};
+  // bf16 MFMA attention backward, head dim 64 / 128: [d128][causal]
+  hipFunction_t attn_bf16_dq[2][2] = {}, attn_bf16_dkdv[2][2] = {};
   hipFunction_t attn_conv_to_f32 = nullptr, attn_conv_to_bf16 = nullptr;  // bf16 <-> fp32 operand copies
   hipFunction_t rmsnorm_grad_w[4] = {};  // wave-per-row rmsnorm_grad, 256 / 512 / 1024 / 2048 columns
   hipFunction_t silu_grad = nullptr, softmax_grad = nullptr, rmsnorm_grad = nullptr, col_partials_sum = nullptr,
@@ -187,6 +189,11 @@ BwppHipStatus resolve_all(BwppHip *h) {
       if ((s = resolve(h, "bwpp_attn_bwd_f32_mfma_d" + dn + "_dq", &h->attn_f32_dq[d128][causal])) != BWPP_HIP_OK)
         return s;
       if ((s = resolve(h, "bwpp_attn_bwd_f32_mfma_d" + dn + "_dkdv", &h->attn_f32_dkdv[d128][causal])) !=
+          BWPP_HIP_OK)
+        return s;
+      if ((s = resolve(h, "bwpp_attn_bwd_bf16_mfma_d" + dn + "_dq", &h->attn_bf16_dq[d128][causal])) != BWPP_HIP_OK)
+        return s;
+      if ((s = resolve(h, "bwpp_attn_bwd_bf16_mfma_d" + dn + "_dkdv", &h->attn_bf16_dkdv[d128][causal])) !=
           BWPP_HIP_OK)
         return s;
     }
@@ -783,6 +790,20 @@ int attn_f32_variant(const BwppAttentionParams &p, const BwppAttnArgs &g, float 
   return p.K == 128 ? 1 : 0;
 }
 
+// Variant of the bf16 MFMA attention backward for these arguments (0: head
+// dim 64, 1: 128), or -1: K = D in {64, 128}, a finite scale and 16-byte
+// rows (pointers, leading dims and slice strides in multiples of 8 bf16).
+int attn_bf16_bwd_variant(const BwppAttentionParams &p, const BwppAttnArgs &g, float scale,
+                          std::initializer_list<const void *> ptrs) {
+  if (p.dtype != BWPP_HIP_BF16 || p.K != p.D || (p.K != 64 && p.K != 128) || !std::isfinite(scale)) return -1;
+  for (const void *x : ptrs)
+    if (!aligned16(x)) return -1;
+  for (uint64_t v : {(uint64_t)g.ldq, (uint64_t)g.ldk, (uint64_t)g.ldv, (uint64_t)g.ldo, g.q_bs, g.q_hs, g.k_bs,
+                     g.k_hs, g.v_bs, g.v_hs, g.o_bs, g.o_hs})
+    if (v % 8 != 0) return -1;
+  return p.K == 128 ? 1 : 0;
+}
+
 constexpr uint32_t kF32Rows = 64;  // queries (keys) per block of the fp32 MFMA kernels: 2 waves x 32
 
 BwppHipStatus attn_forward(BwppHip *h, const void *q, const void *k, const void *v, void *o, float *lse,
@@ -909,29 +930,31 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   g.dk = dk;
   g.dv = dv;
   g.dsum = static_cast<float *>(h->ws);
-  // fp32 matrix-core passes: dQ (also writes D_m = rowsum(dO * O)), then
-  // dK / dV.
-  auto run_f32 = [&](BwppAttnArgs f, int variant) -> BwppHipStatus {
+  // Matrix-core passes (fp32 or bf16 kernels, same grids): dQ (also writes
+  // D_m = rowsum(dO * O)), then dK / dV.
+  auto run_mfma = [&](BwppAttnArgs f, hipFunction_t fdq, hipFunction_t fdkdv) -> BwppHipStatus {
     f.scale = scale;
     f.scale_log2 = scale * 1.4426950408889634f;
     f.q_tiles = (p.M + kF32Rows - 1) / kF32Rows;
     uint64_t grid = slices * f.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
     BwppHipStatus st;
-    if (p.M > 0 && (st = launch(h, h->attn_f32_dq[variant][causal], (uint32_t)grid, 1, 1, 2 * 64, f)) != BWPP_HIP_OK)
-      return st;
+    if (p.M > 0 && (st = launch(h, fdq, (uint32_t)grid, 1, 1, 2 * 64, f)) != BWPP_HIP_OK) return st;
     f.q_tiles = (p.N + kF32Rows - 1) / kF32Rows;  // key tiles
     grid = slices * f.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
-    if (p.N > 0) return launch(h, h->attn_f32_dkdv[variant][causal], (uint32_t)grid, 1, 1, 2 * 64, f);
+    if (p.N > 0) return launch(h, fdkdv, (uint32_t)grid, 1, 1, 2 * 64, f);
     return BWPP_HIP_OK;
   };
   const int f32v = attn_f32_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
-  if (f32v >= 0) return run_f32(g, f32v);
+  if (f32v >= 0) return run_mfma(g, h->attn_f32_dq[f32v][causal], h->attn_f32_dkdv[f32v][causal]);
+  const int bf16v = attn_bf16_bwd_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
+  if (bf16v >= 0) return run_mfma(g, h->attn_bf16_dq[bf16v][causal], h->attn_bf16_dkdv[bf16v][causal]);
   if (bf && p.K == p.D && (p.K == 64 || p.K == 128) && std::isfinite(scale)) {
-    // bf16 with head dim 64 / 128: fp32 copies of Q, K, V, O, dO in the
-    // workspace go through the fp32 matrix-core passes, and dQ, dK, dV are
-    // rounded back into the caller's bf16 layout.
+    // bf16 with head dim 64 / 128 whose rows are not 16-byte aligned: fp32
+    // copies of Q, K, V, O, dO in the workspace go through the fp32
+    // matrix-core passes, and dQ, dK, dV are rounded back into the caller's
+    // bf16 layout.
     const uint64_t D = p.D, nq = slices * p.M * D, nk = slices * p.N * D;
     if ((s = ensure_ws(h, (4 * nq + 4 * nk + slices * p.M) * sizeof(float))) != BWPP_HIP_OK) return s;
     float *w = static_cast<float *>(h->ws);
@@ -976,7 +999,8 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
     f.q_bs = f.o_bs = (uint64_t)H * p.M * D;
     f.k_hs = f.v_hs = p.N * D;
     f.k_bs = f.v_bs = (uint64_t)H * p.N * D;
-    if ((s = run_f32(f, D == 128 ? 1 : 0)) != BWPP_HIP_OK) return s;
+    const int dv128 = D == 128 ? 1 : 0;
+    if ((s = run_mfma(f, h->attn_f32_dq[dv128][causal], h->attn_f32_dkdv[dv128][causal])) != BWPP_HIP_OK) return s;
     if ((s = conv(dq32, dq, p.M, g.ldq, g.q_bs, g.q_hs, true)) != BWPP_HIP_OK ||
         (s = conv(dk32, dk, p.N, g.ldk, g.k_bs, g.k_hs, true)) != BWPP_HIP_OK)
       return s;

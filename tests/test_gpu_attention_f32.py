@@ -178,25 +178,50 @@ def _bf16_host(t):
 @pytest.mark.parametrize("B,H,M,N,D", [(1, 2, 97, 200, 64), (2, 1, 130, 130, 128), (1, 1, 190, 65, 128),
                                        (1, 2, 256, 256, 128)])
 @pytest.mark.parametrize("causal", [False, True])
-def test_bf16_grad_through_f32_passes(be, oracle, B, H, M, N, D, causal):
-    """bf16 storage, head dim 64 / 128: the forward saves lse (the flash
-    kernel at d = 128), the backward runs the fp32 matrix-core passes on
-    fp32 copies and rounds dQ, dK, dV to bf16.  Bar 2e-2 against the
-    oracle on the exact bf16 input values."""
+def test_bf16_grad_mfma(be, oracle, B, H, M, N, D, causal):
+    """bf16 storage, head dim 64 / 128, 16-byte rows: the forward saves lse
+    (the flash kernel at d = 128), the backward runs the bf16 matrix-core
+    passes (bwpp_attn_bwd_bf16_mfma_*).  Bar 2e-2 against the oracle on the
+    exact bf16 input values."""
+    _bf16_grad_case(be, oracle, B, H, M, N, D, causal, D)
+
+
+@pytest.mark.parametrize("B,H,M,N,D", [(1, 2, 97, 200, 64), (1, 1, 130, 90, 128)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_grad_unaligned_rows(be, oracle, B, H, M, N, D, causal):
+    """Rows of D + 4 bf16 (8-byte aligned only): the backward takes fp32
+    copies through the fp32 matrix-core passes and rounds back to bf16."""
+    _bf16_grad_case(be, oracle, B, H, M, N, D, causal, D + 4)
+
+
+def _bf16_grad_case(be, oracle, B, H, M, N, D, causal, ld):
     torch = _torch()
     seed = B * 100 + M + N
-    (qd, q), (kd, k), (vd, v) = (_bf16_dev(synth.normal(s, seed, i)) for i, s in
-                                 enumerate([(B, H, M, D), (B, H, N, D), (B, H, N, D)]))
-    dod, dout = _bf16_dev(synth.normal((B, H, M, D), seed, 3))
+    shapes = [(B, H, M, D), (B, H, N, D), (B, H, N, D), (B, H, M, D)]
+    vals = [synth.bf16_bits_to_f32(synth.to_bf16_bits(synth.normal(s, seed, i))) for i, s in enumerate(shapes)]
+    q, k, v, dout = vals
+
+    def dev(x, rows):
+        # [B, H, rows, ld] bf16 with the values in the first D columns.
+        full = np.zeros((B, H, rows, ld), np.float32)
+        full[..., :D] = x
+        return _bf16_dev(full)[0]
+
+    qd, kd, vd, dod = dev(q, M), dev(k, N), dev(v, N), dev(dout, M)
     scale = 1.0 / np.sqrt(D)
-    prm = bwpp.AttentionParams(M=M, N=N, K=D, D=D, ldq=D, ldk=D, ldv=D, ldo=D, batch=B, heads=H,
+    prm = bwpp.AttentionParams(M=M, N=N, K=D, D=D, ldq=ld, ldk=ld, ldv=ld, ldo=ld, batch=B, heads=H,
+                               q_batch_stride=H * M * ld, q_head_stride=M * ld, k_batch_stride=H * N * ld,
+                               k_head_stride=N * ld, v_batch_stride=H * N * ld, v_head_stride=N * ld,
+                               o_batch_stride=H * M * ld, o_head_stride=M * ld,
                                scale=scale, causal=int(causal), dtype=int(bwpp.DType.BF16))
-    o = torch.empty((B, H, M, D), dtype=torch.bfloat16, device="cuda")
+    o = dev(np.zeros((B, H, M, D), np.float32), M)
     lse = torch.full((B, H, M), 5.0, device="cuda")
     be.dispatch_attention_lse(qd, kd, vd, o, lse, prm)
     _check_lse(host(lse), oracle.attention_lse(q, k, scale, causal))
-    assert rel_max_err(_bf16_host(o), oracle.attention_bh(q, k, v, scale, causal)) <= 2e-2
+    assert rel_max_err(_bf16_host(o)[..., :D], oracle.attention_bh(q, k, v, scale, causal)) <= 2e-2
     dq, dk, dv = (torch.full_like(t, 7.0) for t in (qd, kd, vd))
     be.dispatch_attention_grad(qd, kd, vd, o, dod, lse, dq, dk, dv, prm)
     for got, want in zip((dq, dk, dv), oracle.attention_grad(q, k, v, dout, scale, causal)):
-        assert rel_max_err(_bf16_host(got), want) <= 2e-2
+        g = _bf16_host(got)
+        assert rel_max_err(g[..., :D], want) <= 2e-2
+        assert np.all(g[..., D:] == 7.0)  # padding columns untouched
