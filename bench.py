@@ -21,8 +21,10 @@ The contraction configs run in the same invocation and are reported under
 "extras" (not part of `value`): C3 bf16 SiLU(X W + b) 4096 x 4096 x 11008
 and its fp32 2048^3 variant (TFLOP/s vs dense MFMA peak), C4 attention
 B8 H32 S2048 d128 bf16 unmasked and causal (causal FLOPs counted as half),
-and C1's 256^3 fp32 GEMM latency.  Each has a CPU oracle timing on a
-bounded slice (rows or heads are independent, so the rate extrapolates).
+the bf16 attention backward at that shape, C1's 256^3 fp32 GEMM latency
+and the C5 fp32 transformer-block training step.  C3 and C4 carry a CPU
+oracle timing on a bounded slice (rows or heads are independent, so the
+rate extrapolates).
 """
 from __future__ import annotations
 
