@@ -255,3 +255,27 @@ def test_f32_split_k_off_matches(oracle, monkeypatch):
         assert rel_max_err(f32_host(c), oracle.matmul(a, b)) <= F32_TOL
     finally:
         be.close()
+
+
+def test_f32_split_k_repeatable(be):
+    """Split-K results do not depend on block timing: back-to-back launches
+    of split-K GEMMs of different shapes, sharing the handle's workspace,
+    each equal their first result bit for bit."""
+    torch = _torch()
+    shapes = [(1024, 1024, 4096, 1, 0), (128, 256, 4000, 0, 1), (256, 384, 2048, 0, 0)]
+    devs = []
+    for i, (M, N, K, ta, tb) in enumerate(shapes):
+        a = synth.uniform((M, K), 50 + i, 0, -1, 1)
+        b = synth.uniform((K, N), 50 + i, 1, -1, 1)
+        bias = synth.uniform((N,), 50 + i, 2, -1, 1)
+        devs.append((f32_dev(stored(a, ta)), f32_dev(stored(b, tb)), f32_dev(bias)))
+    first = {}
+    for rep in range(3):
+        for i, (M, N, K, ta, tb) in enumerate(shapes):
+            ad, bd, biasd = devs[i]
+            c = run(be, bwpp.DType.F32, ad, bd, biasd, M, N, K, 3, ta, tb)
+            torch.cuda.synchronize()
+            if rep == 0:
+                first[i] = c.clone()
+            else:
+                assert torch.equal(c, first[i]), (rep, shapes[i])
