@@ -10,10 +10,10 @@
 // bottom-right aligned causal mask (key n visible to query m iff
 // n <= m + N - M).
 //
-// Work layout as in the fp32 kernels: a block is 2 waves, each wave owns
-// 32 rows (queries in the dQ pass, keys in the dK/dV pass) and the block
-// streams 32-row tiles of the other side through a two-stage LDS ring
-// (register prefetch of tile t+1 during tile t, one barrier per tile).
+// Work layout as in the fp32 kernels, with 4 waves per block: each wave
+// owns 32 rows (queries in the dQ pass, keys in the dK/dV pass) and the
+// block streams 32-row tiles of the other side through a two-stage LDS
+// ring (register prefetch of tile t+1 during tile t, one barrier per tile).
 //
 // MFMA operands (32x32x16 bf16): lane l supplies A[l % 32][8 (l / 32) ..
 // +7] and B[8 (l / 32) .. +7][l % 32]; accumulator register r of lane l is
@@ -47,7 +47,6 @@ typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
 
 namespace {
 
-constexpr int kW = 2;   // waves per block
 constexpr int kR = 32;  // rows per wave and per streamed tile
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -75,10 +74,10 @@ __device__ __forceinline__ uint32_t toff(uint32_t r, uint32_t c) {
 
 // Two [kR x D] bf16 tiles (rows r0.., zeros past `rows`) copied by the
 // block from global memory into registers, then into an LDS stage.
-template <int D>
+template <int D, int W>
 struct TilePairB {
-  static constexpr int CH = D / 8;                 // 16-byte chunks per row
-  static constexpr int PER = kR * CH / (64 * kW);  // chunks per thread per tile
+  static constexpr int CH = D / 8;                // 16-byte chunks per row
+  static constexpr int PER = kR * CH / (64 * W);  // chunks per thread per tile
   u32x4_t x[PER], y[PER];
 
   // rows >= 1.  Rows past the end load row rows - 1 and are then zeroed:
@@ -87,7 +86,7 @@ struct TilePairB {
                                         uint32_t r0, uint32_t rows) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int idx = (int)threadIdx.x + i * 64 * kW;
+      const int idx = (int)threadIdx.x + i * 64 * W;
       const uint32_t row = r0 + (uint32_t)(idx / CH), c = (uint32_t)(idx % CH);
       const uint32_t rr = row < rows ? row : rows - 1;
       x[i] = *reinterpret_cast<const u32x4_t *>(X + (size_t)rr * ldx + 8u * c);
@@ -98,7 +97,7 @@ struct TilePairB {
   __device__ __forceinline__ void stash(unsigned char *lx, unsigned char *ly) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int idx = (int)threadIdx.x + i * 64 * kW;
+      const int idx = (int)threadIdx.x + i * 64 * W;
       const uint32_t off = toff<D>((uint32_t)(idx / CH), (uint32_t)(idx % CH));
       *reinterpret_cast<u32x4_t *>(lx + off) = x[i];
       *reinterpret_cast<u32x4_t *>(ly + off) = y[i];
@@ -208,7 +207,7 @@ __device__ __forceinline__ SliceB slice_b(const BwppAttnArgs &a, uint32_t nbh) {
 
 // dQ pass: a wave owns 32 queries and streams K / V tiles; also writes
 // D_m = rowsum(dO * O) for the dK / dV pass.
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, int kW>
 __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
   constexpr int DB = D / 32, TB = kR * D * 2;
   __shared__ __attribute__((aligned(16))) unsigned char lds[2][2][TB];  // [stage][K, V]
@@ -258,7 +257,7 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
 #pragma unroll
   for (int blk = 0; blk < DB; ++blk) dq[blk] = f32x16_t{};
 
-  TilePairB<D> pf;
+  TilePairB<D, kW> pf;
   if (nt > 0) {
     pf.fetch(K, a.ldk, V, a.ldv, 0, a.N);
     pf.stash(lds[0][0], lds[0][1]);
@@ -296,7 +295,7 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
 
 // dK / dV pass: a wave owns 32 keys and streams Q / dO tiles with their
 // lse and D_m.
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, int kW>
 __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
   constexpr int DB = D / 32, TB = kR * D * 2;
   __shared__ __attribute__((aligned(16))) unsigned char lds[2][2][TB];  // [stage][Q, dO]
@@ -336,7 +335,7 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
   const float c = a.scale_log2;
   const Offsets<D> off(lane);
 
-  TilePairB<D> pf;
+  TilePairB<D, kW> pf;
   float rl = INFINITY, rd = 0.0f;  // lse2 / D_m of row threadIdx.x (< kR)
   auto fetch_rows = [&](uint32_t m0) {
     if (threadIdx.x < (uint32_t)kR) {
@@ -408,14 +407,17 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
 
 }  // namespace
 
+// 4 waves (128 rows) per block: each streamed tile feeds twice the rows of
+// a 2-wave block (measured 5-16 % faster at the C4 / C5-like shapes).
+constexpr int kWB = 4;
 #define BWPP_ATTN_BWD_BF16(D, CAUSAL, SUFFIX)                                                   \
-  extern "C" __global__ __launch_bounds__(64 * kW) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dq( \
+  extern "C" __global__ __launch_bounds__(64 * kWB) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dq( \
       const BwppAttnArgs a) {                                                                   \
-    bwd_dq<D, CAUSAL>(a);                                                                       \
+    bwd_dq<D, CAUSAL, kWB>(a);                                                                  \
   }                                                                                             \
-  extern "C" __global__ __launch_bounds__(64 * kW) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dkdv( \
+  extern "C" __global__ __launch_bounds__(64 * kWB) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dkdv( \
       const BwppAttnArgs a) {                                                                   \
-    bwd_dkdv<D, CAUSAL>(a);                                                                     \
+    bwd_dkdv<D, CAUSAL, kWB>(a);                                                                \
   }
 
 BWPP_ATTN_BWD_BF16(64, false, )
