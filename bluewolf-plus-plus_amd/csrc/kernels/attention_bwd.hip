@@ -408,7 +408,8 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
 }  // namespace
 
 // 4 waves (128 rows) per block: each streamed tile feeds twice the rows of
-// a 2-wave block (measured 5-16 % faster at the C4 / C5-like shapes).
+// a 2-wave block (measured 5-16 % faster at the C4 / C5-like shapes).  The
+// runtime launches 64 * kWB threads and 128-row tiles for these kernels.
 constexpr int kWB = 4;
 #define BWPP_ATTN_BWD_BF16(D, CAUSAL, SUFFIX)                                                   \
   extern "C" __global__ __launch_bounds__(64 * kWB) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dq( \

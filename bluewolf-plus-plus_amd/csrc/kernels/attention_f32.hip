@@ -43,7 +43,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int kW = 2;   // waves per block
+constexpr int kW = 4;   // waves per block (each streamed tile feeds 128 rows)
 constexpr int kR = 32;  // rows per wave and per streamed tile
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kLog2e = 1.4426950408889634f;

@@ -804,7 +804,7 @@ int attn_bf16_bwd_variant(const BwppAttentionParams &p, const BwppAttnArgs &g, f
   return p.K == 128 ? 1 : 0;
 }
 
-constexpr uint32_t kF32Rows = 64;  // queries (keys) per block of the fp32 MFMA kernels: 2 waves x 32
+constexpr uint32_t kAttnWaves = 4;  // waves (32 rows each) per block of the MFMA attention kernels
 
 BwppHipStatus attn_forward(BwppHip *h, const void *q, const void *k, const void *v, void *o, float *lse,
                            const BwppAttentionParams &p) {
@@ -841,10 +841,10 @@ BwppHipStatus attn_forward(BwppHip *h, const void *q, const void *k, const void 
     g.scale = scale;
     g.scale_log2 = scale * 1.4426950408889634f;
     g.lse = lse;
-    g.q_tiles = (p.M + kF32Rows - 1) / kF32Rows;
+    g.q_tiles = (p.M + 32 * kAttnWaves - 1) / (32 * kAttnWaves);
     const uint64_t grid = slices * g.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention: grid too large");
-    return launch(h, h->attn_f32_fwd[f32v][causal], (uint32_t)grid, 1, 1, 2 * 64, g);
+    return launch(h, h->attn_f32_fwd[f32v][causal], (uint32_t)grid, 1, 1, 64 * kAttnWaves, g);
   }
   g.scale_log2 = scale;
   g.lse = lse;
@@ -932,27 +932,27 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   g.dsum = static_cast<float *>(h->ws);
   // Matrix-core passes (fp32 or bf16 kernels, same grids): dQ (also writes
   // D_m = rowsum(dO * O)), then dK / dV.
-  // wq / wk: waves (32 rows each) per block of the dQ / dK-dV kernel.
-  auto run_mfma = [&](BwppAttnArgs f, hipFunction_t fdq, uint32_t wq, hipFunction_t fdkdv,
-                      uint32_t wk) -> BwppHipStatus {
+  auto run_mfma = [&](BwppAttnArgs f, hipFunction_t fdq, hipFunction_t fdkdv) -> BwppHipStatus {
+    constexpr uint32_t rows = 32 * kAttnWaves;
     f.scale = scale;
     f.scale_log2 = scale * 1.4426950408889634f;
-    f.q_tiles = (p.M + 32 * wq - 1) / (32 * wq);
+    f.q_tiles = (p.M + rows - 1) / rows;
     uint64_t grid = slices * f.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
     BwppHipStatus st;
-    if (p.M > 0 && (st = launch(h, fdq, (uint32_t)grid, 1, 1, 64 * wq, f)) != BWPP_HIP_OK) return st;
-    f.q_tiles = (p.N + 32 * wk - 1) / (32 * wk);  // key tiles
+    if (p.M > 0 && (st = launch(h, fdq, (uint32_t)grid, 1, 1, 64 * kAttnWaves, f)) != BWPP_HIP_OK) return st;
+    f.q_tiles = (p.N + rows - 1) / rows;  // key tiles
     grid = slices * f.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
-    if (p.N > 0) return launch(h, fdkdv, (uint32_t)grid, 1, 1, 64 * wk, f);
+    if (p.N > 0) return launch(h, fdkdv, (uint32_t)grid, 1, 1, 64 * kAttnWaves, f);
     return BWPP_HIP_OK;
   };
   const int f32v = attn_f32_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
-  if (f32v >= 0) return run_mfma(g, h->attn_f32_dq[f32v][causal], 2, h->attn_f32_dkdv[f32v][causal], 2);
+  if (f32v >= 0)
+    return run_mfma(g, h->attn_f32_dq[f32v][causal], h->attn_f32_dkdv[f32v][causal]);
   const int bf16v = attn_bf16_bwd_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
   if (bf16v >= 0)
-    return run_mfma(g, h->attn_bf16_dq[bf16v][causal], 4, h->attn_bf16_dkdv[bf16v][causal], 4);
+    return run_mfma(g, h->attn_bf16_dq[bf16v][causal], h->attn_bf16_dkdv[bf16v][causal]);
   if (bf && p.K == p.D && (p.K == 64 || p.K == 128) && std::isfinite(scale)) {
     // bf16 with head dim 64 / 128 whose rows are not 16-byte aligned: fp32
     // copies of Q, K, V, O, dO in the workspace go through the fp32
@@ -1003,8 +1003,7 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
     f.k_hs = f.v_hs = p.N * D;
     f.k_bs = f.v_bs = (uint64_t)H * p.N * D;
     const int dv128 = D == 128 ? 1 : 0;
-    if ((s = run_mfma(f, h->attn_f32_dq[dv128][causal], 2, h->attn_f32_dkdv[dv128][causal], 2)) != BWPP_HIP_OK)
-      return s;
+    if ((s = run_mfma(f, h->attn_f32_dq[dv128][causal], h->attn_f32_dkdv[dv128][causal])) != BWPP_HIP_OK) return s;
     if ((s = conv(dq32, dq, p.M, g.ldq, g.q_bs, g.q_hs, true)) != BWPP_HIP_OK ||
         (s = conv(dk32, dk, p.N, g.ldk, g.k_bs, g.k_hs, true)) != BWPP_HIP_OK)
       return s;
