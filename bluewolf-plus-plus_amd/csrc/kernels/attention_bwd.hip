@@ -76,8 +76,10 @@ __device__ __forceinline__ uint32_t toff(uint32_t r, uint32_t c) {
 // block from global memory into registers, then into an LDS stage.
 template <int D, int W>
 struct TilePairB {
-  static constexpr int CH = D / 8;                // 16-byte chunks per row
-  static constexpr int PER = kR * CH / (64 * W);  // chunks per thread per tile
+  static constexpr int CH = D / 8;                                // 16-byte chunks per row
+  static constexpr int TOT = kR * CH;                             // chunks per tile
+  static constexpr int PER = (TOT + 64 * W - 1) / (64 * W);       // chunks per thread per tile
+  static constexpr bool kPart = TOT % (64 * W) != 0;              // some threads hold fewer
   u32x4_t x[PER], y[PER];
 
   // rows >= 1.  Rows past the end load row rows - 1 and are then zeroed:
@@ -87,6 +89,7 @@ struct TilePairB {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int idx = (int)threadIdx.x + i * 64 * W;
+      if (kPart && idx >= TOT) break;
       const uint32_t row = r0 + (uint32_t)(idx / CH), c = (uint32_t)(idx % CH);
       const uint32_t rr = row < rows ? row : rows - 1;
       x[i] = *reinterpret_cast<const u32x4_t *>(X + (size_t)rr * ldx + 8u * c);
@@ -98,6 +101,7 @@ struct TilePairB {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int idx = (int)threadIdx.x + i * 64 * W;
+      if (kPart && idx >= TOT) break;
       const uint32_t off = toff<D>((uint32_t)(idx / CH), (uint32_t)(idx % CH));
       *reinterpret_cast<u32x4_t *>(lx + off) = x[i];
       *reinterpret_cast<u32x4_t *>(ly + off) = y[i];
@@ -409,19 +413,24 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
 
 // 4 waves (128 rows) per block: each streamed tile feeds twice the rows of
 // a 2-wave block (measured 5-16 % faster at the C4 / C5-like shapes).  The
-// runtime launches 64 * kWB threads and 128-row tiles for these kernels.
-constexpr int kWB = 4;
+// unmasked d = 128 dK/dV pass also comes with 8 waves (256 keys per block;
+// 19 % faster at the C4 shape, slower when causal or at d = 64).  The
+// runtime launches 64 * waves threads and 32 * waves rows per block.
+constexpr int kWQ = 4, kWK = 4;
 #define BWPP_ATTN_BWD_BF16(D, CAUSAL, SUFFIX)                                                   \
-  extern "C" __global__ __launch_bounds__(64 * kWB) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dq( \
+  extern "C" __global__ __launch_bounds__(64 * kWQ) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dq( \
       const BwppAttnArgs a) {                                                                   \
-    bwd_dq<D, CAUSAL, kWB>(a);                                                                  \
+    bwd_dq<D, CAUSAL, kWQ>(a);                                                                  \
   }                                                                                             \
-  extern "C" __global__ __launch_bounds__(64 * kWB) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dkdv( \
+  extern "C" __global__ __launch_bounds__(64 * kWK) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dkdv( \
       const BwppAttnArgs a) {                                                                   \
-    bwd_dkdv<D, CAUSAL, kWB>(a);                                                                \
+    bwd_dkdv<D, CAUSAL, kWK>(a);                                                                \
   }
 
 BWPP_ATTN_BWD_BF16(64, false, )
 BWPP_ATTN_BWD_BF16(64, true, _causal)
 BWPP_ATTN_BWD_BF16(128, false, )
 BWPP_ATTN_BWD_BF16(128, true, _causal)
+extern "C" __global__ __launch_bounds__(512) void bwpp_attn_bwd_bf16_mfma_d128_dkdv_w8(const BwppAttnArgs a) {
+  bwd_dkdv<128, false, 8>(a);
+}

@@ -87,6 +87,7 @@ struct BwppHip {
   hipFunction_t attn_f32_fwd[2][2] = {}, attn_f32_dq[2][2] = {}, attn_f32_dkdv[2][2] = {};
   // bf16 MFMA attention backward, head dim 64 / 128: [d128][causal]
   hipFunction_t attn_bf16_dq[2][2] = {}, attn_bf16_dkdv[2][2] = {};
+  hipFunction_t attn_bf16_dkdv_w8 = nullptr;  // d = 128, unmasked, 8 waves per block
   hipFunction_t attn_conv_to_f32 = nullptr, attn_conv_to_bf16 = nullptr;  // bf16 <-> fp32 operand copies
   hipFunction_t rmsnorm_grad_w[4] = {};  // wave-per-row rmsnorm_grad, 256 / 512 / 1024 / 2048 columns
   hipFunction_t silu_grad = nullptr, softmax_grad = nullptr, rmsnorm_grad = nullptr, col_partials_sum = nullptr,
@@ -158,6 +159,7 @@ BwppHipStatus resolve_all(BwppHip *h) {
       {"bwpp_rmsnorm_grad_w1", &h->rmsnorm_grad_w[0]}, {"bwpp_rmsnorm_grad_w2", &h->rmsnorm_grad_w[1]},
       {"bwpp_rmsnorm_grad_w4", &h->rmsnorm_grad_w[2]}, {"bwpp_rmsnorm_grad_w8", &h->rmsnorm_grad_w[3]},
       {"bwpp_attn_conv_bf16_to_f32", &h->attn_conv_to_f32}, {"bwpp_attn_conv_f32_to_bf16", &h->attn_conv_to_bf16},
+      {"bwpp_attn_bwd_bf16_mfma_d128_dkdv_w8", &h->attn_bf16_dkdv_w8},
   };
   for (auto &e : singles)
     if ((s = resolve(h, e.name, e.slot)) != BWPP_HIP_OK) return s;
@@ -932,27 +934,32 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   g.dsum = static_cast<float *>(h->ws);
   // Matrix-core passes (fp32 or bf16 kernels, same grids): dQ (also writes
   // D_m = rowsum(dO * O)), then dK / dV.
-  auto run_mfma = [&](BwppAttnArgs f, hipFunction_t fdq, hipFunction_t fdkdv) -> BwppHipStatus {
-    constexpr uint32_t rows = 32 * kAttnWaves;
+  // wq / wk: waves (32 rows each) per block of the dQ / dK-dV kernel.
+  auto run_mfma = [&](BwppAttnArgs f, hipFunction_t fdq, hipFunction_t fdkdv, uint32_t wq = kAttnWaves,
+                      uint32_t wk = kAttnWaves) -> BwppHipStatus {
     f.scale = scale;
     f.scale_log2 = scale * 1.4426950408889634f;
-    f.q_tiles = (p.M + rows - 1) / rows;
+    f.q_tiles = (p.M + 32 * wq - 1) / (32 * wq);
     uint64_t grid = slices * f.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
     BwppHipStatus st;
-    if (p.M > 0 && (st = launch(h, fdq, (uint32_t)grid, 1, 1, 64 * kAttnWaves, f)) != BWPP_HIP_OK) return st;
-    f.q_tiles = (p.N + rows - 1) / rows;  // key tiles
+    if (p.M > 0 && (st = launch(h, fdq, (uint32_t)grid, 1, 1, 64 * wq, f)) != BWPP_HIP_OK) return st;
+    f.q_tiles = (p.N + 32 * wk - 1) / (32 * wk);  // key tiles
     grid = slices * f.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
-    if (p.N > 0) return launch(h, fdkdv, (uint32_t)grid, 1, 1, 64 * kAttnWaves, f);
+    if (p.N > 0) return launch(h, fdkdv, (uint32_t)grid, 1, 1, 64 * wk, f);
     return BWPP_HIP_OK;
   };
   const int f32v = attn_f32_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
   if (f32v >= 0)
     return run_mfma(g, h->attn_f32_dq[f32v][causal], h->attn_f32_dkdv[f32v][causal]);
   const int bf16v = attn_bf16_bwd_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
-  if (bf16v >= 0)
+  if (bf16v >= 0) {
+    // Unmasked d = 128: the dK/dV pass with 8 waves (256 keys) per block.
+    if (bf16v == 1 && !causal)
+      return run_mfma(g, h->attn_bf16_dq[1][0], h->attn_bf16_dkdv_w8, kAttnWaves, 8);
     return run_mfma(g, h->attn_bf16_dq[bf16v][causal], h->attn_bf16_dkdv[bf16v][causal]);
+  }
   if (bf && p.K == p.D && (p.K == 64 || p.K == 128) && std::isfinite(scale)) {
     // bf16 with head dim 64 / 128 whose rows are not 16-byte aligned: fp32
     // copies of Q, K, V, O, dO in the workspace go through the fp32
