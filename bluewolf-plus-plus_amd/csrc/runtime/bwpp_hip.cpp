@@ -22,6 +22,7 @@
 #include <cstring>
 #include <initializer_list>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../kargs.h"
@@ -61,6 +62,7 @@ struct BwppHip {
   int cus = 0;
   hipStream_t stream = nullptr;
   std::vector<hipModule_t> modules;
+  std::unordered_map<hipFunction_t, uint32_t> max_threads;  // per resolved kernel
   std::string err;
   int row_cfg_override = -1;  // BWPP_ROW_CFG: index into kRowCfgs (tuning)
   uint32_t row_grid_cap = 0;  // BWPP_ROW_GRID: max blocks per row launch (0 = per-op default)
@@ -121,6 +123,13 @@ BwppHipStatus resolve(BwppHip *h, const std::string &name, hipFunction_t *out) {
   for (hipModule_t m : h->modules) {
     hipFunction_t f = nullptr;
     if (hipModuleGetFunction(&f, m, name.c_str()) == hipSuccess && f) {
+      // The block size each kernel was compiled for (its launch bounds):
+      // launch() refuses larger blocks instead of running a kernel whose
+      // indexing assumes fewer threads.
+      int mt = 0;
+      if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, f) != hipSuccess || mt <= 0)
+        return fail(h, BWPP_HIP_ERR_HIP, "hipFuncGetAttribute(%s) failed", name.c_str());
+      h->max_threads[f] = (uint32_t)mt;
       *out = f;
       return BWPP_HIP_OK;
     }
@@ -232,6 +241,10 @@ template <class Args>
 BwppHipStatus launch(BwppHip *h, hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx,
                      const Args &args, uint32_t shmem = 0) {
   if (gx == 0 || gy == 0 || gz == 0) return BWPP_HIP_OK;
+  const auto mt = h->max_threads.find(f);
+  if (mt == h->max_threads.end() || bx > mt->second)
+    return fail(h, BWPP_HIP_ERR_HIP, "launch of %u threads per block exceeds the kernel's limit (%u)", bx,
+                mt == h->max_threads.end() ? 0u : mt->second);
   void *params[] = {const_cast<Args *>(&args)};
   hipError_t e = hipModuleLaunchKernel(f, gx, gy, gz, bx, 1, 1, shmem, h->stream, params, nullptr);
   if (e != hipSuccess) return fail(h, BWPP_HIP_ERR_HIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
