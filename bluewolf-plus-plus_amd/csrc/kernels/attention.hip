@@ -385,8 +385,9 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
 // with all of their query tiles, so the blocks that stream the same K / V
 // run together on one L2.  Unmasked: one query tile per block.  Causal: a
 // block takes query tiles QT - 1 - p and p of one slice, whose visible key
-// counts add up to the same total for every p, so all blocks carry equal
-// work (the runtime launches slices * ceil(QT / 2) blocks).
+// counts add up to the same total for every p (up to the clamping at 0 and
+// N when M != N), so the blocks carry equal work (the runtime launches
+// slices * ceil(QT / 2) blocks).
 template <bool CAUSAL>
 __device__ __forceinline__ void attn_bf16_d128(const BwppAttnArgs &a) {
   const uint32_t G = gridDim.x, QT = a.q_tiles;

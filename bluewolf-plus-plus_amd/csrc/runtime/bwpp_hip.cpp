@@ -945,9 +945,9 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   g.dk = dk;
   g.dv = dv;
   g.dsum = static_cast<float *>(h->ws);
-  // Matrix-core passes (fp32 or bf16 kernels, same grids): dQ (also writes
-  // D_m = rowsum(dO * O)), then dK / dV.
-  // wq / wk: waves (32 rows each) per block of the dQ / dK-dV kernel.
+  // Matrix-core passes (fp32 or bf16 kernels): dQ (also writes D_m =
+  // rowsum(dO * O)), then dK / dV.  wq / wk: waves (32 rows each) per block
+  // of the dQ / dK-dV kernel, as each was compiled.
   auto run_mfma = [&](BwppAttnArgs f, hipFunction_t fdq, hipFunction_t fdkdv, uint32_t wq = kAttnWaves,
                       uint32_t wk = kAttnWaves) -> BwppHipStatus {
     f.scale = scale;
