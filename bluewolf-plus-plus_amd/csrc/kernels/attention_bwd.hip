@@ -12,8 +12,9 @@
 //
 // Work layout as in the fp32 kernels, with 4 waves per block: each wave
 // owns 32 rows (queries in the dQ pass, keys in the dK/dV pass) and the
-// block streams 32-row tiles of the other side through a two-stage LDS
-// ring (register prefetch of tile t+1 during tile t, one barrier per tile).
+// block streams 64-row tiles of the other side through a two-stage LDS
+// ring (register prefetch of tile t+1 during tile t, one barrier per tile)
+// and works through each tile in 32-row blocks.
 //
 // MFMA operands (32x32x16 bf16): lane l supplies A[l % 32][8 (l / 32) ..
 // +7] and B[8 (l / 32) .. +7][l % 32]; accumulator register r of lane l is
@@ -28,7 +29,7 @@
 //    into the B operand, lane half h taking tile rows 4h..4h+3 and
 //    8+4h..8+4h+3 of each 16, and X^T is read from the row-major tile with
 //    ds_read_b64_tr_b16 at exactly those rows.
-// LDS tiles are [32 rows][D] bf16 with 16-byte chunk c of row r stored at
+// LDS tiles are [rows][D] bf16 with 16-byte chunk c of row r stored at
 // chunk c ^ swz(r); swz is a permutation on any 16 consecutive rows (the
 // row reads) and keeps the two chunks of the four rows that a 16-lane
 // group of a transposing read touches apart.
@@ -47,7 +48,7 @@ typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
 
 namespace {
 
-constexpr int kR = 32;  // rows per wave and per streamed tile
+constexpr int kR = 32;  // rows per wave and per block of a streamed tile
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ f32x16_t mfma16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
@@ -72,12 +73,12 @@ __device__ __forceinline__ uint32_t toff(uint32_t r, uint32_t c) {
   return r * (uint32_t)(D * 2) + 16u * (c ^ swz<D>(r));
 }
 
-// Two [kR x D] bf16 tiles (rows r0.., zeros past `rows`) copied by the
+// Two [TR x D] bf16 tiles (rows r0.., zeros past `rows`) copied by the
 // block from global memory into registers, then into an LDS stage.
-template <int D, int W>
+template <int D, int W, int TR>
 struct TilePairB {
   static constexpr int CH = D / 8;                                // 16-byte chunks per row
-  static constexpr int TOT = kR * CH;                             // chunks per tile
+  static constexpr int TOT = TR * CH;                             // chunks per tile
   static constexpr int PER = (TOT + 64 * W - 1) / (64 * W);       // chunks per thread per tile
   static constexpr bool kPart = TOT % (64 * W) != 0;              // some threads hold fewer
   u32x4_t x[PER], y[PER];
@@ -211,9 +212,9 @@ __device__ __forceinline__ SliceB slice_b(const BwppAttnArgs &a, uint32_t nbh) {
 
 // dQ pass: a wave owns 32 queries and streams K / V tiles; also writes
 // D_m = rowsum(dO * O) for the dK / dV pass.
-template <int D, bool CAUSAL, int kW>
+template <int D, bool CAUSAL, int kW, int TR>
 __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
-  constexpr int DB = D / 32, TB = kR * D * 2;
+  constexpr int DB = D / 32, TB = TR * D * 2, RB = D * 2;
   __shared__ __attribute__((aligned(16))) unsigned char lds[2][2][TB];  // [stage][K, V]
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
   const int li = lane & 31, hi = lane >> 5;
@@ -234,7 +235,7 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
     const int64_t last = (int64_t)min(a.M, qb + kW * kR) - 1 + diag;
     kend = last < 0 ? 0u : (uint32_t)min<int64_t>(last + 1, (int64_t)a.N);
   }
-  const uint32_t nt = (kend + kR - 1) / kR;
+  const uint32_t nt = (kend + TR - 1) / TR;
   const int64_t wlast = (int64_t)q0 + kR - 1 + diag;
 
   bf16x8_t qf[D / 16], gf[D / 16];
@@ -261,7 +262,7 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
 #pragma unroll
   for (int blk = 0; blk < DB; ++blk) dq[blk] = f32x16_t{};
 
-  TilePairB<D, kW> pf;
+  TilePairB<D, kW, TR> pf;
   if (nt > 0) {
     pf.fetch(K, a.ldk, V, a.ldv, 0, a.N);
     pf.stash(lds[0][0], lds[0][1]);
@@ -269,26 +270,31 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
   __syncthreads();
   for (uint32_t t = 0; t < nt; ++t) {
     const int st = (int)(t & 1);
-    const uint32_t k0 = t * kR;
-    if (t + 1 < nt) pf.fetch(K, a.ldk, V, a.ldv, k0 + kR, a.N);
-    if (!CAUSAL || (int64_t)k0 <= wlast) {
-      f32x16_t s = dot_rows<D>(lds[st][0], off, qf);         // S^T [key][query]
-      const f32x16_t dp = dot_rows<D>(lds[st][1], off, gf);  // dP^T = V dO^T
-      const bool edge = k0 + kR > a.N || (CAUSAL && (int64_t)k0 + kR - 1 > (int64_t)q0 + diag);
+    if (t + 1 < nt) pf.fetch(K, a.ldk, V, a.ldv, (t + 1) * TR, a.N);
+    // The tile in 32-key blocks (the swizzle repeats every 16 rows).
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = __builtin_amdgcn_exp2f(s[r] * c - lse2);
-        if (edge) {
-          const uint32_t key = k0 + (uint32_t)acc_row(r, hi);
-          if (key >= a.N || (CAUSAL && (int64_t)key > (int64_t)qi + diag)) p = 0.0f;
+    for (int sb = 0; sb < TR / kR; ++sb) {
+      const uint32_t k0 = t * TR + sb * kR;
+      const unsigned char *Kt = lds[st][0] + sb * kR * RB, *Vt = lds[st][1] + sb * kR * RB;
+      if ((TR == kR || k0 < kend) && (!CAUSAL || (int64_t)k0 <= wlast)) {
+        f32x16_t s = dot_rows<D>(Kt, off, qf);         // S^T [key][query]
+        const f32x16_t dp = dot_rows<D>(Vt, off, gf);  // dP^T = V dO^T
+        const bool edge = k0 + kR > a.N || (CAUSAL && (int64_t)k0 + kR - 1 > (int64_t)q0 + diag);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float p = __builtin_amdgcn_exp2f(s[r] * c - lse2);
+          if (edge) {
+            const uint32_t key = k0 + (uint32_t)acc_row(r, hi);
+            if (key >= a.N || (CAUSAL && (int64_t)key > (int64_t)qi + diag)) p = 0.0f;
+          }
+          s[r] = p * (dp[r] - dsum);  // dS^T
         }
-        s[r] = p * (dp[r] - dsum);  // dS^T
-      }
 #pragma unroll
-      for (int kq = 0; kq < 2; ++kq) {
-        const bf16x8_t w = acc_operand(s, kq);
+        for (int kq = 0; kq < 2; ++kq) {
+          const bf16x8_t w = acc_operand(s, kq);
 #pragma unroll
-        for (int blk = 0; blk < DB; ++blk) dq[blk] = mfma16(tr_operand<D>(lds[st][0], off, blk, kq), w, dq[blk]);
+          for (int blk = 0; blk < DB; ++blk) dq[blk] = mfma16(tr_operand<D>(Kt, off, blk, kq), w, dq[blk]);
+        }
       }
     }
     if (t + 1 < nt) pf.stash(lds[st ^ 1][0], lds[st ^ 1][1]);
@@ -299,11 +305,11 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
 
 // dK / dV pass: a wave owns 32 keys and streams Q / dO tiles with their
 // lse and D_m.
-template <int D, bool CAUSAL, int kW>
+template <int D, bool CAUSAL, int kW, int TR>
 __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
-  constexpr int DB = D / 32, TB = kR * D * 2;
+  constexpr int DB = D / 32, TB = TR * D * 2, RB = D * 2;
   __shared__ __attribute__((aligned(16))) unsigned char lds[2][2][TB];  // [stage][Q, dO]
-  __shared__ __attribute__((aligned(16))) float rowv[2][2][kR];          // [stage][lse2, D_m]
+  __shared__ __attribute__((aligned(16))) float rowv[2][2][TR];          // [stage][lse2, D_m]
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
   const int li = lane & 31, hi = lane >> 5;
   const uint32_t nbh = gridDim.x / a.q_tiles;  // q_tiles holds the key tiles here
@@ -325,9 +331,9 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
   if (CAUSAL) {
     const int64_t first = (int64_t)kb - diag;
     mbeg = first <= 0 ? 0u : (first >= (int64_t)a.M ? a.M : (uint32_t)first);
-    mbeg -= mbeg % kR;
+    mbeg -= mbeg % TR;
   }
-  const uint32_t nt = a.M > mbeg ? (a.M - mbeg + kR - 1) / kR : 0u;
+  const uint32_t nt = a.M > mbeg ? (a.M - mbeg + TR - 1) / TR : 0u;
   const int64_t wfirst = (int64_t)k0w - diag;  // first query that sees any key of the wave
 
   bf16x8_t kf[D / 16], vf[D / 16];
@@ -339,17 +345,17 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
   const float c = a.scale_log2;
   const Offsets<D> off(lane);
 
-  TilePairB<D, kW> pf;
-  float rl = INFINITY, rd = 0.0f;  // lse2 / D_m of row threadIdx.x (< kR)
+  TilePairB<D, kW, TR> pf;
+  float rl = INFINITY, rd = 0.0f;  // lse2 / D_m of row threadIdx.x (< TR)
   auto fetch_rows = [&](uint32_t m0) {
-    if (threadIdx.x < (uint32_t)kR) {
+    if (threadIdx.x < (uint32_t)TR) {
       const uint32_t m = m0 + threadIdx.x;
       rl = m < a.M ? lse[m] * kLog2e : INFINITY;
       rd = m < a.M ? dsum[m] : 0.0f;
     }
   };
   auto stash_rows = [&](int st) {
-    if (threadIdx.x < (uint32_t)kR) {
+    if (threadIdx.x < (uint32_t)TR) {
       rowv[st][0][threadIdx.x] = rl;
       rowv[st][1][threadIdx.x] = rd;
     }
@@ -363,37 +369,42 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
   __syncthreads();
   for (uint32_t t = 0; t < nt; ++t) {
     const int st = (int)(t & 1);
-    const uint32_t m0 = mbeg + t * kR;
     if (t + 1 < nt) {
-      pf.fetch(Q, a.ldq, dO, a.ldo, m0 + kR, a.M);
-      fetch_rows(m0 + kR);
+      pf.fetch(Q, a.ldq, dO, a.ldo, mbeg + (t + 1) * TR, a.M);
+      fetch_rows(mbeg + (t + 1) * TR);
     }
-    if (!CAUSAL || (int64_t)m0 + kR - 1 >= wfirst) {
-      f32x16_t s = dot_rows<D>(lds[st][0], off, kf);         // S [query][key]
-      const f32x16_t dp = dot_rows<D>(lds[st][1], off, vf);  // dP = dO V^T
-      const bool edge = CAUSAL && (int64_t)m0 < wfirst + kR - 1;
-      f32x16_t ds;
+    // The tile in 32-query blocks (the swizzle repeats every 16 rows).
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int row = 8 * r4 + 4 * hi;
-        const f32x4_t l4 = *reinterpret_cast<const f32x4_t *>(&rowv[st][0][row]);
-        const f32x4_t d4 = *reinterpret_cast<const f32x4_t *>(&rowv[st][1][row]);
+    for (int sb = 0; sb < TR / kR; ++sb) {
+      const uint32_t m0 = mbeg + t * TR + sb * kR;
+      const unsigned char *Qt = lds[st][0] + sb * kR * RB, *Gt = lds[st][1] + sb * kR * RB;
+      if ((TR == kR || m0 < a.M) && (!CAUSAL || (int64_t)m0 + kR - 1 >= wfirst)) {
+        f32x16_t s = dot_rows<D>(Qt, off, kf);         // S [query][key]
+        const f32x16_t dp = dot_rows<D>(Gt, off, vf);  // dP = dO V^T
+        const bool edge = CAUSAL && (int64_t)m0 < wfirst + kR - 1;
+        f32x16_t ds;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * r4 + e;
-          float p = __builtin_amdgcn_exp2f(s[r] * c - l4[e]);
-          if (edge && (int64_t)ni > (int64_t)(m0 + (uint32_t)(row + e)) + diag) p = 0.0f;
-          s[r] = p;
-          ds[r] = p * (dp[r] - d4[e]);
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int row = 8 * r4 + 4 * hi;
+          const f32x4_t l4 = *reinterpret_cast<const f32x4_t *>(&rowv[st][0][sb * kR + row]);
+          const f32x4_t d4 = *reinterpret_cast<const f32x4_t *>(&rowv[st][1][sb * kR + row]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * r4 + e;
+            float p = __builtin_amdgcn_exp2f(s[r] * c - l4[e]);
+            if (edge && (int64_t)ni > (int64_t)(m0 + (uint32_t)(row + e)) + diag) p = 0.0f;
+            s[r] = p;
+            ds[r] = p * (dp[r] - d4[e]);
+          }
         }
-      }
 #pragma unroll
-      for (int kq = 0; kq < 2; ++kq) {
-        const bf16x8_t wp = acc_operand(s, kq), wd = acc_operand(ds, kq);
+        for (int kq = 0; kq < 2; ++kq) {
+          const bf16x8_t wp = acc_operand(s, kq), wd = acc_operand(ds, kq);
 #pragma unroll
-        for (int blk = 0; blk < DB; ++blk) {
-          dv[blk] = mfma16(tr_operand<D>(lds[st][1], off, blk, kq), wp, dv[blk]);  // dV^T += dO^T P
-          dk[blk] = mfma16(tr_operand<D>(lds[st][0], off, blk, kq), wd, dk[blk]);  // dK^T += Q^T dS
+          for (int blk = 0; blk < DB; ++blk) {
+            dv[blk] = mfma16(tr_operand<D>(Gt, off, blk, kq), wp, dv[blk]);  // dV^T += dO^T P
+            dk[blk] = mfma16(tr_operand<D>(Qt, off, blk, kq), wd, dk[blk]);  // dK^T += Q^T dS
+          }
         }
       }
     }
@@ -416,15 +427,19 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
 // unmasked d = 128 dK/dV pass also comes with 8 waves (256 keys per block;
 // 19 % faster at the C4 shape, slower when causal or at d = 64).  The
 // runtime launches 64 * waves threads and 32 * waves rows per block.
+// 64-row streamed tiles halve the barriers and prefetch rounds per row
+// (dQ and the causal dK/dV pass 8-9 % faster at the C4 shape); the 8-wave
+// pass keeps 32-row tiles, which it needs to stay within 256 VGPRs.
 constexpr int kWQ = 4, kWK = 4;
+constexpr int kTR = 64;  // rows per streamed K/V or Q/dO tile
 #define BWPP_ATTN_BWD_BF16(D, CAUSAL, SUFFIX)                                                   \
   extern "C" __global__ __launch_bounds__(64 * kWQ) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dq( \
       const BwppAttnArgs a) {                                                                   \
-    bwd_dq<D, CAUSAL, kWQ>(a);                                                                  \
+    bwd_dq<D, CAUSAL, kWQ, kTR>(a);                                                             \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(64 * kWK) void bwpp_attn_bwd_bf16_mfma_d##D##SUFFIX##_dkdv( \
       const BwppAttnArgs a) {                                                                   \
-    bwd_dkdv<D, CAUSAL, kWK>(a);                                                                \
+    bwd_dkdv<D, CAUSAL, kWK, kTR>(a);                                                           \
   }
 
 BWPP_ATTN_BWD_BF16(64, false, )
@@ -432,5 +447,5 @@ BWPP_ATTN_BWD_BF16(64, true, _causal)
 BWPP_ATTN_BWD_BF16(128, false, )
 BWPP_ATTN_BWD_BF16(128, true, _causal)
 extern "C" __global__ __launch_bounds__(512) void bwpp_attn_bwd_bf16_mfma_d128_dkdv_w8(const BwppAttnArgs a) {
-  bwd_dkdv<128, false, 8>(a);
+  bwd_dkdv<128, false, 8, kR>(a);
 }

@@ -176,7 +176,7 @@ def _bf16_host(t):
 
 
 @pytest.mark.parametrize("B,H,M,N,D", [(1, 2, 97, 200, 64), (2, 1, 130, 130, 128), (1, 1, 190, 65, 128),
-                                       (1, 2, 256, 256, 128)])
+                                       (1, 2, 256, 256, 128), (1, 3, 160, 300, 128), (1, 1, 288, 100, 64)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_bf16_grad_mfma(be, oracle, B, H, M, N, D, causal):
     """bf16 storage, head dim 64 / 128, 16-byte rows: the forward saves lse
