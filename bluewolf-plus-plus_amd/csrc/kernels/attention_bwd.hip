@@ -129,22 +129,32 @@ __device__ __forceinline__ void load_row(bf16x8_t (&dst)[D / 16], const uint16_t
 
 // Per-lane LDS offsets: row reads (tile row li, k-step ks) and the two
 // transposing reads (tile rows 0-7 / 8-15 of a 16-row step) of d block blk.
+// Only the k-step 0 / d block 0 offsets are kept: the others differ in the
+// chunk bits that ks (2 ks) and blk (4 blk) occupy, which the swizzle XORs
+// and never carries into, so they are one XOR away.
 template <int D>
 struct Offsets {
-  uint32_t row[D / 16], tlo[D / 32], thi[D / 32];
+  uint32_t row0, tlo0, thi0;
   __device__ __forceinline__ Offsets(int lane) {
     const uint32_t li = (uint32_t)(lane & 31), hi = (uint32_t)(lane >> 5);
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) row[ks] = toff<D>(li, 2u * ks + hi);
+    row0 = toff<D>(li, hi);
     const uint32_t grp = (uint32_t)((lane >> 4) & 3), L = (uint32_t)(lane & 15);
     const uint32_t rb = 4u * (grp >> 1) + (L >> 2);
-#pragma unroll
-    for (int blk = 0; blk < D / 32; ++blk) {
-      const uint32_t col = 32u * blk + 16u * (grp & 1u) + 4u * (L & 3u);
-      tlo[blk] = toff<D>(rb, col >> 3) + (col & 7u) * 2u;
-      thi[blk] = toff<D>(rb + 8u, col >> 3) + (col & 7u) * 2u;
-    }
+    const uint32_t col = 16u * (grp & 1u) + 4u * (L & 3u);
+    tlo0 = toff<D>(rb, col >> 3) + (col & 7u) * 2u;
+    thi0 = toff<D>(rb + 8u, col >> 3) + (col & 7u) * 2u;
   }
+  // A copy the compiler cannot hoist out of a loop over `salt` (an empty
+  // asm that depends on it): the XORs then stay in the loop body instead of
+  // occupying 16 registers across it.
+  __device__ __forceinline__ Offsets fresh(uint32_t salt) const {
+    Offsets o = *this;
+    asm("" : "+v"(o.row0), "+v"(o.tlo0), "+v"(o.thi0) : "s"(salt));
+    return o;
+  }
+  __device__ __forceinline__ uint32_t row(int ks) const { return row0 ^ (32u * (uint32_t)ks); }
+  __device__ __forceinline__ uint32_t tlo(int blk) const { return tlo0 ^ (64u * (uint32_t)blk); }
+  __device__ __forceinline__ uint32_t thi(int blk) const { return thi0 ^ (64u * (uint32_t)blk); }
 };
 
 // A operand X^T (d block blk, tile rows 16 kq .. +15 in the accumulator's
@@ -153,8 +163,8 @@ struct Offsets {
 template <int D>
 __device__ __forceinline__ bf16x8_t tr_operand(const unsigned char *tile, const Offsets<D> &o, int blk, int kq) {
   const uint32_t step = (uint32_t)kq * 16u * (uint32_t)(D * 2);
-  const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(tile + o.tlo[blk] + step));
-  const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(tile + o.thi[blk] + step));
+  const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(tile + o.tlo(blk) + step));
+  const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(tile + o.thi(blk) + step));
   const v8s_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return __builtin_bit_cast(bf16x8_t, v);
 }
@@ -178,7 +188,20 @@ __device__ __forceinline__ f32x16_t dot_rows(const unsigned char *tile, const Of
   f32x16_t acc = {};
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks)
-    acc = mfma16(__builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(tile + o.row[ks])), w[ks], acc);
+    acc = mfma16(__builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(tile + o.row(ks))), w[ks], acc);
+  return acc;
+}
+
+// The same product with W's rows also in LDS (rows li, same swizzle), read
+// at the same offsets as the tile's.
+template <int D>
+__device__ __forceinline__ f32x16_t dot_rows_lds(const unsigned char *tile, const Offsets<D> &o,
+                                                 const unsigned char *wrows) {
+  f32x16_t acc = {};
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+    acc = mfma16(__builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(tile + o.row(ks))),
+                 __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(wrows + o.row(ks))), acc);
   return acc;
 }
 
@@ -256,6 +279,8 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
   // Queries past M: +inf makes every probability exp2(-inf) = 0.
   const float lse2 = qi < a.M ? a.lse[(size_t)sl.bh * a.M + qi] * kLog2e : INFINITY;
   const float c = a.scale_log2;
+  // Here the 16 per-lane offsets stay in registers (hoisted): this pass
+  // has room below 256 VGPRs, and recomputing them was 1.5 % slower.
   const Offsets<D> off(lane);
 
   f32x16_t dq[DB];
@@ -305,11 +330,13 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
 
 // dK / dV pass: a wave owns 32 keys and streams Q / dO tiles with their
 // lse and D_m.
-template <int D, bool CAUSAL, int kW, int TR>
+template <int D, bool CAUSAL, int kW, int TR, bool VL = false>
 __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
   constexpr int DB = D / 32, TB = TR * D * 2, RB = D * 2;
   __shared__ __attribute__((aligned(16))) unsigned char lds[2][2][TB];  // [stage][Q, dO]
   __shared__ __attribute__((aligned(16))) float rowv[2][2][TR];          // [stage][lse2, D_m]
+  // VL: each wave's V rows in LDS instead of 32 registers per lane.
+  __shared__ __attribute__((aligned(16))) unsigned char vrows[VL ? kW : 1][VL ? kR * RB : 16];
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
   const int li = lane & 31, hi = lane >> 5;
   const uint32_t nbh = gridDim.x / a.q_tiles;  // q_tiles holds the key tiles here
@@ -343,7 +370,11 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
 #pragma unroll
   for (int blk = 0; blk < DB; ++blk) dk[blk] = dv[blk] = f32x16_t{};
   const float c = a.scale_log2;
-  const Offsets<D> off(lane);
+  const Offsets<D> offs(lane);
+  if constexpr (VL) {
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) *reinterpret_cast<bf16x8_t *>(vrows[wave] + offs.row(ks)) = vf[ks];
+  }
 
   TilePairB<D, kW, TR> pf;
   float rl = INFINITY, rd = 0.0f;  // lse2 / D_m of row threadIdx.x (< TR)
@@ -373,6 +404,9 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
       pf.fetch(Q, a.ldq, dO, a.ldo, mbeg + (t + 1) * TR, a.M);
       fetch_rows(mbeg + (t + 1) * TR);
     }
+    // Offsets recomputed per tile: 13 fewer live registers (the 8-wave pass
+    // spills 36 instead of 48; 7 % faster, the causal 4-wave pass 3 %).
+    const Offsets<D> off = offs.fresh(t);
     // The tile in 32-query blocks (the swizzle repeats every 16 rows).
 #pragma unroll
     for (int sb = 0; sb < TR / kR; ++sb) {
@@ -380,7 +414,9 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
       const unsigned char *Qt = lds[st][0] + sb * kR * RB, *Gt = lds[st][1] + sb * kR * RB;
       if ((TR == kR || m0 < a.M) && (!CAUSAL || (int64_t)m0 + kR - 1 >= wfirst)) {
         f32x16_t s = dot_rows<D>(Qt, off, kf);         // S [query][key]
-        const f32x16_t dp = dot_rows<D>(Gt, off, vf);  // dP = dO V^T
+        f32x16_t dp;  // dP = dO V^T
+        if constexpr (VL) dp = dot_rows_lds<D>(Gt, off, vrows[wave]);
+        else dp = dot_rows<D>(Gt, off, vf);
         const bool edge = CAUSAL && (int64_t)m0 < wfirst + kR - 1;
         f32x16_t ds;
 #pragma unroll
@@ -424,9 +460,11 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
 
 // 4 waves (128 rows) per block: each streamed tile feeds twice the rows of
 // a 2-wave block (measured 5-16 % faster at the C4 / C5-like shapes).  The
-// unmasked d = 128 dK/dV pass also comes with 8 waves (256 keys per block;
-// 19 % faster at the C4 shape, slower when causal or at d = 64).  The
-// runtime launches 64 * waves threads and 32 * waves rows per block.
+// d = 128 dK/dV pass also comes with 8 waves (256 keys per block, two
+// waves per SIMD), its V rows in LDS rather than registers (no spills;
+// 14 % faster than with them in registers): at the C4 shape 1.35 ms
+// unmasked against 1.8 for the 4-wave pass, 0.83 ms causal against 1.17.
+// The runtime launches 64 * waves threads and 32 * waves rows per block.
 // 64-row streamed tiles halve the barriers and prefetch rounds per row
 // (dQ and the causal dK/dV pass 8-9 % faster at the C4 shape); the 8-wave
 // pass keeps 32-row tiles, which it needs to stay within 256 VGPRs.
@@ -447,5 +485,8 @@ BWPP_ATTN_BWD_BF16(64, true, _causal)
 BWPP_ATTN_BWD_BF16(128, false, )
 BWPP_ATTN_BWD_BF16(128, true, _causal)
 extern "C" __global__ __launch_bounds__(512) void bwpp_attn_bwd_bf16_mfma_d128_dkdv_w8(const BwppAttnArgs a) {
-  bwd_dkdv<128, false, 8, kR>(a);
+  bwd_dkdv<128, false, 8, kR, true>(a);
+}
+extern "C" __global__ __launch_bounds__(512) void bwpp_attn_bwd_bf16_mfma_d128_causal_dkdv_w8(const BwppAttnArgs a) {
+  bwd_dkdv<128, true, 8, kR, true>(a);
 }

@@ -89,7 +89,8 @@ struct BwppHip {
   hipFunction_t attn_f32_fwd[2][2] = {}, attn_f32_dq[2][2] = {}, attn_f32_dkdv[2][2] = {};
   // bf16 MFMA attention backward, head dim 64 / 128: [d128][causal]
   hipFunction_t attn_bf16_dq[2][2] = {}, attn_bf16_dkdv[2][2] = {};
-  hipFunction_t attn_bf16_dkdv_w8 = nullptr;  // d = 128, unmasked, 8 waves per block
+  hipFunction_t attn_bf16_dkdv_w8[2] = {};  // d = 128, 8 waves per block; [causal]
+  uint32_t attn_w8_mask = 3u;  // BWPP_ATTN_BWD_W8: bit c set = 8-wave dK/dV pass allowed when causal == c
   hipFunction_t attn_conv_to_f32 = nullptr, attn_conv_to_bf16 = nullptr;  // bf16 <-> fp32 operand copies
   hipFunction_t rmsnorm_grad_w[4] = {};  // wave-per-row rmsnorm_grad, 256 / 512 / 1024 / 2048 columns
   hipFunction_t silu_grad = nullptr, softmax_grad = nullptr, rmsnorm_grad = nullptr, col_partials_sum = nullptr,
@@ -168,7 +169,8 @@ BwppHipStatus resolve_all(BwppHip *h) {
       {"bwpp_rmsnorm_grad_w1", &h->rmsnorm_grad_w[0]}, {"bwpp_rmsnorm_grad_w2", &h->rmsnorm_grad_w[1]},
       {"bwpp_rmsnorm_grad_w4", &h->rmsnorm_grad_w[2]}, {"bwpp_rmsnorm_grad_w8", &h->rmsnorm_grad_w[3]},
       {"bwpp_attn_conv_bf16_to_f32", &h->attn_conv_to_f32}, {"bwpp_attn_conv_f32_to_bf16", &h->attn_conv_to_bf16},
-      {"bwpp_attn_bwd_bf16_mfma_d128_dkdv_w8", &h->attn_bf16_dkdv_w8},
+      {"bwpp_attn_bwd_bf16_mfma_d128_dkdv_w8", &h->attn_bf16_dkdv_w8[0]},
+      {"bwpp_attn_bwd_bf16_mfma_d128_causal_dkdv_w8", &h->attn_bf16_dkdv_w8[1]},
   };
   for (auto &e : singles)
     if ((s = resolve(h, e.name, e.slot)) != BWPP_HIP_OK) return s;
@@ -337,6 +339,7 @@ BwppHipStatus bwpp_hip_create(BwppHip **out, int device, const char *code_object
   if (const char *gc = getenv("BWPP_ROW_GRID")) h->row_grid_cap = (uint32_t)strtoul(gc, nullptr, 10);
   if (const char *gw = getenv("BWPP_GEMM_WAVES")) h->gemm_waves = (uint32_t)strtoul(gw, nullptr, 10) == 4 ? 4 : 8;
   if (const char *sk = getenv("BWPP_GEMM_SPLITK")) h->gemm_splitk = atoi(sk) != 0 ? 1u : 0u;
+  if (const char *w8 = getenv("BWPP_ATTN_BWD_W8")) h->attn_w8_mask = (uint32_t)strtoul(w8, nullptr, 10) & 3u;
   if (const char *gm = getenv("BWPP_GEMM_GROUP_M")) {
     const uint32_t v = (uint32_t)strtoul(gm, nullptr, 10);
     if (v > 0) h->gemm_group_m = v;
@@ -968,9 +971,13 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
     return run_mfma(g, h->attn_f32_dq[f32v][causal], h->attn_f32_dkdv[f32v][causal]);
   const int bf16v = attn_bf16_bwd_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
   if (bf16v >= 0) {
-    // Unmasked d = 128: the dK/dV pass with 8 waves (256 keys) per block.
-    if (bf16v == 1 && !causal)
-      return run_mfma(g, h->attn_bf16_dq[1][0], h->attn_bf16_dkdv_w8, kAttnWaves, 8);
+    // d = 128: the dK/dV pass with 8 waves (256 keys) per block (one block
+    // per CU).  Causal only when that grid still gives every CU a block:
+    // below that the 4-wave pass's twice as many blocks win (B2 H8 S1000:
+    // 112 against 130 us).
+    const uint64_t w8_blocks = slices * ((p.N + 255ull) / 256ull);
+    if (bf16v == 1 && ((h->attn_w8_mask >> causal) & 1u) && (!causal || w8_blocks >= (uint64_t)h->cus))
+      return run_mfma(g, h->attn_bf16_dq[1][causal], h->attn_bf16_dkdv_w8[causal], kAttnWaves, 8);
     return run_mfma(g, h->attn_bf16_dq[bf16v][causal], h->attn_bf16_dkdv[bf16v][causal]);
   }
   if (bf && p.K == p.D && (p.K == 64 || p.K == 128) && std::isfinite(scale)) {

@@ -194,6 +194,58 @@ def test_bf16_grad_unaligned_rows(be, oracle, B, H, M, N, D, causal):
     _bf16_grad_case(be, oracle, B, H, M, N, D, causal, D + 4)
 
 
+def _backend_with(monkeypatch, w8_mask):
+    monkeypatch.setenv("BWPP_ATTN_BWD_W8", str(w8_mask))
+    be = bwpp.HipBackend(0)
+    be.set_stream(_torch().cuda.current_stream())
+    return be
+
+
+@pytest.mark.parametrize("M,N", [(40, 70), (70, 40)])
+def test_bf16_grad_causal_8wave(oracle, monkeypatch, M, N):
+    """Causal d = 128 with 256 slices: slices x ceil(N / 256) = 256 blocks
+    give every CU one, so the runtime takes the 8-wave dK/dV pass (256 keys
+    per block, V rows in LDS) -- checked against the oracle."""
+    be = _backend_with(monkeypatch, 3)
+    try:
+        _bf16_grad_case(be, oracle, 1, 256, M, N, 128, True, 128)
+    finally:
+        be.close()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_grad_8wave_matches_4wave(monkeypatch, causal):
+    """The 8-wave dK/dV pass against the 4-wave one (BWPP_ATTN_BWD_W8=0) at a
+    shape with several 256-key blocks per slice, M < N and partial tiles:
+    both add the same 32-query blocks in the same order, so dQ, dK, dV are
+    bit-identical."""
+    torch = _torch()
+    B, H, M, N, D = 1, 64, 600, 1000, 128
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    q = torch.randn(B, H, M, D, device="cuda", generator=gen).bfloat16()
+    k = torch.randn(B, H, N, D, device="cuda", generator=gen).bfloat16()
+    v = torch.randn(B, H, N, D, device="cuda", generator=gen).bfloat16()
+    do = torch.randn(B, H, M, D, device="cuda", generator=gen).bfloat16()
+    prm = bwpp.AttentionParams(M=M, N=N, K=D, D=D, ldq=D, ldk=D, ldv=D, ldo=D, batch=B, heads=H,
+                               scale=D ** -0.5, causal=int(causal), dtype=int(bwpp.DType.BF16))
+    outs = []
+    for mask in (3, 0):
+        be = _backend_with(monkeypatch, mask)
+        try:
+            o = torch.empty_like(q)
+            lse = torch.empty(B, H, M, device="cuda")
+            be.dispatch_attention_lse(q, k, v, o, lse, prm)
+            g = [torch.full_like(t, 7.0) for t in (q, k, v)]
+            be.dispatch_attention_grad(q, k, v, o, do, lse, *g, prm)
+            torch.cuda.synchronize()
+            outs.append(g)
+        finally:
+            be.close()
+    for a, b in zip(*outs):
+        assert torch.isfinite(a.float()).all()
+        assert torch.equal(a, b)
+
+
 def _bf16_grad_case(be, oracle, B, H, M, N, D, causal, ld):
     torch = _torch()
     seed = B * 100 + M + N
