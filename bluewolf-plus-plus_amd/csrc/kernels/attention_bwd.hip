@@ -13,8 +13,9 @@
 // Work layout as in the fp32 kernels, with 4 waves per block: each wave
 // owns 32 rows (queries in the dQ pass, keys in the dK/dV pass) and the
 // block streams 64-row tiles of the other side through a two-stage LDS
-// ring (register prefetch of tile t+1 during tile t, one barrier per tile)
-// and works through each tile in 32-row blocks.
+// ring (tile t+1 goes straight from global memory into LDS with
+// global_load_lds while tile t is used, one barrier per tile) and works
+// through each tile in 32-row blocks.
 //
 // MFMA operands (32x32x16 bf16): lane l supplies A[l % 32][8 (l / 32) ..
 // +7] and B[8 (l / 32) .. +7][l % 32]; accumulator register r of lane l is
@@ -73,39 +74,51 @@ __device__ __forceinline__ uint32_t toff(uint32_t r, uint32_t c) {
   return r * (uint32_t)(D * 2) + 16u * (c ^ swz<D>(r));
 }
 
-// Two [TR x D] bf16 tiles (rows r0.., zeros past `rows`) copied by the
-// block from global memory into registers, then into an LDS stage.
-template <int D, int W, int TR>
-struct TilePairB {
-  static constexpr int CH = D / 8;                                // 16-byte chunks per row
-  static constexpr int TOT = TR * CH;                             // chunks per tile
-  static constexpr int PER = (TOT + 64 * W - 1) / (64 * W);       // chunks per thread per tile
-  static constexpr bool kPart = TOT % (64 * W) != 0;              // some threads hold fewer
-  u32x4_t x[PER], y[PER];
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  // s_waitcnt with expcnt / lgkmcnt at their maxima (gfx9 encoding).
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
-  // rows >= 1.  Rows past the end load row rows - 1 and are then zeroed:
-  // no branch around the loads, so they stay in flight across the tile.
-  __device__ __forceinline__ void fetch(const uint16_t *X, uint32_t ldx, const uint16_t *Y, uint32_t ldy,
-                                        uint32_t r0, uint32_t rows) {
+// 16 bytes per lane, global -> LDS (M0 holds the wave's LDS destination;
+// lane l lands at M0 + 16 l).  Inline asm, so that the compiler does not
+// put an s_waitcnt vmcnt(0) before every later LDS read; completion is
+// awaited with wait_vmcnt<0>() and a barrier before the stage is read.
+// M0 is written only here in these kernels.
+__device__ __forceinline__ void g2lds16(const void *gptr, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(gptr) : "memory");
+}
+
+// Two [TR x D] bf16 tiles (rows r0..; a row past `rows` re-reads row
+// rows - 1, which the callers mask) loaded straight into an LDS stage in
+// 1 KiB blocks: lane l of block b fills physical chunk l % (D / 8) of tile
+// row b (1024 / 2D) + l / (D / 8), i.e. logical chunk pc ^ swz(row).
+template <int D, int W, int TR>
+struct TileDmaB {
+  static constexpr int CH = D / 8;               // 16-byte chunks per row
+  static constexpr int RPB = 64 / CH;            // rows per 1 KiB block
+  static constexpr int BPW = TR * D * 2 / 1024 / W;  // blocks per wave per tile
+  static_assert(BPW >= 1 && BPW * W * 1024 == TR * D * 2, "tile must split into whole blocks per wave");
+  uint32_t row[BPW], col[BPW];
+  __device__ __forceinline__ TileDmaB(int wave, int lane) {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int idx = (int)threadIdx.x + i * 64 * W;
-      if (kPart && idx >= TOT) break;
-      const uint32_t row = r0 + (uint32_t)(idx / CH), c = (uint32_t)(idx % CH);
-      const uint32_t rr = row < rows ? row : rows - 1;
-      x[i] = *reinterpret_cast<const u32x4_t *>(X + (size_t)rr * ldx + 8u * c);
-      y[i] = *reinterpret_cast<const u32x4_t *>(Y + (size_t)rr * ldy + 8u * c);
-      if (row >= rows) x[i] = y[i] = u32x4_t{0u, 0u, 0u, 0u};
+    for (int i = 0; i < BPW; ++i) {
+      const uint32_t r = (uint32_t)((wave * BPW + i) * RPB + lane / CH), pc = (uint32_t)(lane % CH);
+      row[i] = r;
+      col[i] = 8u * (pc ^ swz<D>(r));
     }
   }
-  __device__ __forceinline__ void stash(unsigned char *lx, unsigned char *ly) const {
+  // lx, ly: LDS byte addresses of the two destination tiles; wv: the wave
+  // index (uniform).
+  __device__ __forceinline__ void issue(const uint16_t *X, uint32_t ldx, const uint16_t *Y, uint32_t ldy,
+                                        uint32_t r0, uint32_t rows, uint32_t lx, uint32_t ly, uint32_t wv) const {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int idx = (int)threadIdx.x + i * 64 * W;
-      if (kPart && idx >= TOT) break;
-      const uint32_t off = toff<D>((uint32_t)(idx / CH), (uint32_t)(idx % CH));
-      *reinterpret_cast<u32x4_t *>(lx + off) = x[i];
-      *reinterpret_cast<u32x4_t *>(ly + off) = y[i];
+    for (int i = 0; i < BPW; ++i) {
+      const uint32_t r = r0 + row[i], rr = r < rows ? r : rows - 1;
+      const uint32_t dst = (wv * BPW + (uint32_t)i) * 1024u;
+      g2lds16(X + (size_t)rr * ldx + col[i], lx + dst);
+      g2lds16(Y + (size_t)rr * ldy + col[i], ly + dst);
     }
   }
 };
@@ -287,15 +300,21 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
 #pragma unroll
   for (int blk = 0; blk < DB; ++blk) dq[blk] = f32x16_t{};
 
-  TilePairB<D, kW, TR> pf;
+  const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)&lds[0][0][0];
+  const TileDmaB<D, kW, TR> dma(wave, lane);
+  auto issue = [&](uint32_t t) {  // K / V tile t into stage t % 2
+    const uint32_t sb = lds0 + (t & 1u) * (uint32_t)(2 * TB);
+    dma.issue(K, a.ldk, V, a.ldv, t * TR, a.N, sb, sb + (uint32_t)TB, wv);
+  };
   if (nt > 0) {
-    pf.fetch(K, a.ldk, V, a.ldv, 0, a.N);
-    pf.stash(lds[0][0], lds[0][1]);
+    issue(0);
+    wait_vmcnt<0>();
   }
   __syncthreads();
   for (uint32_t t = 0; t < nt; ++t) {
     const int st = (int)(t & 1);
-    if (t + 1 < nt) pf.fetch(K, a.ldk, V, a.ldv, (t + 1) * TR, a.N);
+    if (t + 1 < nt) issue(t + 1);
     // The tile in 32-key blocks (the swizzle repeats every 16 rows).
 #pragma unroll
     for (int sb = 0; sb < TR / kR; ++sb) {
@@ -322,7 +341,7 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
         }
       }
     }
-    if (t + 1 < nt) pf.stash(lds[st ^ 1][0], lds[st ^ 1][1]);
+    wait_vmcnt<0>();  // tile t + 1 is in LDS (this wave's part; the barrier does the rest)
     __syncthreads();
   }
   if (qi < a.M) store_t<D>(dQ, a.ldq, qi, dq, a.scale, hi);
@@ -376,32 +395,42 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
     for (int ks = 0; ks < D / 16; ++ks) *reinterpret_cast<bf16x8_t *>(vrows[wave] + offs.row(ks)) = vf[ks];
   }
 
-  TilePairB<D, kW, TR> pf;
+  const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)&lds[0][0][0];
+  const TileDmaB<D, kW, TR> dma(wave, lane);
+  auto issue = [&](uint32_t t) {  // Q / dO tile t into stage t % 2
+    const uint32_t sb = lds0 + (t & 1u) * (uint32_t)(2 * TB);
+    dma.issue(Q, a.ldq, dO, a.ldo, mbeg + t * TR, a.M, sb, sb + (uint32_t)TB, wv);
+  };
   float rl = INFINITY, rd = 0.0f;  // lse2 / D_m of row threadIdx.x (< TR)
+  // The loads are issued with the tile's and used only when the tile is
+  // stashed: the compiler's wait for them (which also waits for the LDS
+  // DMA issued before them) then falls where the DMA is awaited anyway.
   auto fetch_rows = [&](uint32_t m0) {
     if (threadIdx.x < (uint32_t)TR) {
-      const uint32_t m = m0 + threadIdx.x;
-      rl = m < a.M ? lse[m] * kLog2e : INFINITY;
-      rd = m < a.M ? dsum[m] : 0.0f;
+      const uint32_t m = min(m0 + threadIdx.x, a.M - 1);
+      rl = lse[m];
+      rd = dsum[m];
     }
   };
-  auto stash_rows = [&](int st) {
+  auto stash_rows = [&](int st, uint32_t m0) {
     if (threadIdx.x < (uint32_t)TR) {
-      rowv[st][0][threadIdx.x] = rl;
-      rowv[st][1][threadIdx.x] = rd;
+      const bool in = m0 + threadIdx.x < a.M;
+      rowv[st][0][threadIdx.x] = in ? rl * kLog2e : INFINITY;
+      rowv[st][1][threadIdx.x] = in ? rd : 0.0f;
     }
   };
   if (nt > 0) {
-    pf.fetch(Q, a.ldq, dO, a.ldo, mbeg, a.M);
+    issue(0);
     fetch_rows(mbeg);
-    pf.stash(lds[0][0], lds[0][1]);
-    stash_rows(0);
+    stash_rows(0, mbeg);
+    wait_vmcnt<0>();
   }
   __syncthreads();
   for (uint32_t t = 0; t < nt; ++t) {
     const int st = (int)(t & 1);
     if (t + 1 < nt) {
-      pf.fetch(Q, a.ldq, dO, a.ldo, mbeg + (t + 1) * TR, a.M);
+      issue(t + 1);
       fetch_rows(mbeg + (t + 1) * TR);
     }
     // Offsets recomputed per tile: 13 fewer live registers (the 8-wave pass
@@ -444,10 +473,8 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
         }
       }
     }
-    if (t + 1 < nt) {
-      pf.stash(lds[st ^ 1][0], lds[st ^ 1][1]);
-      stash_rows(st ^ 1);
-    }
+    if (t + 1 < nt) stash_rows(st ^ 1, mbeg + (t + 1) * TR);
+    wait_vmcnt<0>();
     __syncthreads();
   }
   if (ni < a.N) {
@@ -465,9 +492,12 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
 // 14 % faster than with them in registers): at the C4 shape 1.35 ms
 // unmasked against 1.8 for the 4-wave pass, 0.83 ms causal against 1.17.
 // The runtime launches 64 * waves threads and 32 * waves rows per block.
-// 64-row streamed tiles halve the barriers and prefetch rounds per row
-// (dQ and the causal dK/dV pass 8-9 % faster at the C4 shape); the 8-wave
-// pass keeps 32-row tiles, which it needs to stay within 256 VGPRs.
+// 64-row streamed tiles halve the barriers and load rounds per row (dQ
+// and the causal dK/dV pass 8-9 % faster at the C4 shape, measured with
+// register staging); the 8-wave pass keeps 32-row tiles.  Loading the
+// tiles with global_load_lds instead of through registers made the dQ
+// pass 18-20 % and the 8-wave dK/dV pass 16-17 % faster (fewer VGPRs, no
+// LDS write instructions).
 constexpr int kWQ = 4, kWK = 4;
 constexpr int kTR = 64;  // rows per streamed K/V or Q/dO tile
 #define BWPP_ATTN_BWD_BF16(D, CAUSAL, SUFFIX)                                                   \
