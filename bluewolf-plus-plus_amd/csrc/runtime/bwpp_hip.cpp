@@ -972,11 +972,11 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   const int bf16v = attn_bf16_bwd_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
   if (bf16v >= 0) {
     // d = 128: the dK/dV pass with 8 waves (256 keys) per block (one block
-    // per CU).  Causal only when that grid still gives every CU a block:
-    // below that the 4-wave pass's twice as many blocks win (B2 H8 S1000:
-    // 112 against 130 us).
+    // per CU) when that grid still gives every CU a block; below that the
+    // 4-wave pass's twice as many blocks win (B2 H8 S1000: 90 against
+    // 102 us unmasked, 112 against 130 causal).
     const uint64_t w8_blocks = slices * ((p.N + 255ull) / 256ull);
-    if (bf16v == 1 && ((h->attn_w8_mask >> causal) & 1u) && (!causal || w8_blocks >= (uint64_t)h->cus))
+    if (bf16v == 1 && ((h->attn_w8_mask >> causal) & 1u) && w8_blocks >= (uint64_t)h->cus)
       return run_mfma(g, h->attn_bf16_dq[1][causal], h->attn_bf16_dkdv_w8[causal], kAttnWaves, 8);
     return run_mfma(g, h->attn_bf16_dq[bf16v][causal], h->attn_bf16_dkdv[bf16v][causal]);
   }

@@ -202,13 +202,14 @@ def _backend_with(monkeypatch, w8_mask):
 
 
 @pytest.mark.parametrize("M,N", [(40, 70), (70, 40)])
-def test_bf16_grad_causal_8wave(oracle, monkeypatch, M, N):
-    """Causal d = 128 with 256 slices: slices x ceil(N / 256) = 256 blocks
-    give every CU one, so the runtime takes the 8-wave dK/dV pass (256 keys
-    per block, V rows in LDS) -- checked against the oracle."""
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_grad_8wave(oracle, monkeypatch, M, N, causal):
+    """d = 128 with 256 slices: slices x ceil(N / 256) = 256 blocks give
+    every CU one, so the runtime takes the 8-wave dK/dV pass (256 keys per
+    block, V rows in LDS) -- checked against the oracle."""
     be = _backend_with(monkeypatch, 3)
     try:
-        _bf16_grad_case(be, oracle, 1, 256, M, N, 128, True, 128)
+        _bf16_grad_case(be, oracle, 1, 256, M, N, 128, causal, 128)
     finally:
         be.close()
 
