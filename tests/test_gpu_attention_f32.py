@@ -186,6 +186,23 @@ def test_bf16_grad_mfma(be, oracle, B, H, M, N, D, causal):
     _bf16_grad_case(be, oracle, B, H, M, N, D, causal, D)
 
 
+@pytest.mark.parametrize("B,H,M,N,D", [(1, 1, 1, 1, 128), (1, 2, 5, 3, 64), (2, 1, 3, 40, 128), (1, 1, 33, 2, 128)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_grad_tiny(be, oracle, B, H, M, N, D, causal):
+    """Shapes below one 32-row block: the tile loads re-read the last row
+    for every row past the end (straight into LDS), which the passes must
+    mask; M > N causal leaves queries that see no key (lse = -inf)."""
+    _bf16_grad_case(be, oracle, B, H, M, N, D, causal, D)
+
+
+@pytest.mark.parametrize("B,H,M,N,D", [(1, 2, 97, 200, 64), (1, 1, 130, 90, 128)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_grad_padded_rows(be, oracle, B, H, M, N, D, causal):
+    """Rows of D + 8 bf16 (16-byte aligned, padded): the bf16 matrix-core
+    passes load through the row stride and leave the padding untouched."""
+    _bf16_grad_case(be, oracle, B, H, M, N, D, causal, D + 8)
+
+
 @pytest.mark.parametrize("B,H,M,N,D", [(1, 2, 97, 200, 64), (1, 1, 130, 90, 128)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_bf16_grad_unaligned_rows(be, oracle, B, H, M, N, D, causal):
