@@ -159,23 +159,31 @@ def time_c2(bench, steps, warmup):
 WARM_MS = 40.0  # sustained work before any extras timing starts
 
 
-def time_c2_ops(bench, reps):
-    """Average launch duration per operator: `reps` back-to-back launches
-    over the rotating buffer sets, between two events on the launch stream."""
-    torch = bench.torch
+def _launch_times_ms(torch, fn, iters):
+    """Durations (ms) of `iters` back-to-back launches of fn: one event on
+    the launch stream before the first launch and one after each, so
+    launch i is the interval between events i and i + 1 and the stream is
+    never drained in between."""
     stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+    ev[0].record(stream)
+    for i in range(iters):
+        fn(i)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    return [ev[i].elapsed_time(ev[i + 1]) for i in range(iters)]
+
+
+def time_c2_ops(bench, reps):
+    """Median and mean launch duration per operator (ms) over `reps`
+    back-to-back launches on the rotating buffer sets."""
+    torch = bench.torch
     out = {}
     for op in C2_BYTES:
         for i in range(bench.nbuf):
             bench.launch(op, i)
-        s = torch.cuda.Event(enable_timing=True)
-        e = torch.cuda.Event(enable_timing=True)
-        s.record(stream)
-        for i in range(reps):
-            bench.launch(op, i % bench.nbuf)
-        e.record(stream)
-        torch.cuda.synchronize()
-        out[op] = s.elapsed_time(e) / reps
+        t = _launch_times_ms(torch, lambda i: bench.launch(op, i % bench.nbuf), reps)
+        out[op] = (float(np.median(t)), float(np.mean(t)))
     return out
 
 
@@ -225,6 +233,64 @@ def traffic_from_pmc(fetch_dir, write_dir):
         wb = write[k] * 1024.0 * w_scale
         out[k] = {"fetch_bytes": int(fb), "write_bytes": int(wb), "traffic": int(fb + wb)}
     return out
+
+
+def pmc_summary(dirs):
+    """Per-kernel counter table (markdown) from rocprofv3 output dirs: every
+    *counter_collection.csv (--pmc runs) and *kernel_stats.csv (--stats
+    runs) found under them.  Counters are summed over a dispatch's rows and
+    then averaged over the kernel's dispatches.  Derived columns, with
+    XCDS = 8, SIMDS = 4 per CU and CUS from the agent info:
+      clock GHz   = GRBM_GUI_ACTIVE / XCDS / kernel duration
+      MFMA busy   = SQ_VALU_MFMA_BUSY_CYCLES / (CUS * SIMDS * GRBM_GUI_ACTIVE / XCDS)
+      VALU / MFMA = SQ_INSTS_VALU / SQ_INSTS_MFMA
+    (SQ_VALU_MFMA_BUSY_CYCLES counts SIMD cycles with the matrix pipe busy,
+    summed over SIMDs; GRBM_GUI_ACTIVE counts GPU-busy cycles, summed over
+    the XCDs.)"""
+    import csv
+    import glob
+    counters, dur, cus = {}, {}, 256
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*agent_info.csv"), recursive=True):
+            with open(f, newline="") as fh:
+                for row in csv.DictReader(fh):
+                    n = int(row.get("Cu_Count", 0) or 0)
+                    if n > 0:
+                        cus = n
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            per = {}
+            with open(f, newline="") as fh:
+                for row in csv.DictReader(fh):
+                    k = row["Kernel_Name"]
+                    if not k.startswith("bwpp_"):
+                        continue
+                    key = (k, row["Dispatch_Id"])
+                    per.setdefault(key, {}).setdefault(row["Counter_Name"], 0.0)
+                    per[key][row["Counter_Name"]] += float(row["Counter_Value"])
+            for (k, _), cv in per.items():
+                for c, v in cv.items():
+                    counters.setdefault(k, {}).setdefault(c, []).append(v)
+        for f in glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True):
+            with open(f, newline="") as fh:
+                for row in csv.DictReader(fh):
+                    if row["Name"].startswith("bwpp_"):
+                        dur[row["Name"]] = float(row["AverageNs"])
+    cols = ["GRBM_GUI_ACTIVE", "SQ_BUSY_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU",
+            "SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT", "SQ_WAVES"]
+    lines = ["| kernel | avg ns | clock GHz | MFMA busy | VALU/MFMA | " + " | ".join(cols) + " |",
+             "|---" * (len(cols) + 5) + "|"]
+    for k in sorted(set(counters) | set(dur)):
+        c = {n: float(np.mean(v)) for n, v in counters.get(k, {}).items()}
+        ns = dur.get(k)
+        g = c.get("GRBM_GUI_ACTIVE")
+        clock = f"{g / 8 / ns:.2f}" if g and ns else ""
+        busy = f"{c['SQ_VALU_MFMA_BUSY_CYCLES'] / (cus * 4 * g / 8):.3f}" if g and "SQ_VALU_MFMA_BUSY_CYCLES" in c else ""
+        ratio = (f"{c['SQ_INSTS_VALU'] / c['SQ_INSTS_MFMA']:.2f}"
+                 if c.get("SQ_INSTS_MFMA") and "SQ_INSTS_VALU" in c else "")
+        vals = [f"{c[n]:.4g}" if n in c else "" for n in cols]
+        lines.append(f"| {k} | {ns:.0f} | " if ns else f"| {k} | | ")
+        lines[-1] += f"{clock} | {busy} | {ratio} | " + " | ".join(vals) + " |"
+    return "\n".join(lines)
 
 
 def cpu_baseline_c2(seed, reps):
@@ -323,31 +389,24 @@ def regress_json(args):
     return out
 
 
-def _events_us(torch, fn, iters, warm_ms=WARM_MS):
-    """Average launch time of fn over `iters` back-to-back launches, after
-    at least warm_ms of the same work: the MI355X clock ramps up over the
-    first ~35 ms of sustained matrix work (a C3 GEMM goes from ~1035 to
-    ~1180 TFLOP/s), and the figure wanted is the steady state."""
-    stream = torch.cuda.current_stream()
-    s = torch.cuda.Event(enable_timing=True)
-    e = torch.cuda.Event(enable_timing=True)
-    s.record(stream)
-    for _ in range(3):
+_WARM_MS = WARM_MS  # set by extras() from --warm-ms
+
+
+def _events_us(torch, fn, iters, warm_ms=None, stats=None):
+    """Median launch time (us) of fn over `iters` back-to-back launches,
+    after at least warm_ms of the same work: the MI355X clock ramps up over
+    the first ~35 ms of sustained matrix work (a C3 GEMM goes from ~1035 to
+    ~1180 TFLOP/s), and the figure wanted is the steady state.  `stats`, if
+    given, also receives the mean."""
+    warm_ms = _WARM_MS if warm_ms is None else warm_ms
+    t = _launch_times_ms(torch, lambda i: fn(), 3)
+    est_us = max(float(np.mean(t)) * 1e3, 1.0)
+    for _ in range(min(4000, int(warm_ms * 1e3 / est_us) + 1) if warm_ms > 0 else 0):
         fn()
-    e.record(stream)
-    torch.cuda.synchronize()
-    est_us = max(s.elapsed_time(e) / 3 * 1e3, 1.0)
-    for _ in range(min(4000, int(warm_ms * 1e3 / est_us) + 1)):
-        fn()
-    torch.cuda.synchronize()
-    s = torch.cuda.Event(enable_timing=True)
-    e = torch.cuda.Event(enable_timing=True)
-    s.record(stream)
-    for _ in range(iters):
-        fn()
-    e.record(stream)
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / iters * 1e3
+    t = _launch_times_ms(torch, lambda i: fn(), iters)
+    if stats is not None:
+        stats["us_mean"] = round(float(np.mean(t)) * 1e3, 2)
+    return float(np.median(t)) * 1e3
 
 
 def _bf16(torch, x):
@@ -355,10 +414,13 @@ def _bf16(torch, x):
     return torch.from_numpy(synth.to_bf16_bits(x).view(np.int16)).cuda().view(torch.bfloat16)
 
 
-def extras(be, torch, seed, iters, with_cpu):
-    """Contraction configs C3, C3-fp32, C4 (both masks) and C1."""
+def extras(be, torch, seed, iters, with_cpu, warm_ms=WARM_MS):
+    """Contraction configs C3, C3-fp32, C4 (both masks), the C4-shape
+    attention backward, C1 and C5."""
     import bwpp
     from bwpp import synth
+    global _WARM_MS
+    _WARM_MS = warm_ms
     out = {}
     orc = None
     if with_cpu:
@@ -374,9 +436,10 @@ def extras(be, torch, seed, iters, with_cpu):
     x, w, b = _bf16(torch, xh), _bf16(torch, wh), _bf16(torch, bh)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     p = bwpp.MatmulParams(M, N, K, K, N, N, int(bwpp.DType.BF16), 3, 0, 0)
-    us = _events_us(torch, lambda: be.dispatch_matmul(x, w, y, b, p), iters)
+    st = {}
+    us = _events_us(torch, lambda: be.dispatch_matmul(x, w, y, b, p), iters, stats=st)
     fl = 2.0 * M * N * K
-    c3 = {"kernel": "bwpp_gemm_bf16w8_t00_f", "us_per_launch": round(us, 1),
+    c3 = {"kernel": be.last_kernel, "us_per_launch": round(us, 1), **st,
           "TFLOP_s": round(fl / us / 1e6, 1), "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
     if orc is not None:
         rows = 32
@@ -398,14 +461,24 @@ def extras(be, torch, seed, iters, with_cpu):
     bf = torch.from_numpy(synth.uniform((n,), seed, 2, -1, 1)).cuda()
     yf = torch.empty((n, n), device="cuda")
     p = bwpp.MatmulParams(n, n, n, n, n, n, int(bwpp.DType.F32), 3, 0, 0)
-    us = _events_us(torch, lambda: be.dispatch_matmul(xf, wf, yf, bf, p), iters)
+    st = {}
+    us = _events_us(torch, lambda: be.dispatch_matmul(xf, wf, yf, bf, p), iters, stats=st)
     fl = 2.0 * n ** 3
     # 256 tiles of 128 x 128 fill half the chip: the dispatcher splits K in
     # two (bwpp_gemm_f32_t00_s) and adds the halves in a reduce pass.
-    out["c3_gemm_f32_2048"] = {"kernel": "bwpp_gemm_f32_t00_s + bwpp_gemm_f32_splitk_reduce",
-                               "us_per_launch": round(us, 1),
-                               "TFLOP_s": round(fl / us / 1e6, 1),
-                               "frac_f32_peak": round(fl / us / 1e6 / F32_PEAK_TFLOPS, 4)}
+    c3f = {"kernel": "bwpp_gemm_f32_t00_s + bwpp_gemm_f32_splitk_reduce",
+           "us_per_launch": round(us, 1), **st,
+           "TFLOP_s": round(fl / us / 1e6, 1),
+           "frac_f32_peak": round(fl / us / 1e6 / F32_PEAK_TFLOPS, 4)}
+    if orc is not None:
+        rows = 256
+        xr, wr, br = xf[:rows].cpu().numpy(), wf.cpu().numpy(), bf.cpu().numpy()
+        t0 = time.perf_counter()
+        orc.matmul(xr, wr, br, apply_silu=True, apply_bias=True)
+        dt = time.perf_counter() - t0
+        c3f["cpu"] = {"GFLOP_s": round(2.0 * rows * n * n / dt / 1e9, 3), "cores": 1, "kind": "port",
+                      "sample": f"first {rows} rows (exact rows; extrapolated rate)"}
+    out["c3_gemm_f32_2048"] = c3f
     # C1: 256^3 fp32 (latency)
     a1, b1 = xf[:256, :256].contiguous(), wf[:256, :256].contiguous()
     c1 = torch.empty((256, 256), device="cuda")
@@ -425,10 +498,11 @@ def extras(be, torch, seed, iters, with_cpu):
     for causal in (0, 1):
         p = bwpp.AttentionParams(M=S, N=S, K=d, D=d, ldq=d, ldk=d, ldv=d, ldo=d, batch=B, heads=H,
                                  scale=d ** -0.5, causal=causal, dtype=int(bwpp.DType.BF16))
-        us = _events_us(torch, lambda: be.dispatch_attention(q, k, v, o, p), iters)
+        st = {}
+        us = _events_us(torch, lambda: be.dispatch_attention(q, k, v, o, p), iters, stats=st)
         fl = full / 2 if causal else full
-        entry = {"kernel": "bwpp_attn_bf16_d128" + ("_causal" if causal else ""),
-                 "us_per_launch": round(us, 1), "TFLOP_s": round(fl / us / 1e6, 1),
+        entry = {"kernel": be.last_kernel,
+                 "us_per_launch": round(us, 1), **st, "TFLOP_s": round(fl / us / 1e6, 1),
                  "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
         if orc is not None:
             sl = lambda t: synth.bf16_bits_to_f32(synth.to_bf16_bits(t[:1, :1]))
@@ -448,15 +522,24 @@ def extras(be, torch, seed, iters, with_cpu):
         p = bwpp.AttentionParams(M=S, N=S, K=d, D=d, ldq=d, ldk=d, ldv=d, ldo=d, batch=B, heads=H,
                                  scale=d ** -0.5, causal=causal, dtype=int(bwpp.DType.BF16))
         be.dispatch_attention_lse(q, k, v, o, lse, p)
+        st = {}
         us = _events_us(torch, lambda: be.dispatch_attention_grad(q, k, v, o, dout, lse, dq, dk, dv, p),
-                        max(3, iters // 3))
+                        max(3, iters // 3), stats=st)
         fl = 2.5 * (full / 2 if causal else full)
-        out["c4_attention_grad_bf16" + ("_causal" if causal else "")] = {
-            "kernel": "bwpp_attn_bwd_bf16_mfma_d128" + ("_causal" if causal else "") + "_{dq,dkdv}",
-            "us_per_launch": round(us, 1), "TFLOP_s": round(fl / us / 1e6, 1),
-            "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
+        entry = {"kernel": "bwpp_attn_bwd_bf16_mfma_d128" + ("_causal" if causal else "") + "_dq + " + be.last_kernel,
+                 "us_per_launch": round(us, 1), **st, "TFLOP_s": round(fl / us / 1e6, 1),
+                 "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
+        if orc is not None:
+            sl = lambda t: synth.bf16_bits_to_f32(synth.to_bf16_bits(t[:1, :1]))
+            g1 = synth.bf16_bits_to_f32(synth.to_bf16_bits(synth.normal((1, 1, S, d), seed, 3)))
+            t0 = time.perf_counter()
+            orc.attention_grad(sl(qh), sl(kh), sl(vh), g1, d ** -0.5, bool(causal))
+            dt = time.perf_counter() - t0
+            entry["cpu"] = {"GFLOP_s": round(fl / (B * H) / dt / 1e9, 3), "cores": 1, "kind": "port",
+                            "sample": "one (batch, head) slice (extrapolated rate)"}
+        out["c4_attention_grad_bf16" + ("_causal" if causal else "")] = entry
     del q, k, v, o, dout, dq, dk, dv
-    out["c5_block_train_f32"] = block_train(be, torch, seed, max(3, iters // 4))
+    out["c5_block_train_f32"] = block_train(be, torch, seed, max(3, iters // 4), with_cpu=orc is not None)
     return out
 
 
@@ -470,27 +553,48 @@ def block_train_flop(B, T, D, H, F):
     return 3.0 * gemm + 3.0 * attn
 
 
-def block_train(be, torch, seed, iters, B=8, T=512, D=1024, H=16, F=4096):
+def block_inputs(seed, B, T, D, F):
+    """C5's synthetic inputs from the repo's SplitMix64 generator: x ~ N(0,1),
+    gamma ~ U[0.5,1.5], weights ~ N(0,0.02)."""
+    from bwpp import synth
+    w = lambda shape, st: synth.normal(shape, seed, st, 0.0, 0.02)
+    return {"x": synth.normal((B * T, D), seed, 0), "g1": synth.uniform((D,), seed, 1, 0.5, 1.5),
+            "wqkv": w((D, 3 * D), 2), "wo": w((D, D), 3), "g2": synth.uniform((D,), seed, 4, 0.5, 1.5),
+            "w1": w((D, F), 5), "w2": w((F, D), 6)}
+
+
+def block_train(be, torch, seed, iters, B=8, T=512, D=1024, H=16, F=4096, with_cpu=False):
     """C5: one forward + backward step of the pre-norm transformer block
-    (bwpp_ir/compiler/transformer_block.py) in fp32, run by the launch-plan
-    executor from its plan file over one mem-planned device arena."""
+    (examples/tiny_model.bwpp's `block`, 16 causal heads) in fp32, run by
+    the launch-plan executor from its plan file over one mem-planned device
+    arena.  The CPU leg runs the same plan text for one sample (B = 1) on
+    the oracle (oracle/plan_cpu.py), one core."""
     from bwpp import plan
     text = plan.load_text("transformer_block_train", B=B, T=T, D=D, H=H, F=F)
     p = plan.Plan(be, text)
     p.allocate()
-    g = torch.Generator(device="cuda")
-    g.manual_seed(seed)
-    rnd = lambda *shape, std=0.02: torch.randn(*shape, generator=g, device="cuda") * std
-    tensors = {"x": rnd(B * T, D, std=1.0), "g1": 1.0 + rnd(D, std=0.1), "wqkv": rnd(D, 3 * D),
-               "wo": rnd(D, D), "g2": 1.0 + rnd(D, std=0.1), "w1": rnd(D, F), "w2": rnd(F, D)}
-    for name, t in tensors.items():
-        p.bind(name, t)
-    us = _events_us(torch, p.run, iters)
+    for name, a in block_inputs(seed, B, T, D, F).items():
+        p.bind(name, torch.from_numpy(a).cuda())
+    st = {}
+    us = _events_us(torch, p.run, iters, stats=st)
     fl = block_train_flop(B, T, D, H, F)
     res = {"workload": f"B{B} T{T} D{D} H{H} F{F} fp32 fwd+bwd", "us_per_step": round(us, 1),
+           "us_mean": st.get("us_mean"),
            "TFLOP_s": round(fl / us / 1e6, 1), "frac_f32_peak": round(fl / us / 1e6 / F32_PEAK_TFLOPS, 4),
            "arena_bytes": p.arena_bytes, "ops_per_step": sum(1 for ln in text.splitlines() if ln.startswith("op "))}
     p.close()
+    if with_cpu:
+        sys.path.insert(0, ROOT)
+        from oracle.plan_cpu import CpuPlan
+        cp = CpuPlan(plan.load_text("transformer_block_train", B=1, T=T, D=D, H=H, F=F))
+        for name, a in block_inputs(seed, 1, T, D, F).items():
+            cp.bind(name, a)
+        t0 = time.perf_counter()
+        cp.run()
+        dt = time.perf_counter() - t0
+        res["cpu"] = {"GFLOP_s": round(block_train_flop(1, T, D, H, F) / dt / 1e9, 3), "cores": 1, "kind": "port",
+                      "sample": f"one sample (B=1) fwd+bwd through the same plan on the oracle, {dt:.1f} s "
+                                "(extrapolated rate)"}
     return res
 
 
@@ -518,7 +622,19 @@ def main():
     ap.add_argument("--rows", type=int, default=256)
     ap.add_argument("--cols", type=int, default=256)
     ap.add_argument("--iters", type=int, default=10)
+    ap.add_argument("--no-c2", action="store_true",
+                    help="skip the C2 headline (with --no-extras off: time the contractions only)")
+    ap.add_argument("--extras-iters", type=int, default=30, help="timed launches per contraction config")
+    ap.add_argument("--warm-ms", type=float, default=WARM_MS,
+                    help="sustained work before each contraction is timed (0 for counter runs)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="no GPU: print a markdown table of per-kernel counters from rocprofv3 --pmc "
+                         "(and --kernel-trace) output dirs")
     args = ap.parse_args()
+
+    if args.pmc_summary:
+        print(pmc_summary(args.pmc_summary))
+        return
 
     if args.regress_json:
         out = regress_json(args)
@@ -549,6 +665,13 @@ def main():
     be = bwpp.HipBackend(0)
     be.set_stream(torch.cuda.current_stream())
 
+    if args.no_c2:
+        out = {"metric": METRIC, "config": {"workload": "contractions only (no headline)"},
+               "extras": extras(be, torch, args.seed, args.extras_iters, not args.no_cpu, args.warm_ms)}
+        be.close()
+        print(json.dumps(out))
+        return
+
     bench = C2Bench(be, torch, args.seed, args.nbuf)
     torch.cuda.synchronize()
     wall, gpu_s = time_c2(bench, args.steps, args.warmup)
@@ -559,14 +682,15 @@ def main():
     ms_per_step = wall / args.steps * 1e3
     value = step_bytes / (wall / args.steps) / 1e9
 
-    dom = max(per_op_ms, key=per_op_ms.get)
-    achieved = C2_BYTES[dom] / (per_op_ms[dom] * 1e-3) / 1e9
+    dom = max(per_op_ms, key=lambda op: per_op_ms[op][0])
+    achieved = C2_BYTES[dom] / (per_op_ms[dom][0] * 1e-3) / 1e9
     tr = load_traffic().get(C2_KERNEL[dom])
     traffic = tr["traffic"] if tr else None
     ops = {}
-    for op, ms in per_op_ms.items():
+    for op, (ms, mean_ms) in per_op_ms.items():
         gbs = C2_BYTES[op] / (ms * 1e-3) / 1e9
         ops[op] = {"kernel": C2_KERNEL[op], "us_per_launch": round(ms * 1e3, 2),
+                   "us_mean": round(mean_ms * 1e3, 2),
                    "algorithmic_bytes": C2_BYTES[op], "GB_s": round(gbs, 1),
                    "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         t = load_traffic().get(C2_KERNEL[op])
@@ -592,6 +716,7 @@ def main():
                    "rows": ROWS, "cols": COLS, "seed": args.seed, "rotating_buffer_sets": args.nbuf,
                    "step_algorithmic_bytes": step_bytes},
         "roofline": {"bound": "hbm", "kernel": C2_KERNEL[dom], "op": dom,
+                     "us_per_launch": round(per_op_ms[dom][0] * 1e3, 2), "timing": "median",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "ops": ops,
@@ -604,7 +729,7 @@ def main():
     del bench
     if not args.no_extras:
         torch.cuda.empty_cache()
-        out["extras"] = extras(be, torch, args.seed, 30, not args.no_cpu)
+        out["extras"] = extras(be, torch, args.seed, args.extras_iters, not args.no_cpu, args.warm_ms)
     be.close()
     print(json.dumps(out))
 

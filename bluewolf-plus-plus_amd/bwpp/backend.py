@@ -83,6 +83,11 @@ class HipBackend:
     def cus(self) -> int:
         return self.lib.bwpp_hip_device_cus(self._h)
 
+    @property
+    def last_kernel(self) -> str:
+        """Symbol of the last kernel this handle launched ('' if none)."""
+        return self.lib.bwpp_hip_last_kernel(self._h).decode()
+
     # --------------------------------------------------------- operators
     def dispatch_matmul(self, a, b, c, bias, params: MatmulParams):
         self._check(self.lib.bwpp_hip_dispatch_matmul(

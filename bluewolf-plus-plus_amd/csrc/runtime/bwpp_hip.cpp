@@ -63,6 +63,8 @@ struct BwppHip {
   hipStream_t stream = nullptr;
   std::vector<hipModule_t> modules;
   std::unordered_map<hipFunction_t, uint32_t> max_threads;  // per resolved kernel
+  std::unordered_map<hipFunction_t, std::string> names;     // symbol of each resolved kernel
+  const std::string *last_kernel = nullptr;                 // symbol of the last launch
   std::string err;
   int row_cfg_override = -1;  // BWPP_ROW_CFG: index into kRowCfgs (tuning)
   uint32_t row_grid_cap = 0;  // BWPP_ROW_GRID: max blocks per row launch (0 = per-op default)
@@ -131,6 +133,7 @@ BwppHipStatus resolve(BwppHip *h, const std::string &name, hipFunction_t *out) {
       if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, f) != hipSuccess || mt <= 0)
         return fail(h, BWPP_HIP_ERR_HIP, "hipFuncGetAttribute(%s) failed", name.c_str());
       h->max_threads[f] = (uint32_t)mt;
+      h->names[f] = name;
       *out = f;
       return BWPP_HIP_OK;
     }
@@ -250,6 +253,8 @@ BwppHipStatus launch(BwppHip *h, hipFunction_t f, uint32_t gx, uint32_t gy, uint
   void *params[] = {const_cast<Args *>(&args)};
   hipError_t e = hipModuleLaunchKernel(f, gx, gy, gz, bx, 1, 1, shmem, h->stream, params, nullptr);
   if (e != hipSuccess) return fail(h, BWPP_HIP_ERR_HIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
+  const auto nm = h->names.find(f);
+  h->last_kernel = nm == h->names.end() ? nullptr : &nm->second;
   return BWPP_HIP_OK;
 }
 
@@ -380,7 +385,24 @@ void bwpp_hip_destroy(BwppHip *h) {
 
 BwppHipStatus bwpp_hip_set_stream(BwppHip *h, void *hip_stream) {
   if (!h) return BWPP_HIP_ERR_INVALID_ARG;
-  h->stream = (hipStream_t)hip_stream;
+  const hipStream_t ns = (hipStream_t)hip_stream;
+  if (ns == h->stream) return BWPP_HIP_OK;
+  if (h->ws) {
+    // The workspace (split-K partial planes, attention D rows, column
+    // partials) is ordered on the handle's stream.  Work still queued on the
+    // old stream may read or write it, so the new stream waits for that
+    // work before anything launched on it can touch the workspace.
+    BwppHipStatus s = enter(h);
+    if (s != BWPP_HIP_OK) return s;
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(ev, h->stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(ns, ev, 0);
+    if (ev) (void)hipEventDestroy(ev);
+    if (e != hipSuccess) return fail(h, BWPP_HIP_ERR_HIP, "set_stream: ordering after the old stream: %s",
+                                     hipGetErrorString(e));
+  }
+  h->stream = ns;
   return BWPP_HIP_OK;
 }
 
@@ -397,6 +419,10 @@ BwppHipStatus bwpp_hip_sync(BwppHip *h) {
 const char *bwpp_hip_last_error(const BwppHip *h) { return h ? h->err.c_str() : g_create_error.c_str(); }
 
 int bwpp_hip_device_cus(const BwppHip *h) { return h ? h->cus : 0; }
+
+const char *bwpp_hip_last_kernel(const BwppHip *h) {
+  return h && h->last_kernel ? h->last_kernel->c_str() : "";
+}
 
 // ---------------------------------------------------------------- memory
 

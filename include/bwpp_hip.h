@@ -175,7 +175,10 @@ typedef struct BwppHip BwppHip;
 BwppHipStatus bwpp_hip_create(BwppHip **out, int device,
                               const char *code_object_dir);
 void bwpp_hip_destroy(BwppHip *h);
-/* Stream for subsequent launches (a hipStream_t); NULL = the null stream. */
+/* Stream for subsequent launches (a hipStream_t); NULL = the null stream.
+ * The handle's workspace (split-K partials, attention-backward row sums,
+ * column partials) is ordered on the handle's stream: when the stream
+ * changes, the new stream first waits for the work queued on the old one. */
 BwppHipStatus bwpp_hip_set_stream(BwppHip *h, void *hip_stream);
 void *bwpp_hip_get_stream(const BwppHip *h);
 /* Waits for all work on the handle's stream. */
@@ -185,6 +188,9 @@ const char *bwpp_hip_last_error(const BwppHip *h);
 const char *bwpp_hip_status_string(BwppHipStatus s);
 /* Number of compute units of the handle's device (for launch heuristics). */
 int bwpp_hip_device_cus(const BwppHip *h);
+/* Symbol of the last kernel this handle launched ("" if none): which
+ * variant a dispatch chose.  No reference counterpart (diagnostics). */
+const char *bwpp_hip_last_kernel(const BwppHip *h);
 
 /* ---- device memory ---- */
 
@@ -249,7 +255,11 @@ BwppHipStatus bwpp_hip_dispatch_attention(BwppHip *h, const void *q,
  * log-sum-exp of query m's scaled, masked scores (-inf when it sees no key),
  * for the backward below.  No reference counterpart (the reference
  * differentiates attention through its decomposed graph ops,
- * graph_ir.c:1722-1733, 1529-1583); runs the generic kernel. */
+ * graph_ir.c:1722-1733, 1529-1583).  The same kernels as the plain forward
+ * run: bf16 with K = D = 128 and 16-byte rows (pointers, leading dims and
+ * slice strides in multiples of 8 elements) takes the bf16 flash kernel;
+ * fp32 with K = D = 64 or 128 and 16-byte rows takes the fp32 matrix-core
+ * kernel; anything else the generic kernel. */
 BwppHipStatus bwpp_hip_dispatch_attention_lse(BwppHip *h, const void *q,
                                               const void *k, const void *v,
                                               void *o, float *lse,

@@ -24,25 +24,49 @@ static int oracle_matmul_core(const float *a, const float *b, float *c,
                               int apply_silu, int apply_bias) {
   if (!a || !b || !c) return -1;
   if (N == 0 || M == 0) return 0;
-  float *acc = (float *)malloc(sizeof(float) * (size_t)N);
+  /* Rows are processed in groups of up to 4 sharing each B row (or, with
+   * trans_b, each column run); every output still starts from 0.0f and adds
+   * av * b for k = 0, 1, ..., K-1 in that order. */
+  enum { RB = 4 };
+  float *acc = (float *)malloc(sizeof(float) * (size_t)N * RB);
   if (!acc) return -1;
-  for (uint32_t row = 0; row < M; ++row) {
-    for (uint32_t col = 0; col < N; ++col) acc[col] = 0.0f;
-    for (uint32_t k = 0; k < K; ++k) {
-      const float av = trans_a ? a[(size_t)k * lda + row] : a[(size_t)row * lda + k];
-      if (!trans_b) {
+  for (uint32_t row0 = 0; row0 < M; row0 += RB) {
+    const uint32_t nr = M - row0 < RB ? M - row0 : RB;
+    for (size_t i = 0; i < (size_t)N * nr; ++i) acc[i] = 0.0f;
+    if (!trans_b) {
+      for (uint32_t k = 0; k < K; ++k) {
         const float *brow = b + (size_t)k * ldb;
-        for (uint32_t col = 0; col < N; ++col) acc[col] += av * brow[col];
-      } else {
-        for (uint32_t col = 0; col < N; ++col) acc[col] += av * b[(size_t)col * ldb + k];
+        for (uint32_t r = 0; r < nr; ++r) {
+          const uint32_t row = row0 + r;
+          const float av = trans_a ? a[(size_t)k * lda + row] : a[(size_t)row * lda + k];
+          float *ar = acc + (size_t)r * N;
+          for (uint32_t col = 0; col < N; ++col) ar[col] += av * brow[col];
+        }
+      }
+    } else {
+      /* B stored [N x K]: a dot product per output over contiguous k. */
+      for (uint32_t r = 0; r < nr; ++r) {
+        const uint32_t row = row0 + r;
+        for (uint32_t col = 0; col < N; ++col) {
+          const float *bcol = b + (size_t)col * ldb;
+          float s = 0.0f;
+          for (uint32_t k = 0; k < K; ++k) {
+            const float av = trans_a ? a[(size_t)k * lda + row] : a[(size_t)row * lda + k];
+            s += av * bcol[k];
+          }
+          acc[(size_t)r * N + col] = s;
+        }
       }
     }
-    float *crow = c + (size_t)row * ldc;
-    for (uint32_t col = 0; col < N; ++col) {
-      float v = acc[col];
-      if (apply_bias && bias) v += bias[col]; /* bwpp_cpu_ref.c:26-28 */
-      if (apply_silu) v = oracle_silu(v);     /* bwpp_cpu_ref.c:29-31 */
-      crow[col] = v;
+    for (uint32_t r = 0; r < nr; ++r) {
+      float *crow = c + (size_t)(row0 + r) * ldc;
+      const float *ar = acc + (size_t)r * N;
+      for (uint32_t col = 0; col < N; ++col) {
+        float v = ar[col];
+        if (apply_bias && bias) v += bias[col]; /* bwpp_cpu_ref.c:26-28 */
+        if (apply_silu) v = oracle_silu(v);     /* bwpp_cpu_ref.c:29-31 */
+        crow[col] = v;
+      }
     }
   }
   free(acc);

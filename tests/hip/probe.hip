@@ -3,7 +3,7 @@
 // registers from a[l*NA ..], b[l*NB ..] and writes its accumulator registers
 // to c[l*NC ..].  tests/test_gpu_mfma_layout.py checks the results against a
 // CPU model of the operand/accumulator layouts the kernels assume.
-// Not loaded by the runtime.
+// Test code: built by tests/hip/Makefile, never loaded by the runtime.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

@@ -218,15 +218,20 @@ def _backend_with(monkeypatch, w8_mask):
     return be
 
 
+W8_DKDV = "bwpp_attn_bwd_bf16_mfma_d128{}_dkdv_w8"
+
+
 @pytest.mark.parametrize("M,N", [(40, 70), (70, 40)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_bf16_grad_8wave(oracle, monkeypatch, M, N, causal):
-    """d = 128 with 256 slices: slices x ceil(N / 256) = 256 blocks give
+    """d = 128 with one slice per CU: slices x ceil(N / 256) blocks give
     every CU one, so the runtime takes the 8-wave dK/dV pass (256 keys per
-    block, V rows in LDS) -- checked against the oracle."""
+    block, V rows in LDS) -- checked against the oracle, and the launch is
+    checked to have been that kernel."""
     be = _backend_with(monkeypatch, 3)
     try:
-        _bf16_grad_case(be, oracle, 1, 256, M, N, 128, causal, 128)
+        _bf16_grad_case(be, oracle, 1, be.cus, M, N, 128, causal, 128)
+        assert be.last_kernel == W8_DKDV.format("_causal" if causal else "")
     finally:
         be.close()
 
@@ -238,7 +243,11 @@ def test_bf16_grad_8wave_matches_4wave(monkeypatch, causal):
     both add the same 32-query blocks in the same order, so dQ, dK, dV are
     bit-identical."""
     torch = _torch()
-    B, H, M, N, D = 1, 64, 600, 1000, 128
+    be0 = _backend_with(monkeypatch, 3)
+    cus = be0.cus
+    be0.close()
+    # ceil(1000 / 256) = 4 key blocks per slice: cus / 4 slices fill the chip.
+    B, H, M, N, D = 1, max(1, cus // 4), 600, 1000, 128
     gen = torch.Generator(device="cuda").manual_seed(5)
     q = torch.randn(B, H, M, D, device="cuda", generator=gen).bfloat16()
     k = torch.randn(B, H, N, D, device="cuda", generator=gen).bfloat16()
@@ -256,12 +265,44 @@ def test_bf16_grad_8wave_matches_4wave(monkeypatch, causal):
             g = [torch.full_like(t, 7.0) for t in (q, k, v)]
             be.dispatch_attention_grad(q, k, v, o, do, lse, *g, prm)
             torch.cuda.synchronize()
+            w8 = W8_DKDV.format("_causal" if causal else "")
+            assert (be.last_kernel == w8) == (mask == 3), be.last_kernel
             outs.append(g)
         finally:
             be.close()
     for a, b in zip(*outs):
         assert torch.isfinite(a.float()).all()
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_grad_c4_shape(be, oracle, causal):
+    """Config 4's shape, the one the bench times: B8 H32 S2048 d128 bf16,
+    scale 1/sqrt(128).  The forward saves lse through the flash kernel and
+    the backward takes the 8-wave dK/dV pass (both checked by kernel name);
+    O and dQ, dK, dV of two (b, h) slices against the oracle on the exact
+    bf16 inputs.  Bar 2e-2."""
+    torch = _torch()
+    B, H, S, D = 8, 32, 2048, 128
+    cs = "_causal" if causal else ""
+    bits = [synth.to_bf16_bits(synth.normal((B, H, S, D), 21, i)) for i in range(4)]
+    q, k, v, do = (torch.from_numpy(b.view(np.int16)).cuda().view(torch.bfloat16) for b in bits)
+    scale = D ** -0.5
+    prm = bwpp.AttentionParams(M=S, N=S, K=D, D=D, ldq=D, ldk=D, ldv=D, ldo=D, batch=B, heads=H,
+                               scale=scale, causal=int(causal), dtype=int(bwpp.DType.BF16))
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, S), device="cuda")
+    be.dispatch_attention_lse(q, k, v, o, lse, prm)
+    assert be.last_kernel == "bwpp_attn_bf16_d128" + cs
+    dq, dk, dv = (torch.full_like(t, 7.0) for t in (q, k, v))
+    be.dispatch_attention_grad(q, k, v, o, do, lse, dq, dk, dv, prm)
+    assert be.last_kernel == W8_DKDV.format(cs)
+    torch.cuda.synchronize()
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        qs, ks, vs, dos = (synth.bf16_bits_to_f32(np.ascontiguousarray(x[b:b + 1, h:h + 1])) for x in bits)
+        assert rel_max_err(_bf16_host(o[b:b + 1, h:h + 1]), oracle.attention_bh(qs, ks, vs, scale, causal)) <= 2e-2
+        for got, want in zip((dq, dk, dv), oracle.attention_grad(qs, ks, vs, dos, scale, causal)):
+            assert rel_max_err(_bf16_host(got[b:b + 1, h:h + 1]), want) <= 2e-2, (b, h)
 
 
 def _bf16_grad_case(be, oracle, B, H, M, N, D, causal, ld):

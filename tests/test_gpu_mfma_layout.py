@@ -1,6 +1,6 @@
 """Pins the gfx950 MFMA operand and accumulator lane layouts that the GEMM
-and attention kernels are written against (bluewolf-plus-plus_amd/csrc/
-kernels/probe.hip).  Small integers make every product exact, so any
+and attention kernels are written against (probes in tests/hip/probe.hip,
+built by tests/hip/Makefile).  Small integers make every product exact, so any
 mismatch between the hardware and the assumed layout shows as a wrong
 entry."""
 import ctypes
@@ -13,8 +13,7 @@ from hipmod import Module
 
 pytestmark = pytest.mark.gpu
 
-PROBE = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
-                     "bluewolf-plus-plus_amd", "lib", "bwpp_probe.hsaco")
+PROBE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "hip", "bwpp_probe.hsaco")
 
 
 class ProbeArgs(ctypes.Structure):

@@ -54,8 +54,12 @@ def _reference(t, B, T, D, H, F):
     return out.detach().numpy(), float(loss.detach()), grads
 
 
-@pytest.mark.parametrize("B,T,D,H,F", [(2, 64, 128, 2, 256), (1, 100, 192, 3, 384)])
+@pytest.mark.parametrize("B,T,D,H,F", [(2, 64, 128, 2, 256), (1, 100, 192, 3, 384),
+                                       (8, 512, 1024, 16, 4096)])
 def test_transformer_block_train_plan(be, B, T, D, H, F):
+    """The last case is config 5 at full size (the step the bench times):
+    there split-K runs on the K = 4096 weight-gradient GEMMs and attention
+    over 128 (batch, head) slices."""
     import torch
     t = _inputs(B, T, D, F, seed=B * 1000 + T)
     p = plan.Plan(be, plan.load_text("transformer_block_train", B=B, T=T, D=D, H=H, F=F))
