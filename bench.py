@@ -159,30 +159,36 @@ def time_c2(bench, steps, warmup):
 WARM_MS = 40.0  # sustained work before any extras timing starts
 
 
-def _launch_times_ms(torch, fn, iters):
-    """Durations (ms) of `iters` back-to-back launches of fn: one event on
-    the launch stream before the first launch and one after each, so
-    launch i is the interval between events i and i + 1 and the stream is
-    never drained in between."""
+def _launch_times_ms(torch, fn, iters, group=5):
+    """Per-launch durations (ms) of `iters` back-to-back launches of fn, as
+    the mean over consecutive groups of `group` launches: an event on the
+    launch stream before the first launch and after every group, so the
+    stream is never drained and the events add no gap inside a group (an
+    event between every two launches adds ~2 us to a 45 us kernel)."""
     stream = torch.cuda.current_stream()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+    ng = max(1, iters // group)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(ng + 1)]
     ev[0].record(stream)
-    for i in range(iters):
-        fn(i)
-        ev[i + 1].record(stream)
+    i = 0
+    for g in range(ng):
+        for _ in range(group):
+            fn(i)
+            i += 1
+        ev[g + 1].record(stream)
     torch.cuda.synchronize()
-    return [ev[i].elapsed_time(ev[i + 1]) for i in range(iters)]
+    return [ev[g].elapsed_time(ev[g + 1]) / group for g in range(ng)]
 
 
 def time_c2_ops(bench, reps):
-    """Median and mean launch duration per operator (ms) over `reps`
-    back-to-back launches on the rotating buffer sets."""
+    """Median (over groups of 10 back-to-back launches) and mean launch
+    duration per operator (ms), over `reps` launches on the rotating
+    buffer sets."""
     torch = bench.torch
     out = {}
     for op in C2_BYTES:
         for i in range(bench.nbuf):
             bench.launch(op, i)
-        t = _launch_times_ms(torch, lambda i: bench.launch(op, i % bench.nbuf), reps)
+        t = _launch_times_ms(torch, lambda i: bench.launch(op, i % bench.nbuf), reps, group=10)
         out[op] = (float(np.median(t)), float(np.mean(t)))
     return out
 
@@ -241,7 +247,8 @@ def pmc_summary(dirs):
     runs) found under them.  Counters are summed over a dispatch's rows and
     then averaged over the kernel's dispatches.  Derived columns, with
     XCDS = 8, SIMDS = 4 per CU and CUS from the agent info:
-      clock GHz   = GRBM_GUI_ACTIVE / XCDS / kernel duration
+      clock GHz   = GRBM_GUI_ACTIVE / XCDS / duration of the same dispatch
+                    in the counter run (its Start/End timestamps)
       MFMA busy   = SQ_VALU_MFMA_BUSY_CYCLES / (CUS * SIMDS * GRBM_GUI_ACTIVE / XCDS)
       VALU / MFMA = SQ_INSTS_VALU / SQ_INSTS_MFMA
     (SQ_VALU_MFMA_BUSY_CYCLES counts SIMD cycles with the matrix pipe busy,
@@ -249,7 +256,7 @@ def pmc_summary(dirs):
     the XCDs.)"""
     import csv
     import glob
-    counters, dur, cus = {}, {}, 256
+    counters, dur, cus, pmc_ns = {}, {}, 256, {}
     for d in dirs:
         for f in glob.glob(os.path.join(d, "**", "*agent_info.csv"), recursive=True):
             with open(f, newline="") as fh:
@@ -270,6 +277,14 @@ def pmc_summary(dirs):
             for (k, _), cv in per.items():
                 for c, v in cv.items():
                     counters.setdefault(k, {}).setdefault(c, []).append(v)
+            with open(f, newline="") as fh:
+                seen = set()
+                for row in csv.DictReader(fh):
+                    key = (row["Kernel_Name"], row["Dispatch_Id"])
+                    if key[0].startswith("bwpp_") and key not in seen:
+                        seen.add(key)
+                        pmc_ns.setdefault(key[0], []).append(
+                            float(row["End_Timestamp"]) - float(row["Start_Timestamp"]))
         for f in glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True):
             with open(f, newline="") as fh:
                 for row in csv.DictReader(fh):
@@ -277,18 +292,19 @@ def pmc_summary(dirs):
                         dur[row["Name"]] = float(row["AverageNs"])
     cols = ["GRBM_GUI_ACTIVE", "SQ_BUSY_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU",
             "SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT", "SQ_WAVES"]
-    lines = ["| kernel | avg ns | clock GHz | MFMA busy | VALU/MFMA | " + " | ".join(cols) + " |",
-             "|---" * (len(cols) + 5) + "|"]
+    lines = ["| kernel | trace avg ns | pmc-run ns | clock GHz | MFMA busy | VALU/MFMA | " + " | ".join(cols) + " |",
+             "|---" * (len(cols) + 6) + "|"]
     for k in sorted(set(counters) | set(dur)):
         c = {n: float(np.mean(v)) for n, v in counters.get(k, {}).items()}
         ns = dur.get(k)
+        pns = float(np.mean(pmc_ns[k])) if k in pmc_ns else None
         g = c.get("GRBM_GUI_ACTIVE")
-        clock = f"{g / 8 / ns:.2f}" if g and ns else ""
+        clock = f"{g / 8 / pns:.2f}" if g and pns else ""
         busy = f"{c['SQ_VALU_MFMA_BUSY_CYCLES'] / (cus * 4 * g / 8):.3f}" if g and "SQ_VALU_MFMA_BUSY_CYCLES" in c else ""
         ratio = (f"{c['SQ_INSTS_VALU'] / c['SQ_INSTS_MFMA']:.2f}"
                  if c.get("SQ_INSTS_MFMA") and "SQ_INSTS_VALU" in c else "")
         vals = [f"{c[n]:.4g}" if n in c else "" for n in cols]
-        lines.append(f"| {k} | {ns:.0f} | " if ns else f"| {k} | | ")
+        lines.append((f"| {k} | {ns:.0f} | " if ns else f"| {k} | | ") + (f"{pns:.0f} | " if pns else " | "))
         lines[-1] += f"{clock} | {busy} | {ratio} | " + " | ".join(vals) + " |"
     return "\n".join(lines)
 
@@ -399,11 +415,11 @@ def _events_us(torch, fn, iters, warm_ms=None, stats=None):
     ~1180 TFLOP/s), and the figure wanted is the steady state.  `stats`, if
     given, also receives the mean."""
     warm_ms = _WARM_MS if warm_ms is None else warm_ms
-    t = _launch_times_ms(torch, lambda i: fn(), 3)
+    t = _launch_times_ms(torch, lambda i: fn(), 3, group=3)
     est_us = max(float(np.mean(t)) * 1e3, 1.0)
     for _ in range(min(4000, int(warm_ms * 1e3 / est_us) + 1) if warm_ms > 0 else 0):
         fn()
-    t = _launch_times_ms(torch, lambda i: fn(), iters)
+    t = _launch_times_ms(torch, lambda i: fn(), iters, group=max(1, min(5, iters // 3)))
     if stats is not None:
         stats["us_mean"] = round(float(np.mean(t)) * 1e3, 2)
     return float(np.median(t)) * 1e3
@@ -609,7 +625,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true", help="skip the C1/C3/C4 contraction configs")
-    ap.add_argument("--op-reps", type=int, default=30, help="launches per operator for per-kernel timing")
+    ap.add_argument("--op-reps", type=int, default=70, help="launches per operator for per-kernel timing")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="N",
                     help="also run N plain copies of known size (for scaling --pmc byte counters)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),

@@ -5,14 +5,15 @@ objects (lib/); this package only binds them.  There is no CPU fallback:
 if the library or a code object is missing, HipBackend() raises.
 """
 from . import _lib, plan, synth
-from ._lib import (AttentionParams, DType, ElementwiseParams, Epilogue,
+from ._lib import (AttentionParams, CoreDType, DType, ElementwiseParams, Epilogue,
                    LibraryMissing, MatmulParams, ReduceParams, RmsnormParams,
-                   SoftmaxParams, Status)
-from .backend import BwppError, HipBackend
+                   SoftmaxParams, Status, Tensor)
+from .backend import BwppError, HipBackend, tensor_of
 
 __all__ = ["HipBackend", "BwppError", "LibraryMissing", "Status", "DType",
            "Epilogue", "MatmulParams", "SoftmaxParams", "RmsnormParams",
-           "AttentionParams", "ReduceParams", "ElementwiseParams", "synth", "plan",
+           "AttentionParams", "ReduceParams", "ElementwiseParams", "CoreDType", "Tensor",
+           "tensor_of", "synth", "plan",
            "load_library"]
 
 

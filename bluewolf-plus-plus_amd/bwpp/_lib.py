@@ -86,6 +86,19 @@ class Arena(Structure):
                 ("offset", c_size_t), ("device", c_int)]
 
 
+class CoreDType(enum.IntEnum):
+    """runtime/core/tensor.h:7-11 numbering, carried by Tensor.dtype."""
+    F16 = 0
+    BF16 = 1
+    F32 = 2
+
+
+class Tensor(Structure):
+    """BwppHipTensor: runtime/core/tensor.h:18-25 over device memory."""
+    _fields_ = [("dtype", ctypes.c_int32), ("layout", ctypes.c_int32), ("rank", c_uint32),
+                ("shape", c_uint64 * 4), ("stride", c_uint64 * 4), ("buffer", c_void_p)]
+
+
 _P = c_void_p
 # name -> (restype, argtypes); every function include/bwpp_hip.h declares.
 SIGNATURES = {
@@ -102,6 +115,27 @@ SIGNATURES = {
     "bwpp_hip_arena_reset": (None, [POINTER(Arena)]),
     "bwpp_hip_arena_alloc": (_P, [POINTER(Arena), c_size_t, c_size_t]),
     "bwpp_hip_arena_destroy": (None, [POINTER(Arena)]),
+    "bwpp_hip_dtype_from_core": (ctypes.c_int32, [ctypes.c_int32]),
+    "bwpp_hip_dtype_from_graph": (ctypes.c_int32, [ctypes.c_int32]),
+    "bwpp_hip_dtype_to_core": (ctypes.c_int32, [ctypes.c_int32]),
+    "bwpp_hip_dtype_to_graph": (ctypes.c_int32, [ctypes.c_int32]),
+    "bwpp_hip_core_dtype_size": (c_size_t, [ctypes.c_int32]),
+    "bwpp_hip_tensor_init": (c_int, [POINTER(Tensor), ctypes.c_int32, ctypes.c_int32, c_uint32,
+                                     POINTER(c_uint64), _P]),
+    "bwpp_hip_tensor_bytes": (c_size_t, [POINTER(Tensor)]),
+    "bwpp_hip_tensor_alloc": (c_int, [POINTER(Arena), POINTER(Tensor), ctypes.c_int32, ctypes.c_int32,
+                                      c_uint32, POINTER(c_uint64)]),
+    "bwpp_hip_tensor_matrix": (c_int, [POINTER(Tensor), POINTER(c_uint32), POINTER(c_uint32),
+                                       POINTER(c_uint32)]),
+    "bwpp_hip_tensor_matmul": (c_int, [_P, POINTER(Tensor), POINTER(Tensor), POINTER(Tensor),
+                                       POINTER(Tensor), c_uint32]),
+    "bwpp_hip_tensor_softmax": (c_int, [_P, POINTER(Tensor), POINTER(Tensor)]),
+    "bwpp_hip_tensor_rmsnorm": (c_int, [_P, POINTER(Tensor), POINTER(Tensor), POINTER(Tensor),
+                                        POINTER(Tensor), c_float]),
+    "bwpp_hip_tensor_layernorm": (c_int, [_P, POINTER(Tensor), POINTER(Tensor), POINTER(Tensor),
+                                          POINTER(Tensor), c_float]),
+    "bwpp_hip_tensor_attention": (c_int, [_P, POINTER(Tensor), POINTER(Tensor), POINTER(Tensor),
+                                          POINTER(Tensor), c_float, c_uint32]),
     "bwpp_hip_copy_to_device": (c_int, [_P, _P, _P, c_size_t]),
     "bwpp_hip_copy_to_host": (c_int, [_P, _P, _P, c_size_t]),
     "bwpp_hip_plan_create": (c_int, [_P, c_char_p, POINTER(c_void_p)]),
@@ -172,5 +206,6 @@ def load():
 
 __all__ = ["Status", "DType", "Epilogue", "MatmulParams", "SoftmaxParams",
            "RmsnormParams", "AttentionParams", "ReduceParams", "ElementwiseParams", "Arena",
+           "CoreDType", "Tensor",
            "SIGNATURES", "load", "LIB_PATH", "LIB_DIR", "HEADER_PATH",
            "LibraryMissing", "byref", "c_void_p", "c_uint16"]

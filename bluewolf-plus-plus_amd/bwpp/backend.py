@@ -35,6 +35,23 @@ def _ptr(buf) -> int | None:
     raise TypeError(f"cannot pass {type(buf)!r} as a device buffer")
 
 
+def tensor_of(t, layout: int = 0) -> "_lib.Tensor":
+    """BwppHipTensor describing a torch CUDA tensor (f32 or bf16, its own
+    shape and element strides).  layout 1 (column-major) marks a rank-2
+    tensor whose storage is the transpose (e.g. `x.t()` of a row-major x)."""
+    import torch
+    dt = {torch.float32: _lib.CoreDType.F32, torch.bfloat16: _lib.CoreDType.BF16}[t.dtype]
+    r = _lib.Tensor()
+    r.dtype = int(dt)
+    r.layout = layout
+    r.rank = t.dim()
+    for i in range(t.dim()):
+        r.shape[i] = t.shape[i]
+        r.stride[i] = t.stride(i)
+    r.buffer = t.data_ptr()
+    return r
+
+
 class HipBackend:
     """One libbwpp_hip handle (device, loaded code objects, stream)."""
 
@@ -148,6 +165,26 @@ class HipBackend:
 
     def dispatch_reduce_sum(self, x, out, params: ReduceParams):
         self._check(self.lib.bwpp_hip_dispatch_reduce_sum(self._h, _ptr(x), _ptr(out), params))
+
+    # ------------------------------------------------------ tensor forms
+    def tensor_matmul(self, a, b, bias, c, epilogue: int = 0):
+        ref = lambda t: ctypes.byref(t) if t is not None else None
+        self._check(self.lib.bwpp_hip_tensor_matmul(self._h, ref(a), ref(b), ref(bias), ref(c), epilogue))
+
+    def tensor_softmax(self, x, y):
+        self._check(self.lib.bwpp_hip_tensor_softmax(self._h, ctypes.byref(x), ctypes.byref(y)))
+
+    def tensor_rmsnorm(self, x, gamma, beta, y, eps: float):
+        ref = lambda t: ctypes.byref(t) if t is not None else None
+        self._check(self.lib.bwpp_hip_tensor_rmsnorm(self._h, ref(x), ref(gamma), ref(beta), ref(y), eps))
+
+    def tensor_layernorm(self, x, gamma, beta, y, eps: float):
+        ref = lambda t: ctypes.byref(t) if t is not None else None
+        self._check(self.lib.bwpp_hip_tensor_layernorm(self._h, ref(x), ref(gamma), ref(beta), ref(y), eps))
+
+    def tensor_attention(self, q, k, v, o, scale: float, causal: int):
+        self._check(self.lib.bwpp_hip_tensor_attention(self._h, ctypes.byref(q), ctypes.byref(k),
+                                                       ctypes.byref(v), ctypes.byref(o), scale, causal))
 
     def dispatch_elementwise(self, a, b, out, params: ElementwiseParams):
         self._check(self.lib.bwpp_hip_dispatch_elementwise(self._h, _ptr(a), _ptr(b), _ptr(out), params))

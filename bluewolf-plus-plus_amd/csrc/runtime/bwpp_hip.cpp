@@ -122,6 +122,23 @@ BwppHipStatus fail(BwppHip *h, BwppHipStatus s, const char *fmt, ...) {
   return s;
 }
 
+}  // namespace
+
+BwppHipStatus bwpp_hip_set_error(BwppHip *h, BwppHipStatus s, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (h)
+    h->err = buf;
+  else
+    g_create_error = buf;
+  return s;
+}
+
+namespace {
+
 BwppHipStatus resolve(BwppHip *h, const std::string &name, hipFunction_t *out) {
   for (hipModule_t m : h->modules) {
     hipFunction_t f = nullptr;

@@ -10,3 +10,9 @@
 BwppHipStatus bwpp_hip_attention_grad_planned(BwppHip *h, const void *q, const void *k, const void *v,
                                               const void *o, const void *dout, const float *lse, void *dq,
                                               void *dk, void *dv, const BwppAttentionParams &p);
+
+// Records `fmt` as the handle's last-error text (the thread's create error
+// when h is NULL) and returns s.
+BwppHipStatus bwpp_hip_set_error(BwppHip *h, BwppHipStatus s, const char *fmt, ...)
+    __attribute__((format(printf, 3, 4)));
+

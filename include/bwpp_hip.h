@@ -210,6 +210,92 @@ void bwpp_hip_arena_reset(BwppHipArena *arena);
 void *bwpp_hip_arena_alloc(BwppHipArena *arena, size_t size, size_t align);
 void bwpp_hip_arena_destroy(BwppHipArena *arena);
 
+/* ---- tensor metadata (device twin of runtime/core/tensor.h) ---- */
+
+/* The three dtype numberings met on the path:
+ *   runtime/core BwppDType (runtime/core/tensor.h:7-11): F16 0, BF16 1, F32 2
+ *   compiler BwppDType (compiler/include/graph_ir.h:18-23):
+ *                                            UNKNOWN 0, F16 1, BF16 2, F32 3
+ *   BwppHipDType (above):                    F32 0, BF16 1
+ * BwppHipTensor carries runtime/core's numbering, as BwppTensor does; the
+ * mappers below convert between them and return -1 for a dtype with no
+ * counterpart (compiler UNKNOWN; F16, for which this build has no
+ * kernels). */
+typedef enum {
+  BWPP_HIP_CORE_F16 = 0,
+  BWPP_HIP_CORE_BF16 = 1,
+  BWPP_HIP_CORE_F32 = 2
+} BwppHipCoreDType;
+typedef enum {
+  BWPP_HIP_LAYOUT_ROW_MAJOR = 0, /* runtime/core/tensor.h:13-16 */
+  BWPP_HIP_LAYOUT_COL_MAJOR = 1
+} BwppHipLayout;
+
+/* runtime/core/tensor.h:18-25 with a device buffer: same fields, order and
+ * widths (the enums are int-sized), so a BwppTensor that describes device
+ * memory has this layout.  stride[i] is in elements; a contiguous
+ * row-major tensor has stride[rank-1] = 1.  COL_MAJOR marks a rank-2
+ * tensor stored transposed (stride[0] = 1, stride[1] = leading dim). */
+typedef struct {
+  int32_t dtype;  /* BwppHipCoreDType */
+  int32_t layout; /* BwppHipLayout */
+  uint32_t rank;  /* 1..4 */
+  uint64_t shape[4];
+  uint64_t stride[4];
+  void *buffer;   /* device address */
+} BwppHipTensor;
+
+int32_t bwpp_hip_dtype_from_core(int32_t core_dtype);   /* -> BwppHipDType */
+int32_t bwpp_hip_dtype_from_graph(int32_t graph_dtype); /* -> BwppHipDType */
+int32_t bwpp_hip_dtype_to_core(int32_t hip_dtype);      /* -> runtime/core */
+int32_t bwpp_hip_dtype_to_graph(int32_t hip_dtype);     /* -> compiler */
+/* Bytes per element of a runtime/core dtype (0 if unknown). */
+size_t bwpp_hip_core_dtype_size(int32_t core_dtype);
+
+/* Describes `buffer` as a contiguous tensor of `rank` dims in the given
+ * layout (COL_MAJOR needs rank 2).  buffer may be NULL (shape only). */
+BwppHipStatus bwpp_hip_tensor_init(BwppHipTensor *t, int32_t core_dtype,
+                                   int32_t layout, uint32_t rank,
+                                   const uint64_t *shape, void *buffer);
+/* Bytes spanned by the tensor's elements (its strides included). */
+size_t bwpp_hip_tensor_bytes(const BwppHipTensor *t);
+/* bwpp_hip_tensor_init over memory taken from a device arena (256-byte
+ * aligned); OUT_OF_MEMORY when the arena is exhausted. */
+BwppHipStatus bwpp_hip_tensor_alloc(BwppHipArena *arena, BwppHipTensor *t,
+                                    int32_t core_dtype, int32_t layout,
+                                    uint32_t rank, const uint64_t *shape);
+/* The [rows x cols] matrix with row stride ld (elements) that a row-major
+ * tensor is to the row operators: cols = last dim, rows = product of the
+ * others, which must be stacked at one stride.  UNSUPPORTED otherwise. */
+BwppHipStatus bwpp_hip_tensor_matrix(const BwppHipTensor *t, uint32_t *rows,
+                                     uint32_t *cols, uint32_t *ld);
+
+/* Tensor-level forms of the operators below: parameters come from the
+ * metadata (dtype, shape, strides, layout).  C = A·B (+bias) (→SiLU) with A
+ * [M,K], B [K,N], C [M,N] rank 2 (a COL_MAJOR A or B runs transposed);
+ * softmax / rmsnorm / layernorm along the last dim of any rank; attention
+ * over rank-4 [batch, heads, seq, dim] q, k, v, o (slice strides from the
+ * tensors).  dtypes must agree (f32, or bf16 for matmul / attention). */
+BwppHipStatus bwpp_hip_tensor_matmul(BwppHip *h, const BwppHipTensor *a,
+                                     const BwppHipTensor *b,
+                                     const BwppHipTensor *bias,
+                                     BwppHipTensor *c, uint32_t epilogue);
+BwppHipStatus bwpp_hip_tensor_softmax(BwppHip *h, const BwppHipTensor *x,
+                                      BwppHipTensor *y);
+BwppHipStatus bwpp_hip_tensor_rmsnorm(BwppHip *h, const BwppHipTensor *x,
+                                      const BwppHipTensor *gamma,
+                                      const BwppHipTensor *beta,
+                                      BwppHipTensor *y, float eps);
+BwppHipStatus bwpp_hip_tensor_layernorm(BwppHip *h, const BwppHipTensor *x,
+                                        const BwppHipTensor *gamma,
+                                        const BwppHipTensor *beta,
+                                        BwppHipTensor *y, float eps);
+BwppHipStatus bwpp_hip_tensor_attention(BwppHip *h, const BwppHipTensor *q,
+                                        const BwppHipTensor *k,
+                                        const BwppHipTensor *v,
+                                        BwppHipTensor *o, float scale,
+                                        uint32_t causal);
+
 /* Stream-ordered copies, complete on return. */
 BwppHipStatus bwpp_hip_copy_to_device(BwppHip *h, void *dst, const void *src,
                                       size_t bytes);
