@@ -154,6 +154,8 @@ SIGNATURES = {
     "bwpp_hip_dispatch_attention": (c_int, [_P, _P, _P, _P, _P, AttentionParams]),
     "bwpp_hip_dispatch_attention_lse": (c_int, [_P, _P, _P, _P, _P, _P, AttentionParams]),
     "bwpp_hip_dispatch_attention_grad": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, AttentionParams]),
+    "bwpp_hip_dispatch_attention_grad_noalloc": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                         AttentionParams]),
     "bwpp_hip_dispatch_reduce_max": (c_int, [_P, _P, _P, _P, ReduceParams]),
     "bwpp_hip_dispatch_reduce_max_mask": (c_int, [_P, _P, _P, ReduceParams]),
     "bwpp_hip_dispatch_reduce_max_grad": (c_int, [_P, _P, _P, _P, ReduceParams]),

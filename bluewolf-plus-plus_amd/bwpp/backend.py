@@ -135,6 +135,11 @@ class HipBackend:
             self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(dout), _ptr(lse),
             _ptr(dq), _ptr(dk), _ptr(dv), params))
 
+    def dispatch_attention_grad_noalloc(self, q, k, v, o, dout, lse, dq, dk, dv, params: AttentionParams):
+        self._check(self.lib.bwpp_hip_dispatch_attention_grad_noalloc(
+            self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(dout), _ptr(lse),
+            _ptr(dq), _ptr(dk), _ptr(dv), params))
+
     def dispatch_reduce_max(self, x, maxv, argmax, params: ReduceParams):
         self._check(self.lib.bwpp_hip_dispatch_reduce_max(
             self._h, _ptr(x), _ptr(maxv), _ptr(argmax), params))

@@ -102,6 +102,11 @@ struct BwppHip {
   // reuse across calls is safe.
   void *ws = nullptr;
   size_t ws_bytes = 0;
+  // Device address of this device's scratch array (bwpp_scratch.hip), for
+  // the allocation-free entry point; NULL with scratch_why set if the
+  // lookup failed.
+  void *scratch = nullptr;
+  std::string scratch_why;
   uint32_t gemm_group_m = 8;  // BWPP_GEMM_GROUP_M
   uint32_t gemm_waves = 8;    // BWPP_GEMM_WAVES: 4 or 8 waves for full bf16 tiles
   uint32_t gemm_splitk = 1;   // BWPP_GEMM_SPLITK=0 turns fp32 split-K off
@@ -356,6 +361,10 @@ BwppHipStatus bwpp_hip_create(BwppHip **out, int device, const char *code_object
 
   BwppHip *h = new BwppHip();
   h->device = device;
+  {
+    const char *why = "";
+    if (bwpp_hip_scratch_setup(device, &h->scratch, &why) != BWPP_HIP_OK) h->scratch_why = why;
+  }
   (void)hipDeviceGetAttribute(&h->cus, hipDeviceAttributeMultiprocessorCount, device);
   if (const char *cfg = getenv("BWPP_ROW_CFG")) h->row_cfg_override = atoi(cfg);
   if (const char *gc = getenv("BWPP_ROW_GRID")) h->row_grid_cap = (uint32_t)strtoul(gc, nullptr, 10);
@@ -931,13 +940,25 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_attention_lse(BwppHip *h, const void 
 namespace {
 BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const void *v, const void *o,
                              const void *dout, const float *lse, void *dq, void *dk, void *dv,
-                             const BwppAttentionParams &p, bool check_alias);
+                             const BwppAttentionParams &p, bool check_alias, float *dsum_buf = nullptr,
+                             size_t dsum_cap = 0);
 }  // namespace
 
 extern "C" BwppHipStatus bwpp_hip_dispatch_attention_grad(BwppHip *h, const void *q, const void *k, const void *v,
                                                           const void *o, const void *dout, const float *lse,
                                                           void *dq, void *dk, void *dv, BwppAttentionParams p) {
   return attn_grad_impl(h, q, k, v, o, dout, lse, dq, dk, dv, p, true);
+}
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_attention_grad_noalloc(BwppHip *h, const void *q, const void *k,
+                                                                  const void *v, const void *o, const void *dout,
+                                                                  const float *lse, void *dq, void *dk, void *dv,
+                                                                  BwppAttentionParams p) {
+  if (!h) return BWPP_HIP_ERR_INVALID_ARG;
+  if (!h->scratch)
+    return fail(h, BWPP_HIP_ERR_HIP, "attention_grad_noalloc: device scratch unavailable (%s)", h->scratch_why.c_str());
+  return attn_grad_impl(h, q, k, v, o, dout, lse, dq, dk, dv, p, true, static_cast<float *>(h->scratch),
+                        BWPP_HIP_NOALLOC_SCRATCH_BYTES);
 }
 
 BwppHipStatus bwpp_hip_attention_grad_planned(BwppHip *h, const void *q, const void *k, const void *v,
@@ -947,9 +968,12 @@ BwppHipStatus bwpp_hip_attention_grad_planned(BwppHip *h, const void *q, const v
 }
 
 namespace {
+// dsum_buf (the allocation-free entry point): caller-provided device memory
+// of dsum_cap bytes for the per-query row sums instead of the handle's
+// workspace; paths that need more workspace than that are refused.
 BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const void *v, const void *o,
                              const void *dout, const float *lse, void *dq, void *dk, void *dv,
-                             const BwppAttentionParams &p, bool check_alias) {
+                             const BwppAttentionParams &p, bool check_alias, float *dsum_buf, size_t dsum_cap) {
   BwppHipStatus s = enter(h);
   if (s != BWPP_HIP_OK) return s;
   if (!dout || !lse || !dq || !dk || !dv)
@@ -981,7 +1005,15 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
     if (overlaps(edq, edk) || overlaps(edq, edv) || overlaps(edk, edv))
       return fail(h, BWPP_HIP_ERR_ALIAS, "attention_grad: dq, dk and dv overlap");
   }
-  if ((s = ensure_ws(h, (size_t)slices * p.M * sizeof(float) + 4)) != BWPP_HIP_OK) return s;
+  const size_t dsum_bytes = (size_t)slices * p.M * sizeof(float) + 4;
+  if (dsum_buf) {
+    if (dsum_bytes > dsum_cap)
+      return fail(h, BWPP_HIP_ERR_UNSUPPORTED,
+                  "attention_grad_noalloc: batch*heads*M = %llu query rows need %zu bytes of scratch, above the "
+                  "%zu-byte maximum", (unsigned long long)(slices * p.M), dsum_bytes, dsum_cap);
+  } else if ((s = ensure_ws(h, dsum_bytes)) != BWPP_HIP_OK) {
+    return s;
+  }
   const int bf = p.dtype == BWPP_HIP_BF16 ? 1 : 0, causal = p.causal ? 1 : 0;
   const float scale = p.scale != 0.0f ? p.scale : 1.0f;
   g.scale_log2 = scale;
@@ -990,7 +1022,7 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   g.dq = dq;
   g.dk = dk;
   g.dv = dv;
-  g.dsum = static_cast<float *>(h->ws);
+  g.dsum = dsum_buf ? dsum_buf : static_cast<float *>(h->ws);
   // Matrix-core passes (fp32 or bf16 kernels): dQ (also writes D_m =
   // rowsum(dO * O)), then dK / dV.  wq / wk: waves (32 rows each) per block
   // of the dQ / dK-dV kernel, as each was compiled.
@@ -1029,6 +1061,10 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
     // matrix-core passes, and dQ, dK, dV are rounded back into the caller's
     // bf16 layout.
     const uint64_t D = p.D, nq = slices * p.M * D, nk = slices * p.N * D;
+    if (dsum_buf)
+      return fail(h, BWPP_HIP_ERR_UNSUPPORTED,
+                  "attention_grad_noalloc: bf16 rows that are not 16-byte aligned need fp32 copies in the "
+                  "handle's workspace; use bwpp_hip_dispatch_attention_grad");
     if ((s = ensure_ws(h, (4 * nq + 4 * nk + slices * p.M) * sizeof(float))) != BWPP_HIP_OK) return s;
     float *w = static_cast<float *>(h->ws);
     float *q32 = w, *o32 = q32 + nq, *do32 = o32 + nq, *dq32 = do32 + nq;

@@ -16,3 +16,11 @@ BwppHipStatus bwpp_hip_attention_grad_planned(BwppHip *h, const void *q, const v
 BwppHipStatus bwpp_hip_set_error(BwppHip *h, BwppHipStatus s, const char *fmt, ...)
     __attribute__((format(printf, 3, 4)));
 
+// Size of the device-resident scratch array of bwpp_scratch.hip, which the
+// allocation-free attention backward uses for its per-query row sums.
+#define BWPP_HIP_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+// Device address of `device`'s scratch array, looked up once per device
+// (hipGetSymbolAddress) with that device current.  On failure *ptr is NULL,
+// *why names the HIP error and the status is BWPP_HIP_ERR_HIP.
+BwppHipStatus bwpp_hip_scratch_setup(int device, void **ptr, const char **why);

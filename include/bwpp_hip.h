@@ -364,6 +364,23 @@ BwppHipStatus bwpp_hip_dispatch_attention_grad(BwppHip *h, const void *q,
                                                void *dk, void *dv,
                                                BwppAttentionParams params);
 
+/* bwpp_hip_dispatch_attention_grad that allocates nothing: no reference
+ * counterpart; for callers that cannot call hipMalloc (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  The
+ * per-query row sums rowsum(dout * o) live in a device-resident scratch
+ * array of the library (8 MiB per GPU, held until the process ends)
+ * instead of the handle's workspace, so batch * heads * M must stay below
+ * 2,097,151 query rows (UNSUPPORTED beyond, nothing launched).  bf16 rows
+ * that are not 16-byte aligned (which need fp32 copies in the workspace)
+ * are UNSUPPORTED too.  Every call on one GPU shares that GPU's scratch:
+ * calls that overlap on one GPU (several streams, handles or threads) race
+ * on it; calls ordered on one stream do not.  Results are bit-identical to
+ * bwpp_hip_dispatch_attention_grad's. */
+BwppHipStatus bwpp_hip_dispatch_attention_grad_noalloc(
+    BwppHip *h, const void *q, const void *k, const void *v, const void *o,
+    const void *dout, const float *lse, void *dq, void *dk, void *dv,
+    BwppAttentionParams params);
+
 /* reduce_max forward (graph op BWPP_GOP_REDUCE_MAX, graph_ir.h:48; no
  * reference kernel): maxv as the reference's fold, argmax = lowest index
  * holding it (-1 if none).  Either output may be NULL, not both. */
