@@ -571,22 +571,25 @@ def block_train_flop(B, T, D, H, F):
 
 def block_inputs(seed, B, T, D, F):
     """C5's synthetic inputs from the repo's SplitMix64 generator: x ~ N(0,1),
-    gamma ~ U[0.5,1.5], weights ~ N(0,0.02)."""
+    gamma ~ U[0.5,1.5], weights ~ N(0,0.02) (the plan's parameter names:
+    F is the DSL's MLP width H)."""
     from bwpp import synth
     w = lambda shape, st: synth.normal(shape, seed, st, 0.0, 0.02)
     return {"x": synth.normal((B * T, D), seed, 0), "g1": synth.uniform((D,), seed, 1, 0.5, 1.5),
-            "wqkv": w((D, 3 * D), 2), "wo": w((D, D), 3), "g2": synth.uniform((D,), seed, 4, 0.5, 1.5),
-            "w1": w((D, F), 5), "w2": w((F, D), 6)}
+            "g2": synth.uniform((D,), seed, 2, 0.5, 1.5), "wq": w((D, D), 3), "wk": w((D, D), 4),
+            "wv": w((D, D), 5), "wo": w((D, D), 6), "w1": w((D, F), 7), "w2": w((F, D), 8)}
 
 
 def block_train(be, torch, seed, iters, B=8, T=512, D=1024, H=16, F=4096, with_cpu=False):
-    """C5: one forward + backward step of the pre-norm transformer block
-    (examples/tiny_model.bwpp's `block`, 16 causal heads) in fp32, run by
-    the launch-plan executor from its plan file over one mem-planned device
-    arena.  The CPU leg runs the same plan text for one sample (B = 1) on
-    the oracle (oracle/plan_cpu.py), one core."""
+    """C5: one forward + backward step of examples/tiny_model.bwpp's `block`
+    (16 causal heads, loss mean(out^2)) in fp32: the plan bwppc-hip lowers
+    from the DSL and its autodiff (plans/block_train.plan), run by the
+    launch-plan executor over one mem-planned device arena.  The CPU leg
+    runs the same plan text for one sample (B = 1) on the oracle
+    (oracle/plan_cpu.py), one core."""
     from bwpp import plan
-    text = plan.load_text("transformer_block_train", B=B, T=T, D=D, H=H, F=F)
+    dims = dict(BATCH=B, T=T, D=D, H=F, HEADS=H)
+    text = plan.load_text("block_train", **dims)
     p = plan.Plan(be, text)
     p.allocate()
     for name, a in block_inputs(seed, B, T, D, F).items():
@@ -594,15 +597,15 @@ def block_train(be, torch, seed, iters, B=8, T=512, D=1024, H=16, F=4096, with_c
     st = {}
     us = _events_us(torch, p.run, iters, stats=st)
     fl = block_train_flop(B, T, D, H, F)
-    res = {"workload": f"B{B} T{T} D{D} H{H} F{F} fp32 fwd+bwd", "us_per_step": round(us, 1),
-           "us_mean": st.get("us_mean"),
+    res = {"workload": f"B{B} T{T} D{D} H{H} F{F} fp32 fwd+bwd", "plan": "plans/block_train.plan",
+           "us_per_step": round(us, 1), "us_mean": st.get("us_mean"),
            "TFLOP_s": round(fl / us / 1e6, 1), "frac_f32_peak": round(fl / us / 1e6 / F32_PEAK_TFLOPS, 4),
            "arena_bytes": p.arena_bytes, "ops_per_step": sum(1 for ln in text.splitlines() if ln.startswith("op "))}
     p.close()
     if with_cpu:
         sys.path.insert(0, ROOT)
         from oracle.plan_cpu import CpuPlan
-        cp = CpuPlan(plan.load_text("transformer_block_train", B=1, T=T, D=D, H=H, F=F))
+        cp = CpuPlan(plan.load_text("block_train", **dict(dims, BATCH=1)))
         for name, a in block_inputs(seed, 1, T, D, F).items():
             cp.bind(name, a)
         t0 = time.perf_counter()

@@ -16,6 +16,10 @@
 //   value NAME f32 [EXPR,...] KIND    KIND: input | param | temp | output | const=<float>
 //   view NAME of=BASE offset=EXPR ld=EXPR shape=[EXPR,EXPR]
 //   op KIND out=A[,B..] in=X[,Y..] [key=value ...]
+// Op kinds: matmul (ta, tb, epi), softmax, rmsnorm, layernorm,
+// add / sub / mul / div / copy / silu (bcast), reduce_sum, reduce_max,
+// reduce_max_mask (axis), silu_grad, softmax_grad, rmsnorm_grad,
+// attention, attention_grad (batch, heads, causal, scale, layout).
 // Tensors are row-major; row operators see [rows, cols] with cols the last
 // dim and rows the product of the others; a view is a 2-D strided window
 // (offset and row stride ld in elements) into another tensor's storage.
@@ -574,6 +578,20 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
     BwppReduceParams rp = {(uint32_t)X.rows(), (uint32_t)X.cols(), (uint32_t)X.row_stride(),
                            (int32_t)num("axis", 1)};
     s = BWPP_PLAN_CALL(bwpp_hip_dispatch_reduce_sum(h, f32(op.ins[0]), f32(op.outs[0]), rp));
+  } else if (k == "reduce_max" || k == "reduce_max_mask") {
+    // Graph ops BWPP_GOP_REDUCE_MAX (values; graph_ir.c:663-695) and
+    // BWPP_GOP_REDUCE_MAX_MASK (bwpp_cpu_ref.c:146-190) along `axis`.
+    if (!need(1, 1)) return bad("in=X out=Y");
+    const Value &X = val(op.ins[0]);
+    BwppReduceParams rp = {(uint32_t)X.rows(), (uint32_t)X.cols(), (uint32_t)X.row_stride(),
+                           (int32_t)num("axis", 1)};
+    const uint64_t want = k == "reduce_max_mask" ? X.rows() * X.cols() : rp.axis == 0 ? X.cols() : X.rows();
+    if (val(op.outs[0]).elems() != want) return bad("output size does not match the reduction");
+    if (k == "reduce_max_mask" && val(op.outs[0]).row_stride() != X.row_stride())
+      return bad("mask needs X's row stride");
+    s = BWPP_PLAN_CALL(k == "reduce_max"
+                           ? bwpp_hip_dispatch_reduce_max(h, f32(op.ins[0]), f32(op.outs[0]), nullptr, rp)
+                           : bwpp_hip_dispatch_reduce_max_mask(h, f32(op.ins[0]), f32(op.outs[0]), rp));
   } else if (k == "silu_grad") {
     if (!need(2, 1)) return bad("in=X,dY out=dX");
     s = BWPP_PLAN_CALL(
@@ -596,11 +614,20 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
     const bool grad = k == "attention_grad";
     if (grad ? !need(6, 3) : !need(3, 1))
       return bad(grad ? "in=Q,K,V,O,dO,LSE out=dQ,dK,dV" : "in=Q,K,V out=O[,LSE]");
+    // layout=bshd (default): [batch*seq, heads*dim] row blocks, head h of a
+    // row at column h*dim.  layout=bhsd: [batch, heads, seq, dim] with one
+    // row per (batch, head, position).
     const uint64_t B = (uint64_t)num("batch", 1), H = (uint64_t)num("heads", 1);
+    const std::string lay = attr(op, "layout", "bshd");
+    if (lay != "bshd" && lay != "bhsd") return bad("layout must be bshd or bhsd");
+    const bool bhsd = lay == "bhsd";
     const Value &Q = val(op.ins[0]), &Kv = val(op.ins[1]), &V = val(op.ins[2]);
     const Value &O = grad ? val(op.ins[3]) : val(op.outs[0]);
-    if (!B || !H || Q.rows() % B || Kv.rows() % B || Q.cols() % H || V.cols() % H) return bad("bad batch / heads");
-    const uint64_t M = Q.rows() / B, N = Kv.rows() / B, dk = Q.cols() / H, dv = V.cols() / H;
+    const uint64_t qs = bhsd ? B * H : B;  // row blocks per tensor
+    if (!B || !H || Q.rows() % qs || Kv.rows() % qs || (!bhsd && (Q.cols() % H || V.cols() % H)))
+      return bad("bad batch / heads");
+    const uint64_t M = Q.rows() / qs, N = Kv.rows() / qs;
+    const uint64_t dk = bhsd ? Q.cols() : Q.cols() / H, dv = bhsd ? V.cols() : V.cols() / H;
     BwppAttentionParams ap = {};
     ap.M = (uint32_t)M;
     ap.N = (uint32_t)N;
@@ -612,15 +639,16 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
     ap.ldo = (uint32_t)O.row_stride();
     ap.batch = (uint32_t)B;
     ap.heads = (uint32_t)H;
-    ap.q_batch_stride = M * ap.ldq;
-    ap.q_head_stride = dk;
-    ap.k_batch_stride = N * ap.ldk;
-    ap.k_head_stride = dk;
-    ap.v_batch_stride = N * ap.ldv;
-    ap.v_head_stride = dv;
-    ap.o_batch_stride = M * ap.ldo;
-    ap.o_head_stride = dv;
-    ap.scale = (float)num("scale", 0.0);
+    ap.q_head_stride = bhsd ? M * ap.ldq : dk;
+    ap.q_batch_stride = bhsd ? H * M * ap.ldq : M * ap.ldq;
+    ap.k_head_stride = bhsd ? N * ap.ldk : dk;
+    ap.k_batch_stride = bhsd ? H * N * ap.ldk : N * ap.ldk;
+    ap.v_head_stride = bhsd ? N * ap.ldv : dv;
+    ap.v_batch_stride = bhsd ? H * N * ap.ldv : N * ap.ldv;
+    ap.o_head_stride = bhsd ? M * ap.ldo : dv;
+    ap.o_batch_stride = bhsd ? H * M * ap.ldo : M * ap.ldo;
+    // scale=auto: 1/sqrt(head dim), the usual choice the graph cannot state
+    ap.scale = attr(op, "scale", "") == "auto" ? (float)(1.0 / std::sqrt((double)dk)) : (float)num("scale", 0.0);
     ap.causal = (uint32_t)num("causal", 0);
     ap.dtype = Q.dtype;
     if (!grad) {

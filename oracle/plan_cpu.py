@@ -69,9 +69,11 @@ class CpuPlan:
         return n
 
     def _num(self, s: str) -> float:
-        if "." in s or "e" in s.lower():
+        """An attribute: a product of integers and dims, else a float."""
+        try:
+            return float(self._eval(s))
+        except PlanTextError:
             return float(s)
-        return float(self._eval(s))
 
     def _parse(self, text):
         header = False
@@ -196,6 +198,13 @@ class CpuPlan:
             axis = int(kv.get("axis", 1))
             r = o.reduce_sum(np.ascontiguousarray(X[0]), 0 if axis == 0 else 1)
             m(outs[0]).reshape(-1)[...] = r
+        elif k in ("reduce_max", "reduce_max_mask"):
+            axis = int(kv.get("axis", 1))
+            x = np.ascontiguousarray(X[0])
+            if k == "reduce_max":
+                m(outs[0]).reshape(-1)[...] = o.reduce_max(x, 0 if axis == 0 else 1)[0]
+            else:
+                m(outs[0])[...] = o.reduce_max_mask(x, 0 if axis == 0 else 1)
         elif k == "silu_grad":
             m(outs[0])[...] = o.silu_grad(X[0], X[1]).reshape(m(outs[0]).shape)
         elif k == "softmax_grad":
@@ -209,14 +218,23 @@ class CpuPlan:
                 m(outs[2]).reshape(-1)[...] = db
         elif k in ("attention", "attention_grad"):
             B, H = int(self._num(kv.get("batch", "1"))), int(self._num(kv.get("heads", "1")))
-            scale = float(kv.get("scale", 0.0)) or 1.0
             causal = bool(int(kv.get("causal", 0)))
+            bhsd = kv.get("layout", "bshd") == "bhsd"
+            if kv.get("scale") == "auto":  # 1/sqrt(head dim)
+                d = X[0].shape[1] if bhsd else X[0].shape[1] // H
+                scale = float(np.float32(1.0 / np.sqrt(d)))
+            else:
+                scale = float(kv.get("scale", 0.0)) or 1.0
 
-            def split(a):  # [B*T, H*d] -> [B, H, T, d]
+            def split(a):  # [B*T, H*d] (bshd) or [B*H*T, d] (bhsd) -> [B, H, T, d]
+                if bhsd:
+                    return np.ascontiguousarray(a.reshape(B, H, a.shape[0] // (B * H), a.shape[1]))
                 T, C = a.shape[0] // B, a.shape[1] // H
                 return np.ascontiguousarray(a.reshape(B, T, H, C).transpose(0, 2, 1, 3))
 
-            def merge(a):  # [B, H, T, d] -> [B*T, H*d]
+            def merge(a):  # inverse of split
+                if bhsd:
+                    return a.reshape(-1, a.shape[3])
                 return a.transpose(0, 2, 1, 3).reshape(a.shape[0] * a.shape[2], -1)
 
             q, kk, v = split(X[0]), split(X[1]), split(X[2])

@@ -1,95 +1,126 @@
-"""The transformer-block training plan (config 5's graph) run by the
-launch-plan executor on the GPU, against the same block differentiated by
-torch autograd on the CPU in float64 (a floating-point reference of the
-whole graph; every operator in it is also checked alone against the
-oracle).  fp32 bar: 1e-4 relative max-norm on the forward output, the loss
-and every gradient."""
+"""Plans lowered by bwppc-hip from the reference's examples, run by the
+launch-plan executor on the GPU.  Config 5's block (tiny_model's `block`
+and its DSL autodiff) against float64 autograd of the same program and the
+oracle; the rank-4 attention program in bf16 and config 3 as a DSL program
+against the oracle.  fp32 bar: 1e-4 relative max-norm on the forward
+output, the loss and every gradient; bf16 inputs: 2e-2."""
 import numpy as np
 import pytest
 
 import bwpp
 from bwpp import plan, synth
 from conftest import rel_max_err
+from oracle.plan_cpu import CpuPlan
 
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
 
 
-def _inputs(B, T, D, F, seed):
-    w = lambda shape, st: synth.normal(shape, seed, st, 0.0, 0.02)
-    return {
-        "x": synth.normal((B * T, D), seed, 0),
-        "g1": synth.uniform((D,), seed, 1, 0.5, 1.5),
-        "wqkv": w((D, 3 * D), 2),
-        "wo": w((D, D), 3),
-        "g2": synth.uniform((D,), seed, 4, 0.5, 1.5),
-        "w1": w((D, F), 5),
-        "w2": w((F, D), 6),
-    }
-
-
-def _reference(t, B, T, D, H, F):
+@pytest.mark.parametrize("BATCH,T,D,H,HEADS", [(2, 64, 128, 256, 2), (1, 100, 192, 384, 3),
+                                               (8, 512, 1024, 4096, 16)])
+def test_block_train_plan(be, oracle, BATCH, T, D, H, HEADS):
+    """The plan bwppc-hip lowers from tiny_model's block and its DSL autodiff
+    (plans/block_train.plan), rebound to each size; the last case is
+    config 5 itself (the step the bench times), where split-K runs on the
+    K = 4096 weight-gradient GEMMs and attention over 128 (batch, head)
+    slices.  Against float64 autograd of the same program, and at the small
+    sizes also against the same plan run op by op on the oracle."""
     import torch
-    p = {k: torch.tensor(v, dtype=torch.float64, requires_grad=True) for k, v in t.items()}
-    rms = lambda a, g: a / torch.sqrt((a * a).mean(dim=1, keepdim=True) + 1e-5) * g
-    n1 = rms(p["x"], p["g1"])
-    qkv = n1 @ p["wqkv"]
-    dh = D // H
-
-    def heads(m):
-        return m.reshape(B, T, H, dh).permute(0, 2, 1, 3)
-
-    q, k, v = heads(qkv[:, :D]), heads(qkv[:, D:2 * D]), heads(qkv[:, 2 * D:])
-    s = (q @ k.transpose(-1, -2)) * 0.125
-    mask = torch.ones(T, T, dtype=torch.bool).tril()
-    s = s.masked_fill(~mask, float("-inf"))
-    att = (torch.softmax(s, dim=-1) @ v).permute(0, 2, 1, 3).reshape(B * T, D)
-    x1 = p["x"] + att @ p["wo"]
-    z = rms(x1, p["g2"]) @ p["w1"]
-    out = x1 + torch.nn.functional.silu(z) @ p["w2"]
-    loss = (out * out).mean()
-    loss.backward()
-    grads = {f"d{k}": p[k].grad.numpy() for k in ("x", "g1", "wqkv", "wo", "g2", "w1", "w2")}
-    return out.detach().numpy(), float(loss.detach()), grads
-
-
-@pytest.mark.parametrize("B,T,D,H,F", [(2, 64, 128, 2, 256), (1, 100, 192, 3, 384),
-                                       (8, 512, 1024, 16, 4096)])
-def test_transformer_block_train_plan(be, B, T, D, H, F):
-    """The last case is config 5 at full size (the step the bench times):
-    there split-K runs on the K = 4096 weight-gradient GEMMs and attention
-    over 128 (batch, head) slices."""
-    import torch
-    t = _inputs(B, T, D, F, seed=B * 1000 + T)
-    p = plan.Plan(be, plan.load_text("transformer_block_train", B=B, T=T, D=D, H=H, F=F))
+    from blockref import block_inputs, block_reference, grad_shapes
+    text = plan.load_text("block_train", BATCH=BATCH, T=T, D=D, H=H, HEADS=HEADS)
+    t = block_inputs(BATCH, T, D, H, seed=BATCH * 1000 + T)
+    p = plan.Plan(be, text)
     p.allocate()
     dev = {k: torch.from_numpy(v).cuda() for k, v in t.items()}
     for k, v in dev.items():
         p.bind(k, v)
     p.run()
-    out = p.host("out", (B * T, D))
+    out = p.host("out", (BATCH * T, D))
     loss = float(p.host("loss", (1,))[0])
-    ref_out, ref_loss, ref_g = _reference(t, B, T, D, H, F)
+    shapes = grad_shapes(BATCH, T, D, H)
+    got = {name: p.host(name, shape) for name, shape in shapes.items()}
+    ref_out, ref_loss, ref_g = block_reference(t, BATCH, T, D, H, HEADS)
     assert rel_max_err(out, ref_out) <= TOL
     assert abs(loss - ref_loss) <= TOL * abs(ref_loss)
-    shapes = {"dx": (B * T, D), "dg1": (D,), "dwqkv": (D, 3 * D), "dwo": (D, D), "dg2": (D,),
-              "dw1": (D, F), "dw2": (F, D)}
-    for name, shape in shapes.items():
-        got = p.host(name, shape)
-        assert rel_max_err(got, ref_g[name]) <= TOL, name
+    for name in shapes:
+        assert rel_max_err(got[name], ref_g[name]) <= TOL, name
+    if BATCH * T <= 256:
+        cp = CpuPlan(text, oracle)
+        for k, v in t.items():
+            cp.bind(k, v)
+        cp.run()
+        assert rel_max_err(out, cp.get("out")) <= TOL
+        for name, shape in shapes.items():
+            assert rel_max_err(got[name], cp.get(name).reshape(shape)) <= TOL, name
     # A second run over the same arena gives the same result.
     p.run()
-    assert rel_max_err(p.host("dwqkv", shapes["dwqkv"]), ref_g["dwqkv"]) <= TOL
+    assert np.array_equal(p.host("dwq", shapes["dwq"]), got["dwq"])
     p.close()
 
 
 def test_plan_unbound_input_is_an_error(be):
-    p = plan.Plan(be, plan.load_text("transformer_block_train", B=1, T=8, D=64, H=1, F=64))
+    p = plan.Plan(be, plan.load_text("block_train", BATCH=1, T=8, D=64, H=64, HEADS=1))
     p.allocate()
     with pytest.raises(plan.PlanError) as e:
         p.run()
     assert "not bound" in str(e.value)
+    p.close()
+
+
+def _bf16_dev(torch, a):
+    return torch.from_numpy(synth.to_bf16_bits(a).view(np.int16)).cuda()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_plans_bf16(be, oracle, causal):
+    """attention.bwpp lowered for bf16 [B, H, T, D] operands: the training
+    plan (forward with lse, backward seeded by dout) and the causal
+    forward, at T = 2048, d = 128 (config 4's per-head shape), two (b, h)
+    slices checked against the oracle on the exact bf16 inputs; bar 2e-2."""
+    import torch
+    B, H, T, D = 2, 4, 2048, 128
+    vals = [synth.normal((B, H, T, D), 12, i) for i in range(4)]
+    bits = [synth.to_bf16_bits(v) for v in vals]
+    exact = [synth.bf16_bits_to_f32(b) for b in bits]
+    name = "attention_causal_bf16" if causal else "attention_train_bf16"
+    p = plan.Plan(be, plan.load_text(name, B=B, H=H, T=T, D=D))
+    p.allocate()
+    devs = [_bf16_dev(torch, v) for v in vals]
+    for n, d in zip(("q", "k", "v", "dout"), devs):
+        if not (causal and n == "dout"):
+            p.bind(n, d)
+    p.run()
+    scale = D ** -0.5
+    out = synth.bf16_bits_to_f32(p.host("out", (B, H, T, D), np.uint16))
+    grads = None if causal else [synth.bf16_bits_to_f32(p.host(n, (B, H, T, D), np.uint16)) for n in ("dq", "dk", "dv")]
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        sl = [np.ascontiguousarray(e[b:b + 1, h:h + 1]) for e in exact]
+        assert rel_max_err(out[b:b + 1, h:h + 1], oracle.attention_bh(*sl[:3], scale, causal)) <= 2e-2
+        if grads:
+            for got, want in zip(grads, oracle.attention_grad(*sl, scale, causal)):
+                assert rel_max_err(got[b:b + 1, h:h + 1], want) <= 2e-2
+    p.close()
+
+
+def test_c3_plan_bf16_gemm(be, oracle):
+    """matmul_add_silu.bwpp lowered at config 3's size (bf16): one GEMM with
+    the bias + SiLU epilogue; 64 rows against the oracle."""
+    import torch
+    M, K, N = 4096, 4096, 11008
+    a = synth.normal((M, K), 13, 0, 0.0, 0.02)
+    b = synth.normal((K, N), 13, 1, 0.0, 0.02)
+    bias = synth.normal((N,), 13, 2, 0.0, 0.02)
+    p = plan.Plan(be, plan.load_text("matmul_add_silu"))
+    p.allocate()
+    for n, v in (("a", a), ("b", b), ("bias", bias)):
+        p.bind(n, _bf16_dev(torch, v))
+    p.run()
+    y = synth.bf16_bits_to_f32(p.host("out", (M, N), np.uint16))
+    ex = lambda v: synth.bf16_bits_to_f32(synth.to_bf16_bits(v))
+    rows = np.r_[0:32, M - 32:M]
+    want = oracle.matmul(ex(a[rows]), ex(b), ex(bias), apply_silu=True, apply_bias=True)
+    assert rel_max_err(y[rows], want) <= 2e-2
     p.close()
 
 

@@ -9,7 +9,7 @@ import pytest
 
 from bwpp import plan
 
-SMALL = dict(B=2, T=64, D=128, H=2, F=256)
+SMALL = dict(BATCH=2, T=64, D=128, H=256, HEADS=2)
 
 
 def _ops_and_views(text):
@@ -32,7 +32,7 @@ def _buffers(report):
 
 @pytest.mark.parametrize("dims", [{}, SMALL])
 def test_block_plan_report_and_no_self_alias(dims):
-    text = plan.load_text("transformer_block_train", **dims)
+    text = plan.load_text("block_train", **dims)
     p = plan.Plan(None, text)
     rep = p.report()
     head = rep.splitlines()[0]
@@ -54,7 +54,7 @@ def test_block_plan_report_and_no_self_alias(dims):
 
 def test_block_plan_arena_fits_reuse():
     """Full-size config 5: every temp of fwd + bwd in well under 1 GB."""
-    p = plan.Plan(None, plan.load_text("transformer_block_train"))
+    p = plan.Plan(None, plan.load_text("block_train"))
     assert 0.3e9 < p.arena_bytes < 1.0e9
 
 

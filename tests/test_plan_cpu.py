@@ -1,6 +1,7 @@
 """The CPU plan executor (oracle/plan_cpu.py), which checks plans run on the
 GPU and times config 5's CPU baseline: it must reproduce float64 autograd of
-the same block (a textbook reference of the whole graph), and the oracle's
+the block the plan was lowered from (a textbook reference of the whole
+graph), and the oracle's
 transposed-operand matmuls it relies on must be bit-identical to the plain
 matmul on explicitly transposed copies (the reordered loops keep each
 output's k-order fp32 sum)."""
@@ -27,47 +28,22 @@ def test_transposed_matmul_bit_identical(oracle, ta, tb, M, N, K):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-def _block_inputs(B, T, D, F, seed):
-    from bwpp import synth
-    w = lambda shape, st: synth.normal(shape, seed, st, 0.0, 0.02)
-    return {"x": synth.normal((B * T, D), seed, 0), "g1": synth.uniform((D,), seed, 1, 0.5, 1.5),
-            "wqkv": w((D, 3 * D), 2), "wo": w((D, D), 3), "g2": synth.uniform((D,), seed, 4, 0.5, 1.5),
-            "w1": w((D, F), 5), "w2": w((F, D), 6)}
-
-
-def _torch_block(t, B, T, D, H, F):
-    import torch
-    p = {k: torch.tensor(v, dtype=torch.float64, requires_grad=True) for k, v in t.items()}
-    rms = lambda a, g: a / torch.sqrt((a * a).mean(dim=1, keepdim=True) + 1e-5) * g
-    n1 = rms(p["x"], p["g1"])
-    qkv = n1 @ p["wqkv"]
-    dh = D // H
-    heads = lambda m: m.reshape(B, T, H, dh).permute(0, 2, 1, 3)
-    q, k, v = heads(qkv[:, :D]), heads(qkv[:, D:2 * D]), heads(qkv[:, 2 * D:])
-    s = (q @ k.transpose(-1, -2)) * (dh ** -0.5)
-    s = s.masked_fill(~torch.ones(T, T, dtype=torch.bool).tril(), float("-inf"))
-    att = (torch.softmax(s, dim=-1) @ v).permute(0, 2, 1, 3).reshape(B * T, D)
-    x1 = p["x"] + att @ p["wo"]
-    out = x1 + torch.nn.functional.silu(rms(x1, p["g2"]) @ p["w1"]) @ p["w2"]
-    loss = (out * out).mean()
-    loss.backward()
-    return out.detach().numpy(), float(loss.detach()), {f"d{k}": p[k].grad.numpy() for k in t}
-
-
-@pytest.mark.parametrize("B,T,D,H,F", [(2, 16, 64, 1, 128), (1, 40, 96, 3, 192)])
-def test_cpu_plan_matches_float64_autograd(B, T, D, H, F):
-    text = plan.load_text("transformer_block_train", B=B, T=T, D=D, H=H, F=F)
-    text = text.replace("scale=0.125", f"scale={(D // H) ** -0.5!r}")
-    t = _block_inputs(B, T, D, F, seed=T)
+@pytest.mark.parametrize("BATCH,T,D,H,HEADS", [(2, 16, 64, 128, 1), (1, 40, 96, 192, 3)])
+def test_cpu_plan_matches_float64_autograd(BATCH, T, D, H, HEADS):
+    """The lowered training plan of tiny_model's block, run op by op on the
+    oracle, against float64 autograd of the same program."""
+    from blockref import block_inputs, block_reference, grad_shapes
+    text = plan.load_text("block_train", BATCH=BATCH, T=T, D=D, H=H, HEADS=HEADS)
+    t = block_inputs(BATCH, T, D, H, seed=T)
     cp = CpuPlan(text)
     for k, v in t.items():
         cp.bind(k, v)
     cp.run()
-    out, loss, grads = _torch_block(t, B, T, D, H, F)
+    out, loss, grads = block_reference(t, BATCH, T, D, H, HEADS)
     assert rel_max_err(cp.get("out"), out) <= 1e-5
     assert abs(float(cp.get("loss")[0, 0]) - loss) <= 1e-5 * abs(loss)
-    for name, want in grads.items():
-        assert rel_max_err(cp.get(name).reshape(want.shape), want) <= 1e-5, name
+    for name, shape in grad_shapes(BATCH, T, D, H).items():
+        assert rel_max_err(cp.get(name).reshape(shape), grads[name]) <= 1e-5, name
 
 
 def test_cpu_plan_rejects_bad_text():
