@@ -309,6 +309,64 @@ def pmc_summary(dirs):
     return "\n".join(lines)
 
 
+def stream_ceiling(torch, nbuf=3, reps=20):
+    """The box's read+write HBM ceiling for the C2 byte pattern: the best
+    GB/s of plain non-temporal 128-bit copies of X[8192 x 4096] fp32 (the
+    bytes one row operator moves), over float4-per-thread x block x grid
+    (tests/hip/stream.hip, loaded through HIP's module API), each timed as
+    the median of groups of back-to-back launches over `nbuf` rotating
+    buffer pairs."""
+    import ctypes
+    path = os.path.join(ROOT, "tests", "hip", "bwpp_stream.hsaco")
+    if not os.path.exists(path):
+        return None
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    mod = ctypes.c_void_p()
+    if hip.hipModuleLoad(ctypes.byref(mod), path.encode()) != 0:
+        return None
+
+    class Args(ctypes.Structure):
+        _fields_ = [("x", ctypes.c_void_p), ("y", ctypes.c_void_p), ("n", ctypes.c_uint64)]
+
+    n16 = ROWS * COLS // 4
+    xs = [torch.empty(ROWS * COLS, dtype=torch.float32, device="cuda").normal_() for _ in range(nbuf)]
+    ys = [torch.empty_like(x) for x in xs]
+    hip.hipModuleLaunchKernel.argtypes = [ctypes.c_void_p] + [ctypes.c_uint] * 7 + [ctypes.c_void_p] * 3
+    stream = torch.cuda.current_stream().cuda_stream
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    best = None
+    for v in (1, 2, 4, 8):
+        fn = ctypes.c_void_p()
+        if hip.hipModuleGetFunction(ctypes.byref(fn), mod, f"bwpp_stream_copy_v{v}".encode()) != 0:
+            continue
+        for block in (256, 512, 1024):
+            full = (n16 + block * v - 1) // (block * v)
+            for grid in sorted({cus, 2 * cus, 4 * cus, 8 * cus, full}):
+                if grid > full:
+                    continue
+                args = [Args(xs[i].data_ptr(), ys[i].data_ptr(), n16) for i in range(nbuf)]
+                params = [(ctypes.c_void_p * 1)(ctypes.addressof(a)) for a in args]
+
+                def launch(i):
+                    rc = hip.hipModuleLaunchKernel(fn, grid, 1, 1, block, 1, 1, 0, ctypes.c_void_p(stream),
+                                                   params[i % nbuf], None)
+                    if rc != 0:
+                        raise RuntimeError(f"stream launch failed ({rc})")
+
+                for i in range(nbuf * 2):
+                    launch(i)
+                t = _launch_times_ms(torch, launch, reps, group=10)
+                us = float(np.median(t)) * 1e3
+                gbs = 2 * ROWS * COLS * F / us / 1e3
+                if best is None or gbs > best["GB_s"]:
+                    best = {"GB_s": round(gbs, 1), "us_per_launch": round(us, 2), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                            "config": {"float4_per_thread": v, "block": block, "grid": grid}}
+    torch.cuda.synchronize()
+    hip.hipModuleUnload(mod)
+    best["kernel"] = "tests/hip/stream.hip bwpp_stream_copy_v*"
+    return best
+
+
 def cpu_baseline_c2(seed, reps):
     """The oracle on one host core over the five C2 operators at full size."""
     sys.path.insert(0, ROOT)
@@ -741,6 +799,11 @@ def main():
         "ops": ops,
         "host": host_info(),
     }
+    ceil = stream_ceiling(torch)
+    if ceil:
+        out["stream_ceiling"] = ceil
+        for op in ops.values():
+            op["frac_of_stream_ceiling"] = round(op["GB_s"] / ceil["GB_s"], 4)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_c2(args.seed, args.cpu_reps)
     else:

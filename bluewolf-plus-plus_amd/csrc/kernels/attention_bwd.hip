@@ -62,12 +62,20 @@ __device__ __forceinline__ float sum32(float v) {
 // Tile row of accumulator register r for lane half hi.
 __device__ __forceinline__ int acc_row(int r, int hi) { return 8 * (r >> 2) + 4 * hi + (r & 3); }
 
+// Two readers share every tile: 16-byte row reads (16 consecutive rows at
+// one logical chunk per 16-lane quarter) and the transposing reads (32 lanes
+// of 8 bytes: four consecutive rows x logical chunks q..q+3 of one
+// 64-byte quartet, q a multiple of 4).  With 64 four-byte banks both are
+// conflict-free when swz is a permutation on any 16 consecutive rows (row
+// reads) and, for D = 128, the four rows of a transposing read land in four
+// different quartets (bits 2-3 of swz take r & 3); for D = 64 (two rows per
+// 256 bank bytes) rows of equal parity do (bit 2 takes (r >> 1) & 1).
 template <int D>
 __device__ __forceinline__ uint32_t swz(uint32_t r) {
   if constexpr (D == 128)
-    return ((r & 3u) << 1) | ((r >> 2) & 1u) | (r & 8u);  // 16 chunks per 256-byte row
+    return ((r & 3u) << 2) | ((r >> 2) & 3u);  // 16 chunks per 256-byte row
   else
-    return (((r >> 1) & 1u) << 1) | ((r >> 2) & 1u) | (((r >> 3) & 1u) << 2);  // 8 chunks per 128-byte row
+    return (((r >> 1) & 1u) << 2) | (((r >> 2) & 1u) << 1) | ((r >> 3) & 1u);  // 8 chunks per 128-byte row
 }
 template <int D>
 __device__ __forceinline__ uint32_t toff(uint32_t r, uint32_t c) {
