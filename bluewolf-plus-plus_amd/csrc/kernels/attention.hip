@@ -349,8 +349,10 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
   }
   __syncthreads();
 
-  // O = O^T / l, staged through LDS ([query][d] bf16 per wave), then stored
-  // with 16-byte row chunks.
+  // O = O^T / l, staged through LDS ([query][d] bf16 per wave, 256-byte
+  // rows, 16-byte chunk c of row q at c ^ (q & 15)), then stored with
+  // 16-byte row chunks.  Without the swizzle the 32 rows a staging write
+  // touches at one column all fall on the same banks.
   uint16_t *os = reinterpret_cast<uint16_t *>(smem) + (size_t)wave * kQW * D;
   // Natural-log log-sum-exp of the scaled scores when asked for: the sum of
   // exp(scale s) is 2^mrow * lrow (mrow in log2 units).
@@ -363,11 +365,11 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
     for (int d = 0; d < DB; ++d)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        const uint32_t dd = 32u * d + 8u * q4 + 4u * lh;
+        const uint32_t chunk = (4u * d + q4) ^ (lq & 15u);
         uint2 w;
         w.x = pack_bf16x2(o[d][4 * q4 + 0] * inv, o[d][4 * q4 + 1] * inv);
         w.y = pack_bf16x2(o[d][4 * q4 + 2] * inv, o[d][4 * q4 + 3] * inv);
-        *reinterpret_cast<uint2 *>(os + lq * D + dd) = w;
+        *reinterpret_cast<uint2 *>(os + lq * D + 8u * chunk + 4u * lh) = w;
       }
   }
   __syncthreads();
@@ -379,7 +381,7 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
     const uint32_t qo = q0 + ql;
     if (qo < a.M)
       *reinterpret_cast<uint4 *>(O + (size_t)qo * a.ldo + 8u * cc) =
-          *reinterpret_cast<const uint4 *>(os + ql * D + 8u * cc);
+          *reinterpret_cast<const uint4 *>(os + ql * D + 8u * (cc ^ (ql & 15u)));
   }
   __syncthreads();  // the block's next tile reuses smem
 }
