@@ -40,6 +40,9 @@ typedef struct {
   uint32_t rank;
   char d[BWPP_GRAPH_MAX_DIMS][DIM_LEN + 8]; /* plan dims (batched) */
   char kind[64];
+  /* a 2-D strided window into plan value view_of (kind "view") */
+  int view_of;
+  char off[DIM_LEN + 8], ld[DIM_LEN + 8];
 } PVal;
 
 typedef struct {
@@ -50,6 +53,7 @@ typedef struct {
   int batched;  /* leading dim stacked `batch` times in the plan */
   int bf16;
   int known;    /* shape inferred */
+  int preset;   /* pv chosen before the producer is lowered (a view) */
   Shape shape;  /* logical shape (unbatched) */
   Shape src;    /* bcast: shape of pv's data */
 } LVal;
@@ -64,6 +68,31 @@ typedef struct {
   float scale;
 } AttnRegion;
 
+/* Sibling GEMMs: matmuls that share their left operand and take weights
+ * (params) of one shape, Y_m = A @ W_m.  They run as one GEMM against the
+ * column concatenation [W_0 | W_1 | ...] into [Y_0 | Y_1 | ...], each Y_m a
+ * column view.  In the autodiff graph (matmul rule, graph_ir.c:1529-1583)
+ * each member has dW_m = transpose(A') @ dY_m and dA_m = dY_m @
+ * transpose(W_m'), and the dA_m are summed by adds; with the dY_m written
+ * as column views of one [dY_0 | dY_1 | ...] these become two GEMMs:
+ * [dW_0 | dW_1 | ...] = transpose(A) @ dYcat and sum_m dA_m = dYcat @
+ * transpose(Wcat). */
+#define MM_GROUP_MAX 8
+typedef struct {
+  uint32_t a;
+  int n;
+  int node[MM_GROUP_MAX];
+  uint32_t w[MM_GROUP_MAX], y[MM_GROUP_MAX];
+  int wcat_pv;
+  /* autodiff graph */
+  int bwd;                      /* dW / dY grouping applies */
+  int da;                       /* the dA sum is grouped too */
+  int dw_node[MM_GROUP_MAX], da_node[MM_GROUP_MAX];
+  uint32_t dy[MM_GROUP_MAX];
+  uint32_t da_sum;              /* value holding sum_m dA_m */
+  int first_bwd;                /* node that emits the backward GEMMs */
+} MMGroup;
+
 typedef struct {
   const BwppLowerOptions *opt;
   char *err;
@@ -77,6 +106,8 @@ typedef struct {
   uint32_t const_used;
   AttnRegion *regions;
   int nregions;
+  MMGroup *groups;
+  int ngroups;
 } Ctx;
 
 typedef struct {
@@ -222,6 +253,7 @@ static int new_pv(Ctx *c, const char *base, const Shape *s, int batched, int bf1
   }
   PVal *p = &c->pv[c->npv];
   memset(p, 0, sizeof *p);
+  p->view_of = -1;
   sanitize(base, p->name);
   p->bf16 = bf16;
   p->rank = s->rank ? s->rank : 1;
@@ -237,6 +269,18 @@ static int new_pv(Ctx *c, const char *base, const Shape *s, int batched, int bf1
   }
   snprintf(p->kind, sizeof p->kind, "%s", kind);
   return c->npv++;
+}
+
+/* A view of plan value `base`: shape `s` (rank 2), columns from `off`, row
+ * stride `ld` (dim expressions, in elements). */
+static int new_view(Ctx *c, int base, const char *name, const Shape *s, int batched, const char *off,
+                    const char *ld) {
+  const int pv = new_pv(c, name, s, batched, base >= 0 ? c->pv[base].bf16 : 0, "view");
+  if (pv < 0) return pv;
+  c->pv[pv].view_of = base;
+  snprintf(c->pv[pv].off, sizeof c->pv[pv].off, "%s", off);
+  snprintf(c->pv[pv].ld, sizeof c->pv[pv].ld, "%s", ld);
+  return pv;
 }
 
 static void value_name(const BwppGraph *g, uint32_t v, const char *dflt, char *out) {
@@ -450,6 +494,7 @@ static int lval_batched(const Ctx *c, const Shape *s) {
 /* Gives graph value `v` a fresh plan value (temp) for its shape. */
 static int assign_pv(Ctx *c, GCtx *gc, uint32_t v, const char *prefix) {
   LVal *l = &gc->lv[v];
+  if (l->preset) return l->pv;
   char base[NAME_LEN];
   value_name(gc->g, v, prefix, base);
   l->batched = lval_batched(c, &l->shape);
@@ -760,6 +805,281 @@ static void find_norm_grads(Ctx *c, GCtx *gc, Bwd *b) {
       gc->skip[j] = gc->skip[mu] = gc->skip[rs] = 1;
       break;
     }
+  }
+}
+
+/* ------------------------------------------------------------ sibling GEMMs */
+
+static void need_known(Ctx *c, const GCtx *gc, uint32_t v);
+
+/* A forward matmul whose result lower_matmul would not fuse into an
+ * epilogue or emit transposed: the candidates for grouping. */
+static int mm_groupable(const GCtx *gc, uint32_t node) {
+  const BwppGraph *g = gc->g;
+  const BwppGraphNode *n = &g->nodes[node];
+  if (n->op != BWPP_GOP_MATMUL || n->input_count < 2 || gc->skip[node]) return 0;
+  const uint32_t w = n->inputs[1], y = n->output;
+  if (!(g->values[w].flags & BWPP_GRAPH_VALUE_INPUT) || g->values[w].shape.rank != 2) return 0;
+  if (is_output(g, y)) return 0;
+  /* the result becomes a strided column view: only readers that take a row
+   * stride (a fused attention region, another matmul) */
+  for (uint32_t j = 0; j < gc->ncons[y]; ++j) {
+    const uint32_t k = gc->cons[y][j];
+    if (!gc->skip[k] && g->nodes[k].op != BWPP_GOP_MATMUL) return 0;
+  }
+  return 1;
+}
+
+static int same_shape_text(const BwppShape *a, const BwppShape *b) {
+  if (a->rank != b->rank) return 0;
+  for (uint32_t i = 0; i < a->rank; ++i)
+    if (a->dims[i].len != b->dims[i].len || memcmp(a->dims[i].ptr, b->dims[i].ptr, a->dims[i].len)) return 0;
+  return 1;
+}
+
+static void find_mm_groups(Ctx *c, GCtx *gc) {
+  const BwppGraph *g = gc->g;
+  uint8_t *taken = (uint8_t *)calloc(g->node_count ? g->node_count : 1, 1);
+  if (!taken) {
+    fail(c, "out of memory");
+    return;
+  }
+  for (uint32_t i = 0; i < g->node_count; ++i) {
+    if (taken[i] || !mm_groupable(gc, i)) continue;
+    const BwppGraphNode *ni = &g->nodes[i];
+    MMGroup G;
+    memset(&G, 0, sizeof G);
+    G.a = ni->inputs[0];
+    G.node[0] = (int)i;
+    G.w[0] = ni->inputs[1];
+    G.y[0] = ni->output;
+    G.n = 1;
+    for (uint32_t j = i + 1; j < g->node_count && G.n < MM_GROUP_MAX; ++j) {
+      const BwppGraphNode *nj = &g->nodes[j];
+      if (taken[j] || !mm_groupable(gc, j) || nj->inputs[0] != G.a) continue;
+      const BwppGraphValue *wi = &g->values[G.w[0]], *wj = &g->values[nj->inputs[1]];
+      if (wi->dtype != wj->dtype || !same_shape_text(&wi->shape, &wj->shape) || nj->inputs[1] == G.w[0]) continue;
+      G.node[G.n] = (int)j;
+      G.w[G.n] = nj->inputs[1];
+      G.y[G.n] = nj->output;
+      ++G.n;
+    }
+    if (G.n < 2) continue;
+    for (int m = 0; m < G.n; ++m) {
+      taken[G.node[m]] = 1;
+      if (m) gc->skip[G.node[m]] = 1;
+    }
+    G.wcat_pv = -1;
+    G.first_bwd = -1;
+    MMGroup *p = (MMGroup *)realloc(c->groups, (size_t)(c->ngroups + 1) * sizeof(MMGroup));
+    if (!p) {
+      fail(c, "out of memory");
+      break;
+    }
+    c->groups = p;
+    c->groups[c->ngroups++] = G;
+  }
+  free(taken);
+}
+
+/* "m*N" for column block m of width N (dim text). */
+static void block_expr(char *buf, size_t cap, int m, const char *n) {
+  if (m == 0)
+    snprintf(buf, cap, "0");
+  else if (m == 1)
+    snprintf(buf, cap, "%s", n);
+  else
+    snprintf(buf, cap, "%d*%s", m, n);
+}
+
+/* Emits a forward group at its first node: the weight concatenation, one
+ * GEMM, and the members' results as column views. */
+static void lower_mm_group(Ctx *c, GCtx *gc, MMGroup *G) {
+  const LVal *A = &gc->lv[G->a];
+  need_known(c, gc, G->a);
+  if (c->failed) return;
+  if (A->shape.rank != 2 || A->trans || A->bcast || A->pv < 0) {
+    fail(c, "grouped matmul: left operand v%u is not a plain matrix", G->a);
+    return;
+  }
+  const LVal *W0 = &gc->lv[G->w[0]];
+  if (W0->shape.rank != 2 || W0->shape.n[0] != A->shape.n[1] || W0->bf16 != A->bf16) {
+    fail(c, "grouped matmul: weight shape or dtype does not match the left operand");
+    return;
+  }
+  char ncat[DIM_LEN + 8], off[DIM_LEN + 8], nm[NAME_LEN];
+  snprintf(ncat, sizeof ncat, "%d*%s", G->n, W0->shape.d[1]);
+  Shape ws = W0->shape;
+  shape_set_dim(&ws, 1, ncat, W0->shape.n[1] * (uint64_t)G->n);
+  G->wcat_pv = new_pv(c, "wcat", &ws, 0, A->bf16, "temp");
+  for (int m = 0; m < G->n; ++m) {
+    block_expr(off, sizeof off, m, W0->shape.d[1]);
+    value_name(gc->g, G->w[m], "w", nm);
+    char vn[NAME_LEN + 8];
+    snprintf(vn, sizeof vn, "%s_in_cat", nm);
+    const int view = new_view(c, G->wcat_pv, vn, &W0->shape, 0, off, ncat);
+    emit(c, "op copy out=%s in=%s bcast=full\n", ref(view).s, operand(c, gc, G->w[m]).s);
+  }
+  Shape ys;
+  memset(&ys, 0, sizeof ys);
+  ys.rank = 2;
+  shape_set_dim(&ys, 0, A->shape.d[0], A->shape.n[0]);
+  shape_set_dim(&ys, 1, ncat, W0->shape.n[1] * (uint64_t)G->n);
+  const int ycat = new_pv(c, "ycat", &ys, A->batched, A->bf16, "temp");
+  emit(c, "op matmul out=%s in=%s,%s\n", ref(ycat).s, ref(A->pv).s, ref(G->wcat_pv).s);
+  for (int m = 0; m < G->n; ++m) {
+    LVal *Y = &gc->lv[G->y[m]];
+    memset(&Y->shape, 0, sizeof Y->shape);
+    Y->shape.rank = 2;
+    shape_set_dim(&Y->shape, 0, A->shape.d[0], A->shape.n[0]);
+    shape_set_dim(&Y->shape, 1, W0->shape.d[1], W0->shape.n[1]);
+    Y->known = 1;
+    Y->bf16 = A->bf16;
+    Y->batched = A->batched;
+    Y->trans = Y->bcast = 0;
+    block_expr(off, sizeof off, m, W0->shape.d[1]);
+    value_name(gc->g, G->y[m], "y", nm);
+    Y->pv = new_view(c, ycat, nm, &Y->shape, Y->batched, off, ncat);
+  }
+}
+
+/* The members' autodiff terms (see MMGroup).  Applies when every dY_m is
+ * an output of a fused attention_grad (which writes strided blocks) and is
+ * read only by its dW_m and dA_m. */
+static void find_mm_group_grads(Ctx *c, GCtx *gc, Bwd *b) {
+  const BwppGraph *g = gc->g;
+  uint8_t *mask = (uint8_t *)calloc(g->value_count ? g->value_count : 1, 1);
+  if (!mask) {
+    fail(c, "out of memory");
+    return;
+  }
+  for (int gi = 0; gi < c->ngroups; ++gi) {
+    MMGroup *G = &c->groups[gi];
+    G->bwd = G->da = 0;
+    if (G->wcat_pv < 0) continue;
+    int ok = 1;
+    for (int m = 0; m < G->n && ok; ++m) {
+      int da = -1, dw = -1;
+      for (uint32_t i = 0; i < g->node_count && da < 0; ++i)
+        if (!gc->skip[i] && mm_with_tclone(b, gc, (int)i, 1, G->w[m])) da = (int)i;
+      if (da < 0) {
+        ok = 0;
+        break;
+      }
+      const uint32_t dy = g->nodes[da].inputs[0];
+      for (uint32_t j = 0; j < gc->ncons[dy]; ++j) {
+        const int k = (int)gc->cons[dy][j];
+        if (k != da && g->nodes[k].input_count >= 2 && g->nodes[k].inputs[1] == dy &&
+            mm_with_tclone(b, gc, k, 0, G->a))
+          dw = k;
+      }
+      int from_attn = 0;
+      for (int a = 0; a < b->nag; ++a)
+        from_attn |= b->ag[a].dq == dy || b->ag[a].dk == dy || b->ag[a].dv == dy;
+      /* dW_m becomes a view too: it must be read by nothing (a grad output) */
+      if (dw < 0 || gc->ncons[dy] != 2 || !from_attn || is_output(g, dy) ||
+          gc->ncons[g->nodes[dw].output] != 0)
+        ok = 0;
+      G->da_node[m] = da;
+      G->dw_node[m] = dw;
+      G->dy[m] = dy;
+    }
+    if (!ok) continue;
+    G->bwd = 1;
+    /* the adds that sum the dA_m */
+    memset(mask, 0, g->value_count);
+    const uint8_t full = (uint8_t)((1u << G->n) - 1u);
+    int da_ok = 1;
+    for (int m = 0; m < G->n; ++m) {
+      const uint32_t o = g->nodes[G->da_node[m]].output;
+      if (gc->ncons[o] != 1 || is_output(g, o)) da_ok = 0;
+      mask[o] = (uint8_t)(1u << m);
+    }
+    int adds[MM_GROUP_MAX], nadds = 0;
+    int32_t sum = -1;
+    for (uint32_t i = 0; i < g->node_count && da_ok && sum < 0; ++i) {
+      const BwppGraphNode *n = &g->nodes[i];
+      if (n->op != BWPP_GOP_ADD || n->input_count < 2 || gc->skip[i]) continue;
+      const uint8_t ma = mask[n->inputs[0]], mb = mask[n->inputs[1]];
+      if (!ma || !mb) continue;
+      if ((ma & mb) || gc->ncons[n->inputs[0]] != 1 || gc->ncons[n->inputs[1]] != 1 || nadds >= MM_GROUP_MAX) {
+        da_ok = 0;
+        break;
+      }
+      adds[nadds++] = (int)i;
+      mask[n->output] = (uint8_t)(ma | mb);
+      if (mask[n->output] == full) sum = (int32_t)n->output;
+    }
+    G->da = da_ok && sum >= 0;
+    G->first_bwd = G->dw_node[0];
+    for (int m = 0; m < G->n; ++m) {
+      if (G->dw_node[m] < G->first_bwd) G->first_bwd = G->dw_node[m];
+      gc->skip[G->dw_node[m]] = 1;
+      if (G->da) {
+        if (G->da_node[m] < G->first_bwd) G->first_bwd = G->da_node[m];
+        gc->skip[G->da_node[m]] = 1;
+      }
+    }
+    if (G->da) {
+      G->da_sum = (uint32_t)sum;
+      for (int k = 0; k < nadds; ++k) gc->skip[adds[k]] = 1;
+    }
+    /* dY_m: column views of one [rows, n*N] buffer, filled by attention_grad */
+    const LVal *Y0 = &b->fc->lv[G->y[0]];
+    char ncat[DIM_LEN + 8], off[DIM_LEN + 8], nm[NAME_LEN];
+    snprintf(ncat, sizeof ncat, "%d*%s", G->n, Y0->shape.d[1]);
+    Shape ys = Y0->shape;
+    shape_set_dim(&ys, 1, ncat, Y0->shape.n[1] * (uint64_t)G->n);
+    const int dycat = new_pv(c, "dycat", &ys, Y0->batched, Y0->bf16, "temp");
+    for (int m = 0; m < G->n; ++m) {
+      LVal *l = &gc->lv[G->dy[m]];
+      l->shape = Y0->shape;
+      l->known = 1;
+      l->bf16 = Y0->bf16;
+      l->batched = Y0->batched;
+      l->trans = l->bcast = 0;
+      block_expr(off, sizeof off, m, Y0->shape.d[1]);
+      value_name(b->f, G->y[m], "y", nm);
+      char vn[NAME_LEN + 8];
+      snprintf(vn, sizeof vn, "d%s", nm);
+      l->pv = new_view(c, dycat, vn, &Y0->shape, Y0->batched, off, ncat);
+      l->preset = 1;
+    }
+  }
+  free(mask);
+}
+
+/* The backward GEMMs of a group, at its first autodiff node. */
+static void lower_mm_group_grad(Ctx *c, GCtx *gc, const Bwd *b, const MMGroup *G) {
+  const GCtx *fc = b->fc;
+  const LVal *A = &fc->lv[G->a], *W0 = &fc->lv[G->w[0]];
+  const int dycat = c->pv[gc->lv[G->dy[0]].pv].view_of;
+  char ncat[DIM_LEN + 8], off[DIM_LEN + 8];
+  snprintf(ncat, sizeof ncat, "%d*%s", G->n, W0->shape.d[1]);
+  Shape ws = W0->shape;
+  shape_set_dim(&ws, 1, ncat, W0->shape.n[1] * (uint64_t)G->n);
+  const int dwcat = new_pv(c, "dwcat", &ws, 0, A->bf16, "temp");
+  emit(c, "op matmul out=%s in=%s,%s ta=1\n", ref(dwcat).s, ref(A->pv).s, ref(dycat).s);
+  for (int m = 0; m < G->n; ++m) {
+    LVal *l = &gc->lv[gc->g->nodes[G->dw_node[m]].output];
+    l->shape = W0->shape;
+    l->known = 1;
+    l->bf16 = A->bf16;
+    l->batched = 0;
+    l->trans = l->bcast = 0;
+    block_expr(off, sizeof off, m, W0->shape.d[1]);
+    char nm[NAME_LEN], vn[NAME_LEN + 8];
+    value_name(b->f, G->w[m], "w", nm);
+    snprintf(vn, sizeof vn, "d%s_in_cat", nm);
+    l->pv = new_view(c, dwcat, vn, &W0->shape, 0, off, ncat);
+  }
+  if (G->da) {
+    LVal *l = &gc->lv[G->da_sum];
+    l->shape = A->shape;
+    l->known = 1;
+    l->bf16 = A->bf16;
+    assign_pv(c, gc, G->da_sum, "t");
+    emit(c, "op matmul out=%s in=%s,%s tb=1\n", ref(l->pv).s, ref(dycat).s, ref(G->wcat_pv).s);
   }
 }
 
@@ -1125,7 +1445,14 @@ static void lower_nodes(Ctx *c, GCtx *gc, const uint8_t *needed, Bwd *bwd, int w
     if (!gc->is_grad) {
       for (int r = 0; r < c->nregions; ++r)
         if (c->regions[r].mm2 == (int)i) lower_attention(c, gc, &c->regions[r], with_lse);
+      for (int k = 0; k < c->ngroups; ++k)
+        if (c->groups[k].node[0] == (int)i) {
+          lower_mm_group(c, gc, &c->groups[k]);
+          gc->skip[i] = 2;  /* emitted */
+        }
     } else if (bwd) {
+      for (int k = 0; k < c->ngroups; ++k)
+        if (c->groups[k].bwd && c->groups[k].first_bwd == (int)i) lower_mm_group_grad(c, gc, bwd, &c->groups[k]);
       for (int a = 0; a < bwd->nag; ++a) {
         const AttnGrad *ag = &bwd->ag[a];
         if (ag->first != (int)i) continue;
@@ -1214,6 +1541,7 @@ void bwpp_lower_options_init(BwppLowerOptions *opt) {
   opt->heads = 1;
   opt->f16_as = BWPP_DTYPE_F32;
   opt->fuse_attention = 1;
+  opt->group_gemms = 1;
 }
 
 static void render(Ctx *c, FILE *out) {
@@ -1249,9 +1577,16 @@ static void render(Ctx *c, FILE *out) {
   fprintf(out, "\n");
   for (int i = 0; i < c->npv; ++i) {
     const PVal *p = &c->pv[i];
+    if (p->view_of >= 0) continue;
     fprintf(out, "value %s %s [", names[i], p->bf16 ? "bf16" : "f32");
     for (uint32_t d = 0; d < p->rank; ++d) fprintf(out, "%s%s", d ? "," : "", p->d[d]);
     fprintf(out, "] %s\n", p->kind);
+  }
+  for (int i = 0; i < c->npv; ++i) {
+    const PVal *p = &c->pv[i];
+    if (p->view_of < 0) continue;
+    fprintf(out, "view %s of=%s offset=%s ld=%s shape=[%s,%s]\n", names[i], names[p->view_of], p->off, p->ld,
+            p->d[0], p->d[1]);
   }
   fprintf(out, "\n");
   for (const char *s = c->ops; s && *s; ++s) {
@@ -1318,6 +1653,7 @@ BwppStatus bwpp_codegen_hip(const BwppGraph *graph, const BwppGraph *grad, const
      * lower the nodes ahead of each region first (cheap: one pass) */
     find_attention(&c, &fc);
   }
+  if (opt->group_gemms && !c.failed) find_mm_groups(&c, &fc);
   lower_nodes(&c, &fc, needed, NULL, opt->train != BWPP_LOWER_TRAIN_NONE);
   if (c.failed) goto done;
   if (graph->output_count != 1) {
@@ -1430,6 +1766,7 @@ BwppStatus bwpp_codegen_hip(const BwppGraph *graph, const BwppGraph *grad, const
     if (c.failed) goto done;
     lower_consts(&c, &gcx);
     if (opt->fuse_attention) find_attention_grads(&c, &gcx, &bwd);
+    if (!c.failed) find_mm_group_grads(&c, &gcx, &bwd);
     find_norm_grads(&c, &gcx, &bwd);
     lower_nodes(&c, &gcx, NULL, &bwd, 0);
     if (c.failed) goto done;
@@ -1465,5 +1802,6 @@ done:
   free(c.pv);
   free(c.ops);
   free(c.regions);
+  free(c.groups);
   return c.failed ? BWPP_ERR : BWPP_OK;
 }

@@ -21,7 +21,11 @@
  *     intermediate (the backward's activations included);
  *   - rmsnorm_grad plus the graph's dGamma chain (div / mul / reduce_sum,
  *     graph_ir.c:1747-1781) become one rmsnorm_grad launch with two
- *     outputs.
+ *     outputs;
+ *   - matmuls that share their left operand and take weights of one shape
+ *     (q, k, v projections) run as one GEMM against the weights' column
+ *     concatenation, their results column views; in training their weight
+ *     gradients and the sum of their input gradients are one GEMM each.
  * Shapes are inferred here rather than read from the graph where the graph
  * leaves them unset: `@` and transpose of rank 3/4 (graph_ir.c:557-562,
  * 848-863).  Symbolic dims are bound by the caller (--dim).  Numeric
@@ -73,6 +77,10 @@ typedef struct {
   BwppDType f16_as;
   BwppLowerTrain train;
   int fuse_attention; /* 0: lower the attention pattern op by op */
+  int group_gemms;    /* matmuls sharing their left operand, with weights of
+                         one shape, run as one GEMM against the weights'
+                         column concatenation (and so do their dW and dA
+                         terms in training); 0: one GEMM each */
   /* payloads of the graph's valueless numeric literals, in value order */
   float const_values[BWPP_LOWER_MAX_CONSTS];
   uint32_t const_count;

@@ -107,7 +107,9 @@ typedef struct {
   uint32_t op;      /* elementwise op */
   uint32_t bmode;   /* broadcast of b: 0 full, 1 row vector [cols], 2 column vector [rows], 3 scalar */
   uint32_t nparts;  /* partial rows to reduce */
-  uint32_t vec;     /* 1: a, b, out are 16-byte aligned (flat ops) */
+  uint32_t vec;     /* 1: a, b, out are 16-byte aligned (flat ops); 16-byte
+                       rows (elementwise) */
+  uint32_t ldb;     /* elementwise, full broadcast: row stride of b */
 } BwppGradArgs;
 
 #endif /* BWPP_KARGS_H */

@@ -1162,6 +1162,29 @@ uint32_t row_grid(const BwppHip *h, uint32_t rows) {
   return rows < cap ? rows : cap;
 }
 
+// bwpp_elementwise over rows x cols: a / out with row stride ld, b (when
+// full) with ldb.  The 128-bit path needs 16-byte rows and pointers.
+BwppHipStatus elementwise_launch(BwppHip *h, const float *a, const float *b, uint32_t ldb, float *out, uint32_t ld,
+                                 uint32_t rows, uint32_t cols, uint32_t op, uint32_t bmode) {
+  auto a16 = [](const void *q) { return ((uintptr_t)q & 15u) == 0; };
+  BwppGradArgs g = {};
+  g.a = a;
+  g.b = b;
+  g.out = out;
+  g.rows = rows;
+  g.cols = cols;
+  g.ld = ld;
+  g.ldb = ldb;
+  g.op = op;
+  g.bmode = bmode;
+  g.vec = cols % 4 == 0 && ld % 4 == 0 && a16(out) && (!a || a16(a)) &&
+                  (bmode == BWPP_HIP_BCAST_COL || bmode == BWPP_HIP_BCAST_SCALAR || a16(b)) &&
+                  (bmode != BWPP_HIP_BCAST_FULL || ldb % 4 == 0)
+              ? 1u
+              : 0u;
+  return launch(h, h->elementwise, row_grid(h, rows), 1, 1, 256, g);
+}
+
 }  // namespace
 
 extern "C" BwppHipStatus bwpp_hip_dispatch_silu_grad(BwppHip *h, const float *x, const float *dy, float *dx,
@@ -1300,14 +1323,16 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_elementwise(BwppHip *h, const float *
   const uint32_t ld = eff_ld(p.ld, p.cols);
   if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
   if (p.rows == 0 || p.cols == 0) return BWPP_HIP_OK;
-  BwppGradArgs g = {};
-  g.a = unary ? nullptr : a;
-  g.b = b;
-  g.out = out;
-  g.rows = p.rows;
-  g.cols = p.cols;
-  g.ld = ld;
-  g.op = p.op;
-  g.bmode = p.bmode;
-  return launch(h, h->elementwise, row_grid(h, p.rows), 1, 1, 256, g);
+  return elementwise_launch(h, unary ? nullptr : a, b, ld, out, ld, p.rows, p.cols, p.op, p.bmode);
+}
+
+BwppHipStatus bwpp_hip_copy_strided(BwppHip *h, const float *src, uint32_t ld_src, float *dst, uint32_t ld_dst,
+                                    uint32_t rows, uint32_t cols) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!src || !dst) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "copy: NULL pointer");
+  if (ld_src < cols || ld_dst < cols)
+    return fail(h, BWPP_HIP_ERR_INVALID_ARG, "copy: row strides (%u, %u) below cols (%u)", ld_src, ld_dst, cols);
+  if (rows == 0 || cols == 0) return BWPP_HIP_OK;
+  return elementwise_launch(h, nullptr, src, ld_src, dst, ld_dst, rows, cols, BWPP_HIP_OP_COPY, BWPP_HIP_BCAST_FULL);
 }

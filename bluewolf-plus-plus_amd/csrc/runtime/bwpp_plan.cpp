@@ -567,6 +567,16 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
                            : bm == "scalar" ? BWPP_HIP_BCAST_SCALAR : BWPP_HIP_BCAST_FULL;
     const uint32_t opc = k == "add" ? BWPP_HIP_OP_ADD : k == "sub" ? BWPP_HIP_OP_SUB : k == "mul" ? BWPP_HIP_OP_MUL
                          : k == "div" ? BWPP_HIP_OP_DIV : k == "copy" ? BWPP_HIP_OP_COPY : BWPP_HIP_OP_SILU;
+    if (k == "copy" && bmode == BWPP_HIP_BCAST_FULL && val(bi).row_stride() != C.row_stride()) {
+      // a copy between a tensor and a strided view (e.g. one weight into
+      // its column block of a concatenation): strides may differ
+      const Value &X = val(bi);
+      if (X.rows() != C.rows() || X.cols() != C.cols()) return bad("copy needs equal shapes");
+      s = BWPP_PLAN_CALL(bwpp_hip_copy_strided(h, f32(bi), (uint32_t)X.row_stride(), f32(op.outs[0]),
+                                               (uint32_t)C.row_stride(), (uint32_t)C.rows(), (uint32_t)C.cols()));
+      if (s != BWPP_HIP_OK) return perr(&p, s, "line %d (%s): %s", op.line, k.c_str(), bwpp_hip_last_error(h));
+      return BWPP_HIP_OK;
+    }
     if (bmode == BWPP_HIP_BCAST_FULL && val(bi).row_stride() != C.row_stride()) return bad("full b needs C's stride");
     if (!unary && val(op.ins[0]).row_stride() != C.row_stride()) return bad("a needs C's stride");
     BwppElementwiseParams ep = {(uint32_t)C.rows(), (uint32_t)C.cols(), (uint32_t)C.row_stride(), opc, bmode};

@@ -24,3 +24,9 @@ BwppHipStatus bwpp_hip_set_error(BwppHip *h, BwppHipStatus s, const char *fmt, .
 // (hipGetSymbolAddress) with that device current.  On failure *ptr is NULL,
 // *why names the HIP error and the status is BWPP_HIP_ERR_HIP.
 BwppHipStatus bwpp_hip_scratch_setup(int device, void **ptr, const char **why);
+
+// dst[r][c] = src[r][c] for rows x cols with independent row strides (in
+// elements), on the handle's stream: the plan executor's copy between a
+// tensor and a strided view of another.
+BwppHipStatus bwpp_hip_copy_strided(BwppHip *h, const float *src, uint32_t ld_src, float *dst, uint32_t ld_dst,
+                                    uint32_t rows, uint32_t cols);

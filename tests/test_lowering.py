@@ -170,6 +170,35 @@ def test_fused_attention_matches_op_by_op_lowering(bwppc, tmp_path):
 
 
 @needs_reference
+def test_grouped_projections_match_separate_gemms(bwppc, tmp_path):
+    """q, k, v = x @ wq, x @ wk, x @ wv run as one GEMM against [wq | wk |
+    wv] (column views for q, k, v), and in training dwq / dwk / dwv and
+    dx's three terms as one GEMM each; the step equals the lowering with
+    one GEMM per projection."""
+    from blockref import block_inputs
+    src = os.path.join(REFERENCE, "examples", "tiny_model.bwpp")
+    B, T, D, H, HEADS = 2, 32, 48, 96, 3
+    dims = ["--entry", "block", "--dim", f"T={T}", "--dim", f"D={D}", "--dim", f"H={H}", "--batch", str(B),
+            "--heads", str(HEADS), "--causal", "--attn-scale", "auto", "--train", "mean_square"]
+    grouped = lower(bwppc, src, tmp_path, *dims)
+    separate = lower(bwppc, src, tmp_path, *dims, "--no-group-gemms")
+    n_mm = lambda t: sum(l.startswith("op matmul ") for l in t.splitlines())
+    assert n_mm(separate) - n_mm(grouped) == 2 + 4  # forward 3 -> 1; dW 3 -> 1, dx terms 3 -> 1
+    assert "view q of=ycat offset=0 ld=3*D shape=[BATCH*T,D]" in grouped
+    assert "op matmul out=dwcat in=n1,dycat ta=1" in grouped
+    t = block_inputs(B, T, D, H, seed=11)
+    runs = []
+    for text in (grouped, separate):
+        cp = CpuPlan(text)
+        for k, v in t.items():
+            cp.bind(k, v)
+        cp.run()
+        runs.append(cp)
+    for name in ("out", "loss", "dx", "dwq", "dwk", "dwv", "dwo", "dw1", "dw2", "dg1", "dg2"):
+        assert rel_max_err(runs[0].get(name), runs[1].get(name)) <= 1e-5, name
+
+
+@needs_reference
 def test_literal_values_must_be_supplied(bwppc, tmp_path):
     src = os.path.join(FIXTURES, "scaled.bwpp")
     err = lower(bwppc, src, tmp_path, "--dim", "M=4", "--dim", "N=8", ok=False)
