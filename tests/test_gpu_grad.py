@@ -114,18 +114,30 @@ def test_reduce_sum(be, oracle, rows, cols, axis):
 
 @pytest.mark.parametrize("op", [0, 1, 2, 3, 4])
 @pytest.mark.parametrize("bmode", [0, 1, 2, 3])
-def test_elementwise(be, op, bmode):
+@pytest.mark.parametrize("rows,cols,ld,shift", [(13, 70, 70, 0), (13, 72, 72, 0), (9, 1024, 1028, 0),
+                                                (5, 72, 76, 1)])
+def test_elementwise(be, op, bmode, rows, cols, ld, shift):
+    """Scalar path (cols 70, or a / b / out one element off 16-byte
+    alignment) and 128-bit path (cols and ld multiples of 4), padded rows
+    left untouched."""
     torch = _torch()
-    rows, cols = 13, 70
-    a = synth.normal((rows, cols), 1, 0)
-    bshape = {0: (rows, cols), 1: (cols,), 2: (rows,), 3: (1,)}[bmode]
+    a = synth.normal((rows, ld), 1, 0)
+    bshape = {0: (rows, ld), 1: (cols,), 2: (rows,), 3: (1,)}[bmode]
     b = synth.uniform(bshape, 2, 1, 0.5, 2.0)
-    out = torch.empty((rows, cols), device="cuda")
-    be.dispatch_elementwise(dev(a), dev(b), out, bwpp.ElementwiseParams(rows, cols, cols, op, bmode))
-    bb = b if bmode == 0 else b[None, :] if bmode == 1 else b[:, None] if bmode == 2 else b.reshape(1, 1)
+    base = torch.full((rows * ld + shift,), 9.0, device="cuda")
+    out = base[shift:].view(rows, ld)
+    ad = torch.zeros(rows * ld + shift, device="cuda")
+    ad[shift:] = dev(a).reshape(-1)
+    bd = torch.zeros(b.size + shift, device="cuda")
+    bd[shift:] = dev(b).reshape(-1)
+    be.dispatch_elementwise(ad[shift:], bd[shift:], out, bwpp.ElementwiseParams(rows, cols, ld, op, bmode))
+    bb = b[:, :cols] if bmode == 0 else b[None, :] if bmode == 1 else b[:, None] if bmode == 2 else b.reshape(1, 1)
     bb = np.broadcast_to(bb, (rows, cols)).astype(np.float32)
-    want = {0: a + bb, 1: a - bb, 2: a * bb, 3: a / bb, 4: bb}[op].astype(np.float32)
-    assert_bits_equal(host(out), want)
+    aa = a[:, :cols]
+    want = {0: aa + bb, 1: aa - bb, 2: aa * bb, 3: aa / bb, 4: bb}[op].astype(np.float32)
+    got = host(out)
+    assert_bits_equal(got[:, :cols], want)
+    assert np.all(got[:, cols:] == 9.0)
 
 
 @pytest.mark.parametrize("n", [1, 70, 4096 * 1024 + 3])

@@ -168,3 +168,38 @@ op attention out=o,lse in=q,k,v batch={B} heads={H} causal=1 scale=0.125
     wl = oracle.attention_lse(q, k, 0.125, True)
     assert np.max(np.abs(lse - wl)) <= 2e-2 * max(1.0, np.abs(wl).max())
     p.close()
+
+
+@pytest.mark.parametrize("C", [6, 8])
+def test_copy_between_strided_views(be, C):
+    """Copies into and out of column views of a wider tensor (the weight
+    concatenation of grouped GEMMs): the executor's strided copy, on the
+    scalar path (C = 6) and the 128-bit path (C = 8)."""
+    import torch
+    R = 5
+    text = f"""bwpp.plan 1
+dim R {R}
+dim C {C}
+value x f32 [R,C] input
+value y f32 [R,C] input
+value cat f32 [R,2*C] temp
+value whole f32 [R,2*C] output
+value back f32 [R,C] output
+view xc of=cat offset=0 ld=2*C shape=[R,C]
+view yc of=cat offset=C ld=2*C shape=[R,C]
+op copy out=xc in=x bcast=full
+op copy out=yc in=y bcast=full
+op copy out=whole in=cat bcast=full
+op copy out=back in=yc bcast=full
+"""
+    x, y = synth.normal((R, C), 1, 0), synth.normal((R, C), 2, 0)
+    p = plan.Plan(be, text)
+    p.allocate()
+    xd = torch.from_numpy(x).cuda()
+    yd = torch.from_numpy(y).cuda()
+    p.bind("x", xd)
+    p.bind("y", yd)
+    p.run()
+    assert np.array_equal(p.host("whole", (R, 2 * C)), np.hstack([x, y]))
+    assert np.array_equal(p.host("back", (R, C)), y)
+    p.close()
