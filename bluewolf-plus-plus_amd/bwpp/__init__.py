@@ -5,13 +5,13 @@ objects (lib/); this package only binds them.  There is no CPU fallback:
 if the library or a code object is missing, HipBackend() raises.
 """
 from . import _lib, plan, synth
-from ._lib import (AttentionParams, CoreDType, DType, ElementwiseParams, Epilogue,
-                   LibraryMissing, MatmulParams, ReduceParams, RmsnormParams,
+from ._lib import (AttentionParams, CoreDType, DType, ElementwiseParams, Epilogue, Fusion,
+                   FusionParams, LibraryMissing, MatmulParams, ReduceParams, RmsnormParams,
                    SoftmaxParams, Status, Tensor)
 from .backend import BwppError, HipBackend, tensor_of
 
 __all__ = ["HipBackend", "BwppError", "LibraryMissing", "Status", "DType",
-           "Epilogue", "MatmulParams", "SoftmaxParams", "RmsnormParams",
+           "Epilogue", "Fusion", "FusionParams", "MatmulParams", "SoftmaxParams", "RmsnormParams",
            "AttentionParams", "ReduceParams", "ElementwiseParams", "CoreDType", "Tensor",
            "tensor_of", "synth", "plan",
            "load_library"]

@@ -50,6 +50,17 @@ class MatmulParams(Structure):
                 ("trans_a", c_uint32), ("trans_b", c_uint32)]
 
 
+class Fusion(enum.IntEnum):
+    NONE = 0
+    RESIDUAL = 1
+    DUAL_SILU = 2
+    SILU_GRAD = 3
+
+
+class FusionParams(Structure):
+    _fields_ = [("kind", c_uint32), ("ld_aux", c_uint32), ("ld_c2", c_uint32)]
+
+
 class SoftmaxParams(Structure):
     _fields_ = [("rows", c_uint32), ("cols", c_uint32), ("ld", c_uint32)]
 
@@ -148,6 +159,7 @@ SIGNATURES = {
     "bwpp_hip_plan_run": (c_int, [_P]),
     "bwpp_hip_plan_report": (c_size_t, [_P, c_char_p, c_size_t]),
     "bwpp_hip_dispatch_matmul": (c_int, [_P, _P, _P, _P, _P, MatmulParams]),
+    "bwpp_hip_dispatch_matmul_fused": (c_int, [_P, _P, _P, _P, _P, _P, _P, MatmulParams, FusionParams]),
     "bwpp_hip_dispatch_softmax": (c_int, [_P, _P, _P, SoftmaxParams]),
     "bwpp_hip_dispatch_rmsnorm": (c_int, [_P, _P, _P, _P, _P, RmsnormParams]),
     "bwpp_hip_dispatch_layernorm": (c_int, [_P, _P, _P, _P, _P, RmsnormParams]),
@@ -206,7 +218,7 @@ def load():
     return lib
 
 
-__all__ = ["Status", "DType", "Epilogue", "MatmulParams", "SoftmaxParams",
+__all__ = ["Status", "DType", "Epilogue", "MatmulParams", "Fusion", "FusionParams", "SoftmaxParams",
            "RmsnormParams", "AttentionParams", "ReduceParams", "ElementwiseParams", "Arena",
            "CoreDType", "Tensor",
            "SIGNATURES", "load", "LIB_PATH", "LIB_DIR", "HEADER_PATH",

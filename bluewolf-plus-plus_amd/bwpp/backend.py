@@ -110,6 +110,10 @@ class HipBackend:
         self._check(self.lib.bwpp_hip_dispatch_matmul(
             self._h, _ptr(a), _ptr(b), _ptr(c), _ptr(bias), params))
 
+    def dispatch_matmul_fused(self, a, b, c, bias, aux, c2, params: MatmulParams, fusion):
+        self._check(self.lib.bwpp_hip_dispatch_matmul_fused(
+            self._h, _ptr(a), _ptr(b), _ptr(c), _ptr(bias), _ptr(aux), _ptr(c2), params, fusion))
+
     def dispatch_softmax(self, x, y, params: SoftmaxParams):
         self._check(self.lib.bwpp_hip_dispatch_softmax(
             self._h, _ptr(x), _ptr(y), params))

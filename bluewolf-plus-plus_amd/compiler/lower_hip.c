@@ -1226,8 +1226,81 @@ static void lower_matmul(Ctx *c, GCtx *gc, uint32_t node, const uint8_t *needed)
       last = c1->output;
     }
   }
+  /* fp32 tails fused after the epilogue (BWPP_HIP_FUSE_*):
+   *   residual   the result's only reader adds a full matrix already computed
+   *   dual_silu  SiLU of the result where the result itself is also needed
+   *              (the backward's silu_grad reads it)
+   *   silu_grad  the result is the dY of silu_grad(x, dY) (autodiff graph) */
+  const char *fuse = "none";
+  int aux = -1, c2v = -1;
+  if (!A->bf16 && gc->ncons[last] == 1 && !gc->skip[gc->cons[last][0]] && c->opt->fuse_tails) {
+    const uint32_t cn = gc->cons[last][0];
+    const BwppGraphNode *c1 = &g->nodes[cn];
+    if (c1->op == BWPP_GOP_ADD && c1->input_count == 2 && !is_needed(needed, gc, last)) {
+      const uint32_t r = c1->inputs[0] == last ? c1->inputs[1] : c1->inputs[0];
+      const LVal *R = &gc->lv[r];
+      if (r != last && R->known && R->pv >= 0 && !R->trans && !R->bcast && !R->bf16 && R->shape.rank >= 1 &&
+          shape_elems(&R->shape) == o.n[0] * o.n[1] && R->shape.n[R->shape.rank - 1] == o.n[1]) {
+        fuse = "residual";
+        aux = (int)r;
+        gc->skip[cn] = 1;
+        gc->lv[last].fused = 1;
+        last = c1->output;
+      }
+    } else if (c1->op == BWPP_GOP_SILU && !gc->is_grad && strcmp(epi, "silu") && strcmp(epi, "add_silu")) {
+      fuse = "dual_silu";
+      c2v = (int)c1->output;
+      gc->skip[cn] = 1;
+    } else if (c1->op == BWPP_GOP_SILU_GRAD && c1->input_count >= 2 && c1->inputs[1] == last &&
+               c1->inputs[0] != last && !strcmp(epi, "none") && !is_needed(needed, gc, last)) {
+      const LVal *X = &gc->lv[c1->inputs[0]];
+      if (X->known && X->pv >= 0 && !X->trans && !X->bcast && !X->bf16 &&
+          shape_elems(&X->shape) == o.n[0] * o.n[1] && X->shape.n[X->shape.rank - 1] == o.n[1]) {
+        fuse = "silu_grad";
+        aux = (int)c1->inputs[0];
+        gc->skip[cn] = 1;
+        gc->lv[last].fused = 1;
+        last = c1->output;
+      }
+    }
+  }
   const Ref ar = ref(A->pv), br = ref(B->pv);
   char extra[64] = "";
+  if (strcmp(fuse, "none")) {
+    LVal *out = &gc->lv[last];
+    out->shape = o;
+    out->known = 1;
+    out->bf16 = 0;
+    assign_pv(c, gc, last, "t");
+    char ins[160], outs[96];
+    snprintf(ins, sizeof ins, "%s,%s", ar.s, br.s);
+    if (bias >= 0) {
+      strcat(ins, ",");
+      strcat(ins, ref(gc->lv[bias].pv).s);
+    }
+    if (aux >= 0) {
+      strcat(ins, ",");
+      strcat(ins, ref(gc->lv[aux].pv).s);
+    }
+    snprintf(outs, sizeof outs, "%s", ref(out->pv).s);
+    if (c2v >= 0) {
+      LVal *o2 = &gc->lv[c2v];
+      o2->shape = o;
+      o2->known = 1;
+      o2->bf16 = 0;
+      assign_pv(c, gc, (uint32_t)c2v, "t");
+      strcat(outs, ",");
+      strcat(outs, ref(o2->pv).s);
+    }
+    if (A->trans) strcat(extra, " ta=1");
+    if (B->trans) strcat(extra, " tb=1");
+    if (strcmp(epi, "none")) {
+      strcat(extra, " epi=");
+      strcat(extra, epi);
+    }
+    emit(c, "op matmul out=%s in=%s%s fuse=%s\n", outs, ins, extra, fuse);
+    return;
+  }
   if (!strcmp(epi, "none") && gc->ncons[last] == 1 && !is_needed(needed, gc, last) &&
       !gc->skip[gc->cons[last][0]] && g->nodes[gc->cons[last][0]].op == BWPP_GOP_TRANSPOSE) {
     /* Only read transposed: compute C^T = B^T A^T, so the transpose that
@@ -1542,6 +1615,7 @@ void bwpp_lower_options_init(BwppLowerOptions *opt) {
   opt->f16_as = BWPP_DTYPE_F32;
   opt->fuse_attention = 1;
   opt->group_gemms = 1;
+  opt->fuse_tails = 1;
 }
 
 static void render(Ctx *c, FILE *out) {

@@ -22,6 +22,9 @@
  *   - rmsnorm_grad plus the graph's dGamma chain (div / mul / reduce_sum,
  *     graph_ir.c:1747-1781) become one rmsnorm_grad launch with two
  *     outputs;
+ *   - in fp32, the add of a full matrix to a matmul result, SiLU of a
+ *     result the backward also reads (both written), and silu_grad whose
+ *     dY is a matmul result fuse into that GEMM's tail;
  *   - matmuls that share their left operand and take weights of one shape
  *     (q, k, v projections) run as one GEMM against the weights' column
  *     concatenation, their results column views; in training their weight
@@ -81,6 +84,9 @@ typedef struct {
                          one shape, run as one GEMM against the weights'
                          column concatenation (and so do their dW and dA
                          terms in training); 0: one GEMM each */
+  int fuse_tails;     /* fp32 GEMM tails: a residual add of the result, SiLU
+                         of a result the backward also reads (both written),
+                         silu_grad whose dY is the result; 0: separate ops */
   /* payloads of the graph's valueless numeric literals, in value order */
   float const_values[BWPP_LOWER_MAX_CONSTS];
   uint32_t const_count;

@@ -48,6 +48,13 @@ typedef struct {
   uint32_t ksplit;
   uint32_t kchunk;
   float *part;
+  /* fp32 fusions after the epilogue (BWPP_HIP_FUSE_*): residual C += aux,
+   * dual output c2 = SiLU(C), SiLU gradient C *= silu'(aux) */
+  uint32_t fuse;
+  uint32_t ldaux;
+  const float *aux;
+  float *c2;
+  uint32_t ldc2;
 } BwppGemmArgs;
 
 /* Attention: O = softmax(scale * Q K^T [causal]) V per (batch, head). */

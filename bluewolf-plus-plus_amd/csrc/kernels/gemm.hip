@@ -65,6 +65,24 @@ __device__ __forceinline__ float silu(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
 }
 
+// Fused tails of the fp32 kernels (BWPP_HIP_FUSE_*), applied to the
+// epilogue's result y of element (m, n): residual y + aux, SiLU gradient
+// y * s (1 + x (1 - s)) with x = aux (the form of grad.hip's silu_grad),
+// dual output c2 = SiLU(y) (written by the caller of this function).
+constexpr uint32_t kFuseResidual = 1u, kFuseDualSilu = 2u, kFuseSiluGrad = 3u;
+__device__ __forceinline__ float fuse1(uint32_t fuse, float y, float x) {
+  if (fuse == kFuseResidual) return y + x;
+  if (fuse == kFuseSiluGrad) {
+    const float s = 1.0f / (1.0f + __expf(-x));
+    return y * (s * (1.0f + x * (1.0f - s)));
+  }
+  return y;
+}
+__device__ __forceinline__ float4 fuse4(uint32_t fuse, float4 y, float4 x) {
+  return make_float4(fuse1(fuse, y.x, x.x), fuse1(fuse, y.y, x.y), fuse1(fuse, y.z, x.z), fuse1(fuse, y.w, x.w));
+}
+__device__ __forceinline__ bool fuse_reads_aux(uint32_t fuse) { return fuse == kFuseResidual || fuse == kFuseSiluGrad; }
+
 // ---------------------------------------------------------------- bf16
 
 __device__ __forceinline__ uint32_t dword(const uint4 &v, int d) {
@@ -827,19 +845,29 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
   __syncthreads();
   float *C = SPLIT ? a.part + (size_t)split * a.M * a.N : static_cast<float *>(a.c);
   const uint32_t ldc = SPLIT ? a.N : a.ldc;
+  const uint32_t fuse = SPLIT ? 0u : a.fuse;  // split-K: the reduce kernel fuses
   constexpr int kRowVecs = BN / 4;
 #pragma unroll 4
   for (int it = 0; it < BM * kRowVecs / NT; ++it) {
     const int q = tid + it * NT;
     const int row = q / kRowVecs, c = q % kRowVecs;
     const uint32_t m = m0 + row, n = n0 + c * 4;
-    const float4 v = *reinterpret_cast<const float4 *>(smemf + row * kCld + c * 4);
+    float4 v = *reinterpret_cast<const float4 *>(smemf + row * kCld + c * 4);
     if (!EDGE || (m < a.M && n + 4 <= a.N && vec)) {
+      if (fuse_reads_aux(fuse)) v = fuse4(fuse, v, *reinterpret_cast<const float4 *>(a.aux + (size_t)m * a.ldaux + n));
       *reinterpret_cast<float4 *>(C + (size_t)m * ldc + n) = v;
+      if (fuse == kFuseDualSilu)
+        *reinterpret_cast<float4 *>(a.c2 + (size_t)m * a.ldc2 + n) =
+            make_float4(silu(v.x), silu(v.y), silu(v.z), silu(v.w));
     } else if (m < a.M) {
       const float *h = smemf + row * kCld + c * 4;
       for (int e = 0; e < 4; ++e)
-        if (n + e < a.N) C[(size_t)m * ldc + n + e] = h[e];
+        if (n + e < a.N) {
+          float y = h[e];
+          if (fuse_reads_aux(fuse)) y = fuse1(fuse, y, a.aux[(size_t)m * a.ldaux + n + e]);
+          C[(size_t)m * ldc + n + e] = y;
+          if (fuse == kFuseDualSilu) a.c2[(size_t)m * a.ldc2 + n + e] = silu(y);
+        }
     }
   }
 }
@@ -847,8 +875,9 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
 }  // namespace
 
 // Split-K reduction: C[m][n..n+3] = epilogue(sum_s part[s][m][n..n+3]) in
-// split order, then bias and SiLU as the single-pass epilogue.  Needs N a
-// multiple of 4 and 16-byte aligned C rows (the full-tile conditions).
+// split order, then bias and SiLU as the single-pass epilogue, then the
+// fused tail.  Needs N a multiple of 4 and 16-byte aligned C (and aux, c2)
+// rows (the full-tile conditions).
 extern "C" __global__ __launch_bounds__(256) void bwpp_gemm_f32_splitk_reduce(const BwppGemmArgs a) {
   const uint32_t nv = a.N / 4;
   const size_t total = (size_t)a.M * nv, plane = (size_t)a.M * a.N;
@@ -879,7 +908,10 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_gemm_f32_splitk_reduce(co
       t.z = silu(t.z);
       t.w = silu(t.w);
     }
+    if (fuse_reads_aux(a.fuse)) t = fuse4(a.fuse, t, *reinterpret_cast<const float4 *>(a.aux + (size_t)m * a.ldaux + n));
     *reinterpret_cast<float4 *>(C + (size_t)m * a.ldc + n) = t;
+    if (a.fuse == kFuseDualSilu)
+      *reinterpret_cast<float4 *>(a.c2 + (size_t)m * a.ldc2 + n) = make_float4(silu(t.x), silu(t.y), silu(t.z), silu(t.w));
   }
 }
 

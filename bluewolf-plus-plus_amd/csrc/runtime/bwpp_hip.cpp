@@ -675,8 +675,10 @@ BwppHipStatus ensure_ws(BwppHip *h, size_t bytes);
 
 }  // namespace
 
-extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, const void *b, void *c,
-                                                  const void *bias, BwppMatmulParams p) {
+namespace {
+
+BwppHipStatus matmul_impl(BwppHip *h, const void *a, const void *b, void *c, const void *bias, BwppMatmulParams p,
+                          const float *aux, float *c2, BwppHipFusionParams fz) {
   BwppHipStatus s = enter(h);
   if (s != BWPP_HIP_OK) return s;
   if (!a || !b || !c) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "matmul: NULL a, b or c");
@@ -699,6 +701,28 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
   const Extent ebias = use_bias ? extent(bias, 1, p.N, p.N, es) : Extent{};
   if (overlaps(ec, ea) || overlaps(ec, eb) || overlaps(ec, ebias))
     return fail(h, BWPP_HIP_ERR_ALIAS, "matmul: C overlaps A, B or bias");
+  // Fused tail: fp32 only; aux (residual / SiLU input) and c2 (dual output).
+  const uint32_t fuse = fz.kind;
+  const bool use_aux = fuse == BWPP_HIP_FUSE_RESIDUAL || fuse == BWPP_HIP_FUSE_SILU_GRAD;
+  const uint32_t ldaux = fz.ld_aux ? fz.ld_aux : p.N, ldc2 = fz.ld_c2 ? fz.ld_c2 : p.N;
+  if (fuse != BWPP_HIP_FUSE_NONE) {
+    if (fuse > BWPP_HIP_FUSE_SILU_GRAD) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "matmul: unknown fusion %u", fuse);
+    if (bf16) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "matmul: fused tails run on fp32 only");
+    if (use_aux && (!aux || ldaux < p.N)) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "matmul: fusion needs aux (ld >= N)");
+    if (fuse == BWPP_HIP_FUSE_DUAL_SILU && (!c2 || ldc2 < p.N))
+      return fail(h, BWPP_HIP_ERR_INVALID_ARG, "matmul: dual output needs c2 (ld >= N)");
+    if (fuse == BWPP_HIP_FUSE_DUAL_SILU && (p.epilogue & BWPP_HIP_EPILOGUE_SILU))
+      return fail(h, BWPP_HIP_ERR_INVALID_ARG, "matmul: the dual output takes SiLU of a result without SiLU");
+    if (fuse == BWPP_HIP_FUSE_SILU_GRAD && p.epilogue != BWPP_HIP_EPILOGUE_NONE)
+      return fail(h, BWPP_HIP_ERR_INVALID_ARG, "matmul: the SiLU gradient tail takes no epilogue");
+    const Extent eaux = use_aux ? extent(aux, p.M, p.N, ldaux, 4) : Extent{};
+    const Extent ec2 = fuse == BWPP_HIP_FUSE_DUAL_SILU ? extent(c2, p.M, p.N, ldc2, 4) : Extent{};
+    // aux may be C itself (each element is read and written by one thread)
+    const bool aux_is_c = use_aux && (const void *)aux == c && ldaux == ldc;
+    if ((use_aux && !aux_is_c && overlaps(ec, eaux)) || overlaps(ec2, ea) || overlaps(ec2, eb) ||
+        overlaps(ec2, ebias) || overlaps(ec2, ec) || overlaps(ec2, eaux))
+      return fail(h, BWPP_HIP_ERR_ALIAS, "matmul: c2 or aux overlaps another operand");
+  }
 
   // Full-tile kernels: bf16 256 x 256 with K in steps of 32 (pipelined),
   // fp32 128 x 128 with K in steps of 32; anything else takes the guarded
@@ -706,7 +730,8 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
   const uint32_t BM = bf16 ? 256 : 128, BN = bf16 ? 256 : 128, BK = 32;
   const uint32_t vecw = bf16 ? 8 : 4;  // elements per 16 bytes
   const bool vec = aligned16(a) && aligned16(b) && aligned16(c) && lda % vecw == 0 && ldb % vecw == 0 &&
-                   ldc % vecw == 0;
+                   ldc % vecw == 0 && (!use_aux || (aligned16(aux) && ldaux % 4 == 0)) &&
+                   (fuse != BWPP_HIP_FUSE_DUAL_SILU || (aligned16(c2) && ldc2 % 4 == 0));
   // The full-tile kernels also fetch the bias row with 16-byte copies.
   const bool full = vec && (!use_bias || aligned16(bias)) && p.M % BM == 0 && p.N % BN == 0 && p.K % BK == 0;
   BwppGemmArgs g = {};
@@ -725,6 +750,11 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
   g.tiles_n = (p.N + BN - 1) / BN;
   g.group_m = h->gemm_group_m;
   g.vec_ok = vec ? 1u : 0u;
+  g.fuse = fuse;
+  g.aux = use_aux ? aux : nullptr;
+  g.ldaux = ldaux;
+  g.c2 = fuse == BWPP_HIP_FUSE_DUAL_SILU ? c2 : nullptr;
+  g.ldc2 = ldc2;
   const uint64_t tiles = (uint64_t)g.tiles_m * g.tiles_n;
   if (tiles > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "matmul: too many tiles");
   if (bf16 && full && h->gemm_waves == 8)
@@ -773,6 +803,19 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, con
     }
   }
   return launch(h, h->gemm[bf16 ? 1 : 0][ta][tb][full ? 1 : 0], (uint32_t)tiles, 1, 1, 256, g);
+}
+
+}  // namespace
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a, const void *b, void *c,
+                                                  const void *bias, BwppMatmulParams p) {
+  return matmul_impl(h, a, b, c, bias, p, nullptr, nullptr, BwppHipFusionParams{});
+}
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_matmul_fused(BwppHip *h, const void *a, const void *b, void *c,
+                                                        const void *bias, const float *aux, float *c2,
+                                                        BwppMatmulParams p, BwppHipFusionParams f) {
+  return matmul_impl(h, a, b, c, bias, p, aux, c2, f);
 }
 
 namespace {

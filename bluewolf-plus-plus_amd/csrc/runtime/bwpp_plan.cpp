@@ -16,7 +16,7 @@
 //   value NAME f32 [EXPR,...] KIND    KIND: input | param | temp | output | const=<float>
 //   view NAME of=BASE offset=EXPR ld=EXPR shape=[EXPR,EXPR]
 //   op KIND out=A[,B..] in=X[,Y..] [key=value ...]
-// Op kinds: matmul (ta, tb, epi), softmax, rmsnorm, layernorm,
+// Op kinds: matmul (ta, tb, epi, fuse), softmax, rmsnorm, layernorm,
 // add / sub / mul / div / copy / silu (bcast), reduce_sum, reduce_max,
 // reduce_max_mask (axis), silu_grad, softmax_grad, rmsnorm_grad,
 // attention, attention_grad (batch, heads, causal, scale, layout).
@@ -525,7 +525,7 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
     }
   }
   if (k == "matmul") {
-    if (!need(2, 1)) return bad("in=A,B[,bias] out=C");
+    if (op.ins.size() < 2 || op.outs.empty()) return bad("in=A,B[,bias][,aux] out=C[,C2]");
     const Value &A = val(op.ins[0]), &B = val(op.ins[1]), &C = val(op.outs[0]);
     const uint32_t ta = (uint32_t)num("ta", 0), tb = (uint32_t)num("tb", 0);
     const uint64_t M = C.rows(), N = C.cols();
@@ -539,8 +539,34 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
                    : e == "add_silu" ? BWPP_HIP_EPILOGUE_ADD_SILU : BWPP_HIP_EPILOGUE_NONE;
     BwppMatmulParams mp = {(uint32_t)M, (uint32_t)N, (uint32_t)K, (uint32_t)A.row_stride(), (uint32_t)B.row_stride(),
                            (uint32_t)C.row_stride(), C.dtype, epi, ta, tb};
-    s = BWPP_PLAN_CALL(bwpp_hip_dispatch_matmul(h, ptr(op.ins[0]), ptr(op.ins[1]), ptr(op.outs[0]),
-                                 op.ins.size() > 2 ? ptr(op.ins[2]) : nullptr, mp));
+    // fuse=residual (C = epi(A.B) + aux), dual_silu (out=C,C2 with C2 =
+    // SiLU(C)), silu_grad (C = A.B * silu'(aux)): the inputs are then
+    // A, B, the bias when epi adds one, and aux.
+    const std::string fz = attr(op, "fuse", "none");
+    if (fz != "none" && fz != "residual" && fz != "dual_silu" && fz != "silu_grad")
+      return bad("fuse must be none, residual, dual_silu or silu_grad");
+    if (fz == "none") {
+      if (op.ins.size() > 3 || op.outs.size() != 1) return bad("in=A,B[,bias] out=C");
+      s = BWPP_PLAN_CALL(bwpp_hip_dispatch_matmul(h, ptr(op.ins[0]), ptr(op.ins[1]), ptr(op.outs[0]),
+                                                  op.ins.size() > 2 ? ptr(op.ins[2]) : nullptr, mp));
+    } else {
+      BwppHipFusionParams fp = {};
+      fp.kind = fz == "residual" ? BWPP_HIP_FUSE_RESIDUAL : fz == "dual_silu" ? BWPP_HIP_FUSE_DUAL_SILU
+                                                                            : BWPP_HIP_FUSE_SILU_GRAD;
+      const bool has_bias = (epi & BWPP_HIP_EPILOGUE_ADD) != 0, has_aux = fz != "dual_silu";
+      const size_t nin = 2 + (has_bias ? 1 : 0) + (has_aux ? 1 : 0), nout = fz == "dual_silu" ? 2 : 1;
+      if (op.ins.size() != nin || op.outs.size() != nout)
+        return bad("fused matmul: in=A,B[,bias],aux (residual, silu_grad) or in=A,B[,bias] out=C,C2 (dual_silu)");
+      const int ai = has_aux ? op.ins[nin - 1] : -1, c2i = nout == 2 ? op.outs[1] : -1;
+      if (ai >= 0 && (val(ai).rows() != M || val(ai).cols() != N)) return bad("aux must have C's shape");
+      if (c2i >= 0 && (val(c2i).rows() != M || val(c2i).cols() != N)) return bad("C2 must have C's shape");
+      fp.ld_aux = ai >= 0 ? (uint32_t)val(ai).row_stride() : 0u;
+      fp.ld_c2 = c2i >= 0 ? (uint32_t)val(c2i).row_stride() : 0u;
+      s = BWPP_PLAN_CALL(bwpp_hip_dispatch_matmul_fused(h, ptr(op.ins[0]), ptr(op.ins[1]), ptr(op.outs[0]),
+                                                        has_bias ? ptr(op.ins[2]) : nullptr,
+                                                        ai >= 0 ? f32(ai) : nullptr, c2i >= 0 ? f32(c2i) : nullptr,
+                                                        mp, fp));
+    }
   } else if (k == "softmax" || k == "rmsnorm" || k == "layernorm") {
     if (!need(1, 1)) return bad("in=X[,gamma[,beta]] out=Y");
     const Value &X = val(op.ins[0]);

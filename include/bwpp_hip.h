@@ -312,6 +312,38 @@ BwppHipStatus bwpp_hip_dispatch_matmul(BwppHip *h, const void *a,
                                        const void *bias,
                                        BwppMatmulParams params);
 
+/* Matmul with a fused elementwise tail (no reference counterpart: the
+ * HIP lowering's fusions of the graph's add / silu / silu_grad nodes into
+ * the GEMM that feeds them).  fp32 only (dtype F32, else UNSUPPORTED).
+ * After the params' bias / SiLU epilogue, with Y = that result:
+ *   RESIDUAL   C = Y + aux        (aux [M x N], row stride ld_aux; aux may
+ *                                  be C itself, with ld_aux = ldc)
+ *   DUAL_SILU  C = Y, c2 = SiLU(Y) (c2 [M x N], row stride ld_c2; the
+ *                                  params' epilogue may not include SiLU)
+ *   SILU_GRAD  C = Y * s (1 + x (1 - s)), x = aux, s = 1 / (1 + e^-x)
+ *                                 (the graph's silu_grad with Y as dY;
+ *                                  epilogue must be NONE)
+ * NONE is bwpp_hip_dispatch_matmul. */
+typedef enum {
+  BWPP_HIP_FUSE_NONE = 0,
+  BWPP_HIP_FUSE_RESIDUAL = 1,
+  BWPP_HIP_FUSE_DUAL_SILU = 2,
+  BWPP_HIP_FUSE_SILU_GRAD = 3
+} BwppHipFusion;
+
+typedef struct {
+  uint32_t kind;   /* BwppHipFusion */
+  uint32_t ld_aux; /* 0 = N */
+  uint32_t ld_c2;  /* 0 = N */
+} BwppHipFusionParams;
+
+BwppHipStatus bwpp_hip_dispatch_matmul_fused(BwppHip *h, const void *a,
+                                             const void *b, void *c,
+                                             const void *bias,
+                                             const float *aux, float *c2,
+                                             BwppMatmulParams params,
+                                             BwppHipFusionParams fusion);
+
 /* bwpp_metal_dispatch_softmax (dispatch_stub.h:51-56); CPU twin
  * bwpp_cpu_softmax_f32 (bwpp_cpu_ref.c:37-61).  y may equal x. */
 BwppHipStatus bwpp_hip_dispatch_softmax(BwppHip *h, const float *x, float *y,

@@ -164,9 +164,21 @@ class CpuPlan:
         if k == "matmul":
             ta, tb = int(kv.get("ta", 0)), int(kv.get("tb", 0))
             epi = kv.get("epi", "none")
-            bias = X[2].reshape(-1) if len(X) > 2 else None
+            fuse = kv.get("fuse", "none")
+            has_bias = epi in ("add", "add_silu") if fuse != "none" else len(X) > 2
+            bias = X[2].reshape(-1) if has_bias else None
             r = o.matmul(X[0], X[1], bias, apply_silu=epi in ("silu", "add_silu"),
                          apply_bias=epi in ("add", "add_silu"), trans_a=bool(ta), trans_b=bool(tb))
+            # fused tails, each the separate op it replaces
+            if fuse == "residual":
+                r = np.add(r, X[-1], dtype=np.float32)
+            elif fuse == "silu_grad":
+                r = o.silu_grad(np.ascontiguousarray(X[-1]), r).reshape(r.shape)
+            elif fuse == "dual_silu":
+                with np.errstate(all="ignore"):
+                    m(outs[1])[...] = (r / (np.float32(1) + np.exp(-r))).astype(np.float32)
+            elif fuse != "none":
+                raise PlanTextError(f"unknown fuse '{fuse}'")
             m(outs[0])[...] = r
         elif k == "softmax":
             m(outs[0])[...] = o.softmax(np.ascontiguousarray(X[0]))

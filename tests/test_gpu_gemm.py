@@ -279,3 +279,63 @@ def test_f32_split_k_repeatable(be):
                 first[i] = c.clone()
             else:
                 assert torch.equal(c, first[i]), (rep, shapes[i])
+
+
+# ------------------------------------------------------------ fused tails
+@pytest.mark.parametrize("M,N,K", [(100, 70, 50), (256, 256, 128), (256, 128, 4096), (384, 256, 64)])
+@pytest.mark.parametrize("kind", [1, 2, 3])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_fused_tails_f32(be, oracle, M, N, K, kind, with_bias):
+    """bwpp_hip_dispatch_matmul_fused against the oracle's matmul followed
+    by the op each tail replaces: residual add (bit-exact with the GEMM's
+    own result: one fp32 rounding), SiLU gradient (the oracle's
+    silu_grad), dual SiLU output.  Edge tiles (100 x 70), full tiles,
+    split-K (K 4096 over 2 tiles) and an uneven tile count."""
+    torch = _torch()
+    if kind == 3 and with_bias:
+        pytest.skip("the SiLU-gradient tail takes no epilogue")
+    a = synth.uniform((M, K), M + kind, 0, -1.0, 1.0)
+    b = synth.uniform((K, N), N + kind, 1, -1.0, 1.0)
+    bias = synth.uniform((N,), 3, 2, -1.0, 1.0)
+    aux = synth.normal((M, N), 4, 3)
+    epi = 1 if with_bias else 0
+    want = oracle.matmul(a, b, bias if with_bias else None, apply_silu=False, apply_bias=with_bias)
+    c = torch.full((M, N), 7.0, device="cuda")
+    c2 = torch.full((M, N), 7.0, device="cuda")
+    auxd = f32_dev(aux)
+    be.dispatch_matmul_fused(f32_dev(a), f32_dev(b), c, f32_dev(bias) if with_bias else None,
+                             auxd if kind != 2 else None, c2 if kind == 2 else None,
+                             bwpp.MatmulParams(M, N, K, 0, 0, N, 0, epi, 0, 0), bwpp.FusionParams(kind, N, N))
+    got = f32_host(c)
+    if kind == 1:
+        assert rel_max_err(got, np.add(want, aux, dtype=np.float32)) <= F32_TOL
+    elif kind == 3:
+        assert rel_max_err(got, oracle.silu_grad(aux, want).reshape(M, N)) <= F32_TOL
+    else:
+        assert rel_max_err(got, want) <= F32_TOL
+        wd = want.astype(np.float64)
+        assert rel_max_err(f32_host(c2), wd / (1.0 + np.exp(-wd))) <= F32_TOL
+
+
+def test_fused_tails_errors(be):
+    torch = _torch()
+    x = torch.zeros((64, 64), device="cuda")
+    y = torch.zeros((64, 64), device="cuda")
+    p = bwpp.MatmulParams(64, 64, 64, 0, 0, 64, 0, 0, 0, 0)
+    with pytest.raises(bwpp.BwppError):  # residual without aux
+        be.dispatch_matmul_fused(x, x, y, None, None, None, p, bwpp.FusionParams(1, 0, 0))
+    with pytest.raises(bwpp.BwppError):  # dual output without c2
+        be.dispatch_matmul_fused(x, x, y, None, None, None, p, bwpp.FusionParams(2, 0, 0))
+    with pytest.raises(bwpp.BwppError):  # c2 is C
+        be.dispatch_matmul_fused(x, x, y, None, None, y, p, bwpp.FusionParams(2, 0, 0))
+    with pytest.raises(bwpp.BwppError):  # SiLU-gradient tail after an epilogue
+        be.dispatch_matmul_fused(x, x, y, x[0], x, None, bwpp.MatmulParams(64, 64, 64, 0, 0, 64, 0, 1, 0, 0),
+                                 bwpp.FusionParams(3, 0, 0))
+    with pytest.raises(bwpp.BwppError):  # bf16
+        be.dispatch_matmul_fused(x, x, y, None, x, None, bwpp.MatmulParams(64, 64, 64, 0, 0, 64, 1, 0, 0, 0),
+                                 bwpp.FusionParams(1, 0, 0))
+    # residual in place (aux is C): C = A.B + C
+    a = torch.eye(64, device="cuda")
+    c = torch.full((64, 64), 2.0, device="cuda")
+    be.dispatch_matmul_fused(a, a, c, None, c, None, p, bwpp.FusionParams(1, 64, 0))
+    assert np.array_equal(f32_host(c), np.eye(64, dtype=np.float32) + 2.0)

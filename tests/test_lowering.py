@@ -199,6 +199,35 @@ def test_grouped_projections_match_separate_gemms(bwppc, tmp_path):
 
 
 @needs_reference
+def test_fused_tails_match_separate_ops(bwppc, tmp_path):
+    """x1 = x + ctx @ wo and out = x1 + h @ w2 (residual tails), h =
+    silu(n2 @ w1) with the pre-activation kept for the backward (dual
+    output) and silu_grad(t, dO @ w2^T) (SiLU-gradient tail) give the same
+    step as the separate ops."""
+    from blockref import block_inputs
+    src = os.path.join(REFERENCE, "examples", "tiny_model.bwpp")
+    B, T, D, H, HEADS = 2, 32, 48, 96, 3
+    dims = ["--entry", "block", "--dim", f"T={T}", "--dim", f"D={D}", "--dim", f"H={H}", "--batch", str(B),
+            "--heads", str(HEADS), "--causal", "--attn-scale", "auto", "--train", "mean_square"]
+    fused = lower(bwppc, src, tmp_path, *dims)
+    plain = lower(bwppc, src, tmp_path, *dims, "--no-fuse-tails")
+    for f in ("fuse=residual", "fuse=dual_silu", "fuse=silu_grad"):
+        assert f in fused and f not in plain
+    n_ops = lambda t: sum(l.startswith("op ") for l in t.splitlines())
+    assert n_ops(plain) - n_ops(fused) == 4  # two adds, silu, silu_grad
+    t = block_inputs(B, T, D, H, seed=12)
+    runs = []
+    for text in (fused, plain):
+        cp = CpuPlan(text)
+        for k, v in t.items():
+            cp.bind(k, v)
+        cp.run()
+        runs.append(cp)
+    for name in ("out", "loss", "dx", "dwq", "dwk", "dwv", "dwo", "dw1", "dw2", "dg1", "dg2"):
+        assert rel_max_err(runs[0].get(name), runs[1].get(name)) <= 1e-5, name
+
+
+@needs_reference
 def test_literal_values_must_be_supplied(bwppc, tmp_path):
     src = os.path.join(FIXTURES, "scaled.bwpp")
     err = lower(bwppc, src, tmp_path, "--dim", "M=4", "--dim", "N=8", ok=False)
