@@ -309,10 +309,11 @@ def pmc_summary(dirs):
     return "\n".join(lines)
 
 
-def stream_ceiling(torch, nbuf=3, reps=20):
-    """The box's read+write HBM ceiling for the C2 byte pattern: the best
-    GB/s of plain non-temporal 128-bit copies of X[8192 x 4096] fp32 (the
-    bytes one row operator moves), over float4-per-thread x block x grid
+def stream_ceiling(torch, nbuf=3, reps=20, kind="copy"):
+    """The box's HBM ceiling for the C2 byte pattern: the best GB/s of
+    plain non-temporal 128-bit copies of X[8192 x 4096] fp32 (the bytes one
+    read+write row operator moves; kind "read": the same loads without
+    stores, reduce_max's pattern), over float4-per-thread x block x grid
     (tests/hip/stream.hip, loaded through HIP's module API), each timed as
     the median of groups of back-to-back launches over `nbuf` rotating
     buffer pairs."""
@@ -337,7 +338,7 @@ def stream_ceiling(torch, nbuf=3, reps=20):
     best = None
     for v in (1, 2, 4, 8):
         fn = ctypes.c_void_p()
-        if hip.hipModuleGetFunction(ctypes.byref(fn), mod, f"bwpp_stream_copy_v{v}".encode()) != 0:
+        if hip.hipModuleGetFunction(ctypes.byref(fn), mod, f"bwpp_stream_{kind}_v{v}".encode()) != 0:
             continue
         for block in (256, 512, 1024):
             full = (n16 + block * v - 1) // (block * v)
@@ -357,13 +358,13 @@ def stream_ceiling(torch, nbuf=3, reps=20):
                     launch(i)
                 t = _launch_times_ms(torch, launch, reps, group=10)
                 us = float(np.median(t)) * 1e3
-                gbs = 2 * ROWS * COLS * F / us / 1e3
+                gbs = (2 if kind == "copy" else 1) * ROWS * COLS * F / us / 1e3
                 if best is None or gbs > best["GB_s"]:
                     best = {"GB_s": round(gbs, 1), "us_per_launch": round(us, 2), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                             "config": {"float4_per_thread": v, "block": block, "grid": grid}}
     torch.cuda.synchronize()
     hip.hipModuleUnload(mod)
-    best["kernel"] = "tests/hip/stream.hip bwpp_stream_copy_v*"
+    best["kernel"] = f"tests/hip/stream.hip bwpp_stream_{kind}_v*"
     return best
 
 
@@ -800,10 +801,15 @@ def main():
         "host": host_info(),
     }
     ceil = stream_ceiling(torch)
+    rceil = stream_ceiling(torch, kind="read")
     if ceil:
         out["stream_ceiling"] = ceil
-        for op in ops.values():
-            op["frac_of_stream_ceiling"] = round(op["GB_s"] / ceil["GB_s"], 4)
+        if rceil:
+            out["read_ceiling"] = rceil
+        for name, op in ops.items():
+            # reduce_max reads X and writes 64 KB: its ceiling is the read stream
+            c = rceil if (name == "reduce_max" and rceil) else ceil
+            op["frac_of_stream_ceiling"] = round(op["GB_s"] / c["GB_s"], 4)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_c2(args.seed, args.cpu_reps)
     else:

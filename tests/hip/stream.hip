@@ -1,11 +1,12 @@
-// Read+write stream kernels for measuring this box's HBM copy ceiling (the
-// roofline the row operators are held against).  Test/measurement code:
+// Stream kernels for measuring this box's HBM copy and read ceilings (the
+// rooflines the row operators are held against).  Test/measurement code:
 // built by tests/hip/Makefile, never loaded by the runtime.
 //
 // bwpp_stream_copy_v<V>: y[i] = x[i] over n float4, each thread moving V
 // float4 per trip of a grid-stride loop (non-temporal 128-bit loads and
 // stores, the access the row kernels use), all V loads issued before the
-// stores.  Every index is checked against n.
+// stores; bwpp_stream_read_v<V>: the same loads, no stores.  Every index is
+// checked against n.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -36,9 +37,32 @@ __device__ __forceinline__ void stream_copy(const StreamArgs &a) {
   }
 }
 
+// Read-only stream (the ceiling of reduce_max, which reads X and writes a
+// few KB): the loads are summed per thread, and the sum is stored only if
+// it equals a value N(0,1) data never sums to, so nothing is written in
+// practice while the loads stay live.  The store index is below n.
+template <int V>
+__device__ __forceinline__ void stream_read(const StreamArgs &a) {
+  const uint64_t nt = (uint64_t)gridDim.x * blockDim.x;
+  const uint64_t step = nt * V;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint64_t base = (uint64_t)blockIdx.x * blockDim.x * V + threadIdx.x; base < a.n; base += step) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const uint64_t i = base + (uint64_t)j * blockDim.x;
+      if (i < a.n) acc += __builtin_nontemporal_load(a.x + i);
+    }
+  }
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (acc.x == 1.0e30f && t < a.n) a.y[t] = acc;
+}
+
 #define STREAM(V)                                                                         \
   extern "C" __global__ __launch_bounds__(1024) void bwpp_stream_copy_v##V(StreamArgs a) { \
     stream_copy<V>(a);                                                                    \
+  }                                                                                       \
+  extern "C" __global__ __launch_bounds__(1024) void bwpp_stream_read_v##V(StreamArgs a) { \
+    stream_read<V>(a);                                                                    \
   }
 STREAM(1)
 STREAM(2)
