@@ -489,9 +489,12 @@ def _bf16(torch, x):
     return torch.from_numpy(synth.to_bf16_bits(x).view(np.int16)).cuda().view(torch.bfloat16)
 
 
-def extras(be, torch, seed, iters, with_cpu, warm_ms=WARM_MS):
-    """Contraction configs C3, C3-fp32, C4 (both masks), the C4-shape
-    attention backward, C1 and C5."""
+EXTRA_GROUPS = ("c3", "c3f32", "c4", "c5")
+
+
+def extras(be, torch, seed, iters, with_cpu, warm_ms=WARM_MS, only=EXTRA_GROUPS):
+    """Contraction configs C3, C3-fp32 (with C1), C4 (both masks, and the
+    C4-shape attention backward) and C5; `only` selects groups."""
     import bwpp
     from bwpp import synth
     global _WARM_MS
@@ -502,7 +505,20 @@ def extras(be, torch, seed, iters, with_cpu, warm_ms=WARM_MS):
         sys.path.insert(0, ROOT)
         from oracle.oracle import Oracle
         orc = Oracle()
+    if "c3" in only:
+        _extras_c3(be, torch, seed, iters, orc, out)
+    if "c3f32" in only:
+        _extras_c3f32(be, torch, seed, iters, orc, out)
+    if "c4" in only:
+        _extras_c4(be, torch, seed, iters, orc, out)
+    if "c5" in only:
+        out["c5_block_train_f32"] = block_train(be, torch, seed, max(3, iters // 4), with_cpu=orc is not None)
+    return out
 
+
+def _extras_c3(be, torch, seed, iters, orc, out):
+    import bwpp
+    from bwpp import synth
     # C3: Y = SiLU(X W + b), bf16 ~ N(0, 0.02), fp32 accumulation
     M, K, N = 4096, 4096, 11008
     xh = synth.normal((M, K), seed, 0, 0.0, 0.02)
@@ -527,8 +543,11 @@ def extras(be, torch, seed, iters, with_cpu, warm_ms=WARM_MS):
         c3["cpu"] = {"GFLOP_s": round(2.0 * rows * N * K / dt / 1e9, 3), "cores": 1, "kind": "port",
                      "sample": f"first {rows} rows (exact rows; extrapolated rate)"}
     out["c3_gemm_bf16_bias_silu"] = c3
-    del x, w, y, xh, wh
 
+
+def _extras_c3f32(be, torch, seed, iters, orc, out):
+    import bwpp
+    from bwpp import synth
     # C3 fp32 variant: 2048^3, U[-1, 1]
     n = 2048
     xf = torch.from_numpy(synth.uniform((n, n), seed, 0, -1, 1)).cuda()
@@ -560,8 +579,11 @@ def extras(be, torch, seed, iters, with_cpu, warm_ms=WARM_MS):
     p = bwpp.MatmulParams(256, 256, 256, 256, 256, 256)
     us = _events_us(torch, lambda: be.dispatch_matmul(a1, b1, c1, None, p), iters)
     out["c1_gemm_f32_256"] = {"us_per_launch": round(us, 2), "TFLOP_s": round(2.0 * 256 ** 3 / us / 1e6, 2)}
-    del xf, wf, yf
 
+
+def _extras_c4(be, torch, seed, iters, orc, out):
+    import bwpp
+    from bwpp import synth
     # C4: attention B 8, H 32, S 2048, d 128, bf16 ~ N(0, 1)
     B, H, S, d = 8, 32, 2048, 128
     qh = synth.normal((B, H, S, d), seed, 0)
@@ -613,9 +635,6 @@ def extras(be, torch, seed, iters, with_cpu, warm_ms=WARM_MS):
             entry["cpu"] = {"GFLOP_s": round(fl / (B * H) / dt / 1e9, 3), "cores": 1, "kind": "port",
                             "sample": "one (batch, head) slice (extrapolated rate)"}
         out["c4_attention_grad_bf16" + ("_causal" if causal else "")] = entry
-    del q, k, v, o, dout, dq, dk, dv
-    out["c5_block_train_f32"] = block_train(be, torch, seed, max(3, iters // 4), with_cpu=orc is not None)
-    return out
 
 
 # FLOP of one C5 step: forward GEMMs 2*BT*D*(3D + D + 2F), backward twice
@@ -703,6 +722,8 @@ def main():
     ap.add_argument("--no-c2", action="store_true",
                     help="skip the C2 headline (with --no-extras off: time the contractions only)")
     ap.add_argument("--extras-iters", type=int, default=30, help="timed launches per contraction config")
+    ap.add_argument("--extras-only", default=",".join(EXTRA_GROUPS),
+                    help="comma list of contraction groups to run: " + ", ".join(EXTRA_GROUPS))
     ap.add_argument("--warm-ms", type=float, default=WARM_MS,
                     help="sustained work before each contraction is timed (0 for counter runs)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
@@ -742,10 +763,15 @@ def main():
         sys.exit(1)
     be = bwpp.HipBackend(0)
     be.set_stream(torch.cuda.current_stream())
+    only = tuple(g.strip() for g in args.extras_only.split(",") if g.strip())
+    bad = [g for g in only if g not in EXTRA_GROUPS]
+    if bad:
+        print(f"bench.py: unknown --extras-only group(s) {bad}; choose from {list(EXTRA_GROUPS)}", file=sys.stderr)
+        sys.exit(2)
 
     if args.no_c2:
         out = {"metric": METRIC, "config": {"workload": "contractions only (no headline)"},
-               "extras": extras(be, torch, args.seed, args.extras_iters, not args.no_cpu, args.warm_ms)}
+               "extras": extras(be, torch, args.seed, args.extras_iters, not args.no_cpu, args.warm_ms, only)}
         be.close()
         print(json.dumps(out))
         return
@@ -817,7 +843,7 @@ def main():
     del bench
     if not args.no_extras:
         torch.cuda.empty_cache()
-        out["extras"] = extras(be, torch, args.seed, args.extras_iters, not args.no_cpu, args.warm_ms)
+        out["extras"] = extras(be, torch, args.seed, args.extras_iters, not args.no_cpu, args.warm_ms, only)
     be.close()
     print(json.dumps(out))
 
