@@ -157,6 +157,8 @@ SIGNATURES = {
     "bwpp_hip_plan_bind": (c_int, [_P, c_char_p, _P]),
     "bwpp_hip_plan_value_ptr": (_P, [_P, c_char_p]),
     "bwpp_hip_plan_run": (c_int, [_P]),
+    "bwpp_hip_plan_capture": (c_int, [_P]),
+    "bwpp_hip_plan_replay": (c_int, [_P]),
     "bwpp_hip_plan_report": (c_size_t, [_P, c_char_p, c_size_t]),
     "bwpp_hip_dispatch_matmul": (c_int, [_P, _P, _P, _P, _P, MatmulParams]),
     "bwpp_hip_dispatch_matmul_fused": (c_int, [_P, _P, _P, _P, _P, _P, _P, MatmulParams, FusionParams]),

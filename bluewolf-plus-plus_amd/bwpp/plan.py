@@ -90,6 +90,14 @@ class Plan:
     def run(self):
         self._check(self.lib.bwpp_hip_plan_run(self._p))
 
+    def capture(self):
+        """Record one run as a HIP graph (the handle's stream must not be
+        the default stream); replay() launches it."""
+        self._check(self.lib.bwpp_hip_plan_capture(self._p))
+
+    def replay(self):
+        self._check(self.lib.bwpp_hip_plan_replay(self._p))
+
     def close(self):
         if getattr(self, "_p", None):
             self.lib.bwpp_hip_plan_destroy(self._p)

@@ -117,6 +117,9 @@ struct BwppHipPlan {
   bool allocated = false;
   bool check_only = false;  // run_op validates arguments and launches nothing
   std::string err;
+  // bwpp_hip_plan_capture: one run recorded as a HIP graph
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
 };
 
 namespace {
@@ -416,10 +419,62 @@ extern "C" BwppHipStatus bwpp_hip_plan_create(BwppHip *h, const char *text, Bwpp
   return s;
 }
 
+namespace {
+void drop_graph(BwppHipPlan *p) {
+  if (p->exec) (void)hipGraphExecDestroy(p->exec);
+  if (p->graph) (void)hipGraphDestroy(p->graph);
+  p->exec = nullptr;
+  p->graph = nullptr;
+}
+}  // namespace
+
 extern "C" void bwpp_hip_plan_destroy(BwppHipPlan *p) {
   if (!p) return;
+  drop_graph(p);
   if (p->allocated) bwpp_hip_arena_destroy(&p->arena);
   delete p;
+}
+
+extern "C" BwppHipStatus bwpp_hip_plan_capture(BwppHipPlan *p) {
+  if (!p) return BWPP_HIP_ERR_INVALID_ARG;
+  drop_graph(p);
+  if (!p->h) return perr(p, BWPP_HIP_ERR_INVALID_ARG, "plan created without a device handle");
+  hipStream_t st = static_cast<hipStream_t>(bwpp_hip_get_stream(p->h));
+  if (!st) return perr(p, BWPP_HIP_ERR_UNSUPPORTED, "capture needs a non-default stream on the handle");
+  // One eager run first: every workspace the ops use reaches its final size,
+  // so nothing allocates while the stream is being captured.
+  BwppHipStatus s = bwpp_hip_plan_run(p);
+  if (s != BWPP_HIP_OK) return s;
+  if (hipStreamSynchronize(st) != hipSuccess) return perr(p, BWPP_HIP_ERR_HIP, "stream synchronize failed");
+  hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return perr(p, BWPP_HIP_ERR_HIP, "hipStreamBeginCapture: %s", hipGetErrorString(e));
+  for (const Op &op : p->ops) {
+    s = run_op(*p, op);
+    if (s != BWPP_HIP_OK) break;
+  }
+  hipGraph_t g = nullptr;
+  e = hipStreamEndCapture(st, &g);
+  if (s != BWPP_HIP_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return s;
+  }
+  if (e != hipSuccess || !g) return perr(p, BWPP_HIP_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+  p->graph = g;
+  e = hipGraphInstantiate(&p->exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    drop_graph(p);
+    return perr(p, BWPP_HIP_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+  }
+  return BWPP_HIP_OK;
+}
+
+extern "C" BwppHipStatus bwpp_hip_plan_replay(BwppHipPlan *p) {
+  if (!p) return BWPP_HIP_ERR_INVALID_ARG;
+  if (!p->exec) return perr(p, BWPP_HIP_ERR_INVALID_ARG, "no captured graph (capture after the last bind)");
+  hipStream_t st = static_cast<hipStream_t>(bwpp_hip_get_stream(p->h));
+  hipError_t e = hipGraphLaunch(p->exec, st);
+  if (e != hipSuccess) return perr(p, BWPP_HIP_ERR_HIP, "hipGraphLaunch: %s", hipGetErrorString(e));
+  return BWPP_HIP_OK;
 }
 
 extern "C" const char *bwpp_hip_plan_last_error(const BwppHipPlan *p) { return p ? p->err.c_str() : ""; }
@@ -454,6 +509,7 @@ extern "C" BwppHipStatus bwpp_hip_plan_bind(BwppHipPlan *p, const char *name, vo
   Value &v = p->values[it->second];
   if (v.kind != Kind::kInput && v.kind != Kind::kParam)
     return perr(p, BWPP_HIP_ERR_INVALID_ARG, "'%s' is not an input or param", name);
+  if (v.ptr != ptr) drop_graph(p);  // the graph holds the old address
   v.ptr = ptr;
   return BWPP_HIP_OK;
 }

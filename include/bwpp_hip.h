@@ -495,6 +495,16 @@ BwppHipStatus bwpp_hip_plan_bind(BwppHipPlan *plan, const char *name, void *devi
 void *bwpp_hip_plan_value_ptr(const BwppHipPlan *plan, const char *name);
 /* Runs every launch in order on the handle's stream. */
 BwppHipStatus bwpp_hip_plan_run(BwppHipPlan *plan);
+/* Records the plan's launches as a HIP graph (no reference counterpart: for
+ * loops that replay one plan and should not pay the host cost of each
+ * launch).  Runs the plan once eagerly first, so every workspace reaches its
+ * final size, then captures one run on the handle's stream, which must not
+ * be the default (null) stream (UNSUPPORTED).  Binding a different address
+ * afterwards drops the graph; capture again. */
+BwppHipStatus bwpp_hip_plan_capture(BwppHipPlan *plan);
+/* Launches the captured graph on the handle's current stream (INVALID_ARG
+ * when there is none).  Results equal bwpp_hip_plan_run's. */
+BwppHipStatus bwpp_hip_plan_replay(BwppHipPlan *plan);
 /* Memory-plan report in mem_plan.c:176-193's layout plus byte sizes, arena
  * offsets and the total; returns the bytes needed including the NUL. */
 size_t bwpp_hip_plan_report(const BwppHipPlan *plan, char *buf, size_t cap);

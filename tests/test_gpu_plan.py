@@ -203,3 +203,64 @@ op copy out=back in=yc bcast=full
     assert np.array_equal(p.host("whole", (R, 2 * C)), np.hstack([x, y]))
     assert np.array_equal(p.host("back", (R, C)), y)
     p.close()
+
+
+def test_plan_graph_replay(be):
+    """bwpp_hip_plan_capture / replay: a captured training step replays
+    bit-identical to the eager run, three times in a row with other eager
+    work and synchronizations between the replays; rebinding an input drops
+    the graph (replay refuses) until it is captured again."""
+    import torch
+    from blockref import block_inputs, grad_shapes
+    B, T, D, H, HEADS = 2, 64, 128, 256, 2
+    shapes = dict(grad_shapes(B, T, D, H), out=(B * T, D), loss=(1,))
+    side = torch.cuda.Stream()
+    be.set_stream(side)
+    try:
+        p = plan.Plan(be, plan.load_text("block_train", BATCH=B, T=T, D=D, H=H, HEADS=HEADS))
+        p.allocate()
+        dev = {k: torch.from_numpy(v).cuda() for k, v in block_inputs(B, T, D, H, seed=21).items()}
+        torch.cuda.synchronize()
+        for k, v in dev.items():
+            p.bind(k, v)
+        p.run()
+        want = {n: p.host(n, sh) for n, sh in shapes.items()}
+        p.capture()
+        x = torch.randn(4096, 1024, device="cuda")
+        y = torch.empty_like(x)
+        torch.cuda.synchronize()
+        for rep in range(3):
+            p.replay()
+            be.dispatch_softmax(x, y, bwpp.SoftmaxParams(4096, 1024, 1024))  # eager work on the same stream
+            torch.cuda.synchronize()
+            for n, sh in shapes.items():
+                assert np.array_equal(p.host(n, sh).view(np.uint32), want[n].view(np.uint32)), (rep, n)
+        # a different x: the graph is dropped; capture again and compare with an eager run
+        x2 = torch.from_numpy(block_inputs(B, T, D, H, seed=22)["x"]).cuda()
+        torch.cuda.synchronize()
+        p.bind("x", x2)
+        with pytest.raises(plan.PlanError):
+            p.replay()
+        p.run()
+        want2 = p.host("dx", shapes["dx"])
+        assert not np.array_equal(want2, want["dx"])
+        p.capture()
+        p.replay()
+        assert np.array_equal(p.host("dx", shapes["dx"]).view(np.uint32), want2.view(np.uint32))
+        p.close()
+    finally:
+        torch.cuda.synchronize()
+        be.set_stream(torch.cuda.current_stream())
+
+
+def test_plan_capture_needs_a_stream(be):
+    import torch
+    be.set_stream(torch.cuda.default_stream())
+    p = plan.Plan(be, "bwpp.plan 1\ndim N 4\nvalue x f32 [N] input\nvalue y f32 [N] output\nop silu out=y in=x\n")
+    p.allocate()
+    x = torch.ones(4, device="cuda")
+    p.bind("x", x)
+    with pytest.raises(plan.PlanError) as e:
+        p.capture()
+    assert "non-default stream" in str(e.value)
+    p.close()
