@@ -492,6 +492,75 @@ def _bf16(torch, x):
 EXTRA_GROUPS = ("c3", "c3f32", "c4", "c5")
 
 
+def library_baseline(be, torch, seed, iters):
+    """The same contractions through the vendor libraries torch uses on
+    ROCm, timed the same way (steady state, median of grouped launches):
+    C3 as hipBLASLt GEMM alone and GEMM + bias + SiLU (torch.addmm, silu),
+    C3-fp32 as torch.mm, C4 forward and backward through
+    scaled_dot_product_attention restricted to its flash backend (no
+    fallback to the math path).  Next to each, this library's time."""
+    import bwpp
+    from bwpp import synth
+    out = {}
+    M, K, N = 4096, 4096, 11008
+    x = _bf16(torch, synth.normal((M, K), seed, 0, 0.0, 0.02))
+    w = _bf16(torch, synth.normal((K, N), seed, 1, 0.0, 0.02))
+    b = _bf16(torch, synth.normal((N,), seed, 2, 0.0, 0.02))
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    fl = 2.0 * M * N * K
+    t_lib = _events_us(torch, lambda: torch.matmul(x, w, out=y), iters)
+    t_fused = _events_us(torch, lambda: torch.nn.functional.silu(torch.addmm(b, x, w)), iters)
+    p = bwpp.MatmulParams(M, N, K, K, N, N, int(bwpp.DType.BF16), 3, 0, 0)
+    t_ours = _events_us(torch, lambda: be.dispatch_matmul(x, w, y, b, p), iters)
+    out["c3_gemm_bf16"] = {"torch_matmul_us": round(t_lib, 1), "torch_matmul_TFLOP_s": round(fl / t_lib / 1e6, 1),
+                           "torch_addmm_silu_us": round(t_fused, 1),
+                           "bwpp_gemm_bias_silu_us": round(t_ours, 1),
+                           "bwpp_TFLOP_s": round(fl / t_ours / 1e6, 1)}
+    del x, w, y
+    n = 2048
+    xf = torch.from_numpy(synth.uniform((n, n), seed, 0, -1, 1)).cuda()
+    wf = torch.from_numpy(synth.uniform((n, n), seed, 1, -1, 1)).cuda()
+    yf = torch.empty((n, n), device="cuda")
+    fl = 2.0 * n ** 3
+    t_lib = _events_us(torch, lambda: torch.mm(xf, wf, out=yf), iters)
+    p = bwpp.MatmulParams(n, n, n, n, n, n, int(bwpp.DType.F32), 0, 0, 0)
+    t_ours = _events_us(torch, lambda: be.dispatch_matmul(xf, wf, yf, None, p), iters)
+    out["c3_gemm_f32_2048"] = {"torch_mm_us": round(t_lib, 1), "torch_TFLOP_s": round(fl / t_lib / 1e6, 1),
+                               "bwpp_us": round(t_ours, 1), "bwpp_TFLOP_s": round(fl / t_ours / 1e6, 1)}
+    del xf, wf, yf
+    B, H, S, d = 8, 32, 2048, 128
+    q, k, v = (_bf16(torch, synth.normal((B, H, S, d), seed, i)) for i in range(3))
+    o = torch.empty_like(q)
+    full = 4.0 * B * H * S * S * d
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        for causal in (0, 1):
+            p = bwpp.AttentionParams(M=S, N=S, K=d, D=d, ldq=d, ldk=d, ldv=d, ldo=d, batch=B, heads=H,
+                                     scale=d ** -0.5, causal=causal, dtype=int(bwpp.DType.BF16))
+            fl = full / 2 if causal else full
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                f = lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=bool(causal))
+                t_lib = _events_us(torch, f, iters)
+                qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+                og = torch.nn.functional.scaled_dot_product_attention(qg, kg, vg, is_causal=bool(causal))
+                go = torch.ones_like(og)
+                t_lib_bwd = _events_us(torch, lambda: torch.autograd.grad(og, (qg, kg, vg), go, retain_graph=True),
+                                       max(3, iters // 3))
+            t_ours = _events_us(torch, lambda: be.dispatch_attention(q, k, v, o, p), iters)
+            lse = torch.empty((B, H, S), device="cuda")
+            be.dispatch_attention_lse(q, k, v, o, lse, p)
+            dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+            t_ours_bwd = _events_us(torch, lambda: be.dispatch_attention_grad(q, k, v, o, go, lse, dq, dk, dv, p),
+                                    max(3, iters // 3))
+            out["c4_attention" + ("_causal" if causal else "")] = {
+                "torch_sdpa_flash_fwd_us": round(t_lib, 1), "torch_sdpa_flash_bwd_us": round(t_lib_bwd, 1),
+                "bwpp_fwd_us": round(t_ours, 1), "bwpp_bwd_us": round(t_ours_bwd, 1),
+                "torch_fwd_TFLOP_s": round(fl / t_lib / 1e6, 1), "bwpp_fwd_TFLOP_s": round(fl / t_ours / 1e6, 1)}
+    except Exception as e:  # no flash backend: report, do not fall back to the math path
+        out["c4_attention"] = {"error": f"{type(e).__name__}: {e}"}
+    return out
+
+
 def extras(be, torch, seed, iters, with_cpu, warm_ms=WARM_MS, only=EXTRA_GROUPS):
     """Contraction configs C3, C3-fp32 (with C1), C4 (both masks, and the
     C4-shape attention backward) and C5; `only` selects groups."""
@@ -726,6 +795,8 @@ def main():
                     help="comma list of contraction groups to run: " + ", ".join(EXTRA_GROUPS))
     ap.add_argument("--warm-ms", type=float, default=WARM_MS,
                     help="sustained work before each contraction is timed (0 for counter runs)")
+    ap.add_argument("--vs-library", action="store_true",
+                    help="also time C3, C3-fp32 and C4 through torch's vendor-library paths (hipBLASLt, SDPA flash)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="no GPU: print a markdown table of per-kernel counters from rocprofv3 --pmc "
                          "(and --kernel-trace) output dirs")
@@ -772,6 +843,8 @@ def main():
     if args.no_c2:
         out = {"metric": METRIC, "config": {"workload": "contractions only (no headline)"},
                "extras": extras(be, torch, args.seed, args.extras_iters, not args.no_cpu, args.warm_ms, only)}
+        if args.vs_library:
+            out["library"] = library_baseline(be, torch, args.seed, args.extras_iters)
         be.close()
         print(json.dumps(out))
         return
