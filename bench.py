@@ -627,9 +627,9 @@ def _extras_c3f32(be, torch, seed, iters, orc, out):
     st = {}
     us = _events_us(torch, lambda: be.dispatch_matmul(xf, wf, yf, bf, p), iters, stats=st)
     fl = 2.0 * n ** 3
-    # 256 tiles of 128 x 128 fill half the chip: the dispatcher splits K in
-    # two (bwpp_gemm_f32_t00_s) and adds the halves in a reduce pass.
-    c3f = {"kernel": "bwpp_gemm_f32_t00_s + bwpp_gemm_f32_splitk_reduce",
+    # 256 tiles of 128 x 128: the dispatcher's cost model picks the 4-stage
+    # LDS-DMA ring kernel (one block per CU) without a K split.
+    c3f = {"kernel": be.last_kernel,
            "us_per_launch": round(us, 1), **st,
            "TFLOP_s": round(fl / us / 1e6, 1),
            "frac_f32_peak": round(fl / us / 1e6 / F32_PEAK_TFLOPS, 4)}

@@ -872,6 +872,262 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
   }
 }
 
+// ------------------------------------------------------- fp32, DMA ring
+//
+// Full tiles (M, N multiples of 128, K of 32, 16-byte rows): 128 x 128
+// blocks of 4 waves in 2 x 2 (64 x 64 each), K in 32-deep tiles through an
+// S-stage LDS ring filled by global_load_lds_dwordx4, one barrier per tile.
+// S = 2 runs two blocks per CU (two waves per SIMD); S = 4 one block with
+// three tiles in flight ahead of the MFMAs.  Operand tiles keep their memory
+// orientation in LDS, so the DMA copies rows as they are:
+//   K-contiguous (A, or B with TB): [128 rows][32 k], 128-byte rows of
+//     eight 16-byte chunks, logical chunk q of row r at q ^ (r & 7); the
+//     MFMA reads (lane l: row l % 32, chunk 2j + l / 32 of the 8-k chunk j)
+//     then hit distinct bank groups;
+//   MN-contiguous (B, or A with TA): [32 k][128], 16-byte column chunk c of
+//     k row k at c ^ (8 ((k >> 2) & 1)): lanes 32-63 read k + 4, which
+//     would otherwise sit on the banks of lanes 0-31.
+// MFMA step s of 8-k chunk j pairs k = 8j + s (lanes 0-31) with 8j + 4 + s
+// (lanes 32-63), as in the register-staged kernel above.
+// Schedule of tile kt, per wave: chunks 0-2 each after the reads of the
+// next chunk; then wait for tile kt + 1's DMA, barrier (every wave has read
+// tile kt), and chunk 3's MFMAs with the refill of tile kt's stage (tile
+// kt + S) and the reads of chunk 0 of tile kt + 1 issued between them.  The
+// last S tiles run a drain loop without refills.
+constexpr int kF32Tile = 128 * 32 * 4;  // bytes of one operand tile
+constexpr int kF32Stage = 2 * kF32Tile;
+constexpr int kF32Cld = 128 + 4;        // epilogue C tile [128][132] fp32 in the ring
+
+__device__ __forceinline__ uint32_t f32_mnc_pos(uint32_t k, uint32_t c) { return c ^ (((k >> 2) & 1u) << 3); }
+
+// Global source of lane `lane`'s 16 bytes in 1-KiB DMA block `blk` of an
+// operand tile whose first k is 0 (the caller adds the k advance).
+template <bool KC>
+__device__ __forceinline__ const float *f32_dma_src(const float *g, uint32_t ld, uint32_t r0, uint32_t blk,
+                                                    int lane) {
+  if constexpr (KC) {
+    const uint32_t row = blk * 8u + (uint32_t)lane / 8u, pc = (uint32_t)lane & 7u;
+    return g + (size_t)(r0 + row) * ld + 4u * (pc ^ (row & 7u));
+  } else {
+    const uint32_t k = blk * 2u + (uint32_t)lane / 32u, pc = (uint32_t)lane & 31u;
+    return g + (size_t)k * ld + r0 + 4u * f32_mnc_pos(k, pc);
+  }
+}
+
+// The lane's operand values for the four MFMA steps of 8-k chunk j of the
+// 32-row (or 32-column) block starting at rb.
+template <bool KC>
+__device__ __forceinline__ float4 f32_operand(const unsigned char *tile, uint32_t rb, uint32_t j, int lane) {
+  const uint32_t l = (uint32_t)lane & 31u, h = (uint32_t)lane >> 5;
+  if constexpr (KC) {
+    const uint32_t row = rb + l, q = 2u * j + h;
+    return *reinterpret_cast<const float4 *>(tile + row * 128u + 16u * (q ^ (row & 7u)));
+  } else {
+    const uint32_t k = 8u * j + 4u * h, col = rb + l;
+    const float *t = reinterpret_cast<const float *>(tile) + k * 128u + 4u * f32_mnc_pos(k, col >> 2) + (col & 3u);
+    return make_float4(t[0], t[128], t[256], t[384]);
+  }
+}
+
+template <bool TA, bool TB, bool SPLIT, int S>
+__device__ __forceinline__ void gemm_f32_pipe(const BwppGemmArgs &a) {
+  constexpr int BM = 128, BN = 128, BK = 32, WN = 2, NT = 256;
+  constexpr int TM = 64, TN = 64, FM = TM / 32, FN = TN / 32;
+  constexpr int LPW = 16 / 4;         // 1 KiB DMA blocks per wave per operand tile
+  constexpr int kDma = 2 * LPW;       // DMA instructions per wave per K tile
+  constexpr int kSmem = S * kF32Stage > BM * kF32Cld * 4 ? S * kF32Stage : BM * kF32Cld * 4;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmem];
+  float *smemf = reinterpret_cast<float *>(smem);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  uint32_t tm, tn;
+  const float *A = static_cast<const float *>(a.a);
+  const float *B = static_cast<const float *>(a.b);
+  uint32_t Klen = a.K, split = 0;
+  if constexpr (SPLIT) {
+    const uint32_t T = a.tiles_m * a.tiles_n;
+    split = blockIdx.x / T;
+    tile_coords(a, tm, tn, blockIdx.x - split * T);
+    const uint32_t kb = split * a.kchunk;
+    Klen = min(a.kchunk, a.K - kb);
+    A += TA ? (size_t)kb * a.lda : kb;
+    B += TB ? kb : (size_t)kb * a.ldb;
+  } else {
+    tile_coords(a, tm, tn);
+  }
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  const uint32_t nk = Klen / BK;
+
+  // Per-lane DMA sources at k = 0 and their advance per K tile.
+  const float *srcA[LPW], *srcB[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    srcA[i] = f32_dma_src<!TA>(A, a.lda, m0, (uint32_t)(wave * LPW + i), lane);
+    srcB[i] = f32_dma_src<TB>(B, a.ldb, n0, (uint32_t)(wave * LPW + i), lane);
+  }
+  const size_t stepA = TA ? (size_t)BK * a.lda : (size_t)BK;
+  const size_t stepB = TB ? (size_t)BK : (size_t)BK * a.ldb;
+  const uint32_t lds0 =
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)smem + (uint32_t)(wave * LPW) * 1024u;
+  auto dma_one = [&](uint32_t kt, int d) {  // DMA instruction d (A blocks, then B) of tile kt
+    const uint32_t st = lds0 + (kt % S) * kF32Stage;
+    if (d < LPW) g2lds16(srcA[d] + kt * stepA, st + (uint32_t)d * 1024u);
+    else g2lds16(srcB[d - LPW] + kt * stepB, st + kF32Tile + (uint32_t)(d - LPW) * 1024u);
+  };
+  auto dma_tile = [&](uint32_t kt) {
+#pragma unroll
+    for (int d = 0; d < kDma; ++d) dma_one(kt, d);
+  };
+  auto stage_ptr = [&](uint32_t kt) {
+    return smem + __builtin_amdgcn_readfirstlane((kt % S) * kF32Stage);
+  };
+
+  f32x16_t acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  float4 af[2][FM], bf[2][FN];
+  auto read_chunk = [&](const unsigned char *st, uint32_t j, float4(&ar)[FM], float4(&br)[FN]) {
+#pragma unroll
+    for (int f = 0; f < FM; ++f) ar[f] = f32_operand<!TA>(st, (uint32_t)(wm * TM + f * 32), j, lane);
+#pragma unroll
+    for (int f = 0; f < FN; ++f) br[f] = f32_operand<TB>(st + kF32Tile, (uint32_t)(wn * TN + f * 32), j, lane);
+  };
+  // MFMA idx of a chunk: step idx / (FN FM), accumulator (idx / FM) % FN, idx % FM.
+  auto mfma_one = [&](const float4(&ac)[FM], const float4(&bc)[FN], int idx) {
+    const int st = idx / (FN * FM), i = (idx / FM) % FN, jj = idx % FM;
+    const float x = st == 0 ? bc[i].x : st == 1 ? bc[i].y : st == 2 ? bc[i].z : bc[i].w;
+    const float y = st == 0 ? ac[jj].x : st == 1 ? ac[jj].y : st == 2 ? ac[jj].z : ac[jj].w;
+    acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc[i][jj], 0, 0, 0);
+  };
+  auto mfma_chunk = [&](const float4(&ac)[FM], const float4(&bc)[FN]) {
+#pragma unroll
+    for (int idx = 0; idx < 4 * FN * FM; ++idx) mfma_one(ac, bc, idx);
+  };
+  auto read_one = [&](const unsigned char *st, int f) {  // chunk 0 operand f (A fragments, then B) into af/bf[0]
+    if (f < FM) af[0][f] = f32_operand<!TA>(st, (uint32_t)(wm * TM + f * 32), 0, lane);
+    else bf[0][f - FM] = f32_operand<TB>(st + kF32Tile, (uint32_t)(wn * TN + (f - FM) * 32), 0, lane);
+  };
+  // Chunk 3 of a tile after the barrier, with tile kt + S's refill DMAs and
+  // the reads of chunk 0 of tile kt + 1 issued between its MFMAs, so the
+  // matrix pipe restarts right after the barrier.
+  auto tail_chunk = [&](uint32_t kt) {
+    const unsigned char *nxt = stage_ptr(kt + 1);
+#pragma unroll
+    for (int idx = 0; idx < 4 * FN * FM; ++idx) {
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_one(af[1], bf[1], idx);
+      __builtin_amdgcn_sched_barrier(0);
+      if (idx < kDma) dma_one(kt + S, idx);
+      if (idx >= kDma && idx < kDma + FM + FN) read_one(nxt, idx - kDma);
+    }
+  };
+
+  // Prologue: the first min(S, nk) tiles in flight, wait for tile 0.
+#pragma unroll
+  for (int st = 0; st < S; ++st)
+    if ((uint32_t)st < nk) dma_tile((uint32_t)st);
+  if constexpr (S >= 4) {
+    if (nk >= 4) wait_vmcnt<3 * kDma>();
+    else if (nk == 3) wait_vmcnt<2 * kDma>();
+    else if (nk == 2) wait_vmcnt<kDma>();
+    else wait_vmcnt<0>();
+  } else {
+    if (nk >= 2) wait_vmcnt<kDma>();
+    else wait_vmcnt<0>();
+  }
+  __syncthreads();
+  if (nk > 0) read_chunk(stage_ptr(0), 0, af[0], bf[0]);
+
+  auto head_chunks = [&](uint32_t kt) {  // chunks 0-2, each after the reads of the next chunk
+    const unsigned char *cur = stage_ptr(kt);
+#pragma unroll
+    for (uint32_t j = 0; j < 3; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      read_chunk(cur, j + 1, af[(j + 1) & 1], bf[(j + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_chunk(af[j & 1], bf[j & 1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Steady state: tile kt + S exists, so every tile refills its stage and
+  // tiles kt + 2 .. kt + S - 1 stay in flight across the barrier.
+  uint32_t kt = 0;
+  for (; kt + S < nk; ++kt) {
+    head_chunks(kt);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): done reading tile kt
+    wait_vmcnt<(S - 2) * kDma>();
+    __syncthreads();
+    tail_chunk(kt);
+  }
+  // Drain: the last (up to) S tiles, no refills.
+  for (; kt < nk; ++kt) {
+    head_chunks(kt);
+    if (kt + 1 < nk) {
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      const uint32_t younger = nk - 2 - kt;  // tiles still in flight behind kt + 1
+      if (S >= 4 && younger >= 2) wait_vmcnt<2 * kDma>();
+      else if (S >= 3 && younger == 1) wait_vmcnt<kDma>();
+      else wait_vmcnt<0>();
+      __syncthreads();
+      read_chunk(stage_ptr(kt + 1), 0, af[0], bf[0]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    mfma_chunk(af[1], bf[1]);
+  }
+  __syncthreads();  // the epilogue reuses the ring
+
+  // Epilogue through LDS (split-K blocks store raw sums; the reduce kernel
+  // applies the epilogue and the fused tail).
+  const float *bias = static_cast<const float *>(a.bias);
+  const bool add = !SPLIT && (a.epilogue & kEpiAdd) && bias;
+  const bool act = !SPLIT && (a.epilogue & kEpiSilu) != 0;
+  const int lrow = lane & 31, lhalf = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < FN; ++i) {
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int ml = wm * TM + j * 32 + lrow;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = wn * TN + i * 32 + q * 8 + lhalf * 4;
+        float vv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float t = acc[i][j][q * 4 + e];
+          if (add) t += bias[n0 + nl + e];
+          if (act) t = silu(t);
+          vv[e] = t;
+        }
+        *reinterpret_cast<float4 *>(smemf + ml * kF32Cld + nl) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+      }
+    }
+  }
+  __syncthreads();
+  float *C = SPLIT ? a.part + (size_t)split * a.M * a.N : static_cast<float *>(a.c);
+  const uint32_t ldc = SPLIT ? a.N : a.ldc;
+  const uint32_t fuse = SPLIT ? 0u : a.fuse;
+  constexpr int kRowVecs = BN / 4;
+#pragma unroll 4
+  for (int it = 0; it < BM * kRowVecs / NT; ++it) {
+    const int q = tid + it * NT;
+    const int row = q / kRowVecs, c = q % kRowVecs;
+    const uint32_t m = m0 + row, n = n0 + c * 4;
+    float4 v = *reinterpret_cast<const float4 *>(smemf + row * kF32Cld + c * 4);
+    if (fuse_reads_aux(fuse)) v = fuse4(fuse, v, *reinterpret_cast<const float4 *>(a.aux + (size_t)m * a.ldaux + n));
+    *reinterpret_cast<float4 *>(C + (size_t)m * ldc + n) = v;
+    if (fuse == kFuseDualSilu)
+      *reinterpret_cast<float4 *>(a.c2 + (size_t)m * a.ldc2 + n) =
+          make_float4(silu(v.x), silu(v.y), silu(v.z), silu(v.w));
+  }
+}
+
 }  // namespace
 
 // Split-K reduction: C[m][n..n+3] = epilogue(sum_s part[s][m][n..n+3]) in
@@ -963,3 +1219,27 @@ BWPP_GEMM_F32_SPLIT(0, 0)
 BWPP_GEMM_F32_SPLIT(0, 1)
 BWPP_GEMM_F32_SPLIT(1, 0)
 BWPP_GEMM_F32_SPLIT(1, 1)
+// DMA-ring full-tile kernels: bwpp_gemm_f32p_t<TA><TB>_<f|s> (two blocks
+// per CU, 2-stage ring) and bwpp_gemm_f32q_t<TA><TB>_<f|s> (one block per
+// CU, 4-stage ring).
+#define BWPP_GEMM_F32_PIPE(TA, TB)                                                         \
+  extern "C" __global__ __launch_bounds__(256, 2) void bwpp_gemm_f32p_t##TA##TB##_f(     \
+      const BwppGemmArgs a) {                                                             \
+    gemm_f32_pipe<TA, TB, false, 2>(a);                                                   \
+  }                                                                                       \
+  extern "C" __global__ __launch_bounds__(256, 2) void bwpp_gemm_f32p_t##TA##TB##_s(     \
+      const BwppGemmArgs a) {                                                             \
+    gemm_f32_pipe<TA, TB, true, 2>(a);                                                    \
+  }                                                                                       \
+  extern "C" __global__ __launch_bounds__(256) void bwpp_gemm_f32q_t##TA##TB##_f(        \
+      const BwppGemmArgs a) {                                                             \
+    gemm_f32_pipe<TA, TB, false, 4>(a);                                                   \
+  }                                                                                       \
+  extern "C" __global__ __launch_bounds__(256) void bwpp_gemm_f32q_t##TA##TB##_s(        \
+      const BwppGemmArgs a) {                                                             \
+    gemm_f32_pipe<TA, TB, true, 4>(a);                                                    \
+  }
+BWPP_GEMM_F32_PIPE(0, 0)
+BWPP_GEMM_F32_PIPE(0, 1)
+BWPP_GEMM_F32_PIPE(1, 0)
+BWPP_GEMM_F32_PIPE(1, 1)

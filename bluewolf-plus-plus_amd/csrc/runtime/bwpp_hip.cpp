@@ -82,6 +82,7 @@ struct BwppHip {
   hipFunction_t gemm[2][2][2][2] = {};
   hipFunction_t gemm_bf16_w8[2][2] = {};  // 8-wave full-tile bf16: [ta][tb]
   hipFunction_t gemm_f32_split[2][2] = {};  // fp32 full tiles, split-K partials: [ta][tb]
+  hipFunction_t gemm_f32p[2][2][2][2] = {};  // fp32 full tiles, DMA ring: [4-stage][ta][tb][split]
   hipFunction_t gemm_f32_reduce = nullptr;
   hipFunction_t attn_flash[2] = {};       // bf16, d = 128: [causal]
   hipFunction_t attn_generic[2][2] = {};  // [bf16][causal]
@@ -110,6 +111,7 @@ struct BwppHip {
   uint32_t gemm_group_m = 8;  // BWPP_GEMM_GROUP_M
   uint32_t gemm_waves = 8;    // BWPP_GEMM_WAVES: 4 or 8 waves for full bf16 tiles
   uint32_t gemm_splitk = 1;   // BWPP_GEMM_SPLITK=0 turns fp32 split-K off
+  uint32_t gemm_f32_pipe = 1;  // BWPP_GEMM_F32_PIPE: fp32 full tiles 0 staged, 1 auto, 2 ring4, 3 ring2
 };
 
 namespace {
@@ -213,6 +215,13 @@ BwppHipStatus resolve_all(BwppHip *h) {
       if ((s = resolve(h, n, &h->gemm_bf16_w8[ta][tb])) != BWPP_HIP_OK) return s;
       const std::string ns = std::string("bwpp_gemm_f32_t") + char('0' + ta) + char('0' + tb) + "_s";
       if ((s = resolve(h, ns, &h->gemm_f32_split[ta][tb])) != BWPP_HIP_OK) return s;
+      for (int sp = 0; sp < 2; ++sp) {
+        for (int q = 0; q < 2; ++q) {
+          const std::string np = std::string(q ? "bwpp_gemm_f32q_t" : "bwpp_gemm_f32p_t") + char('0' + ta) +
+                                 char('0' + tb) + (sp ? "_s" : "_f");
+          if ((s = resolve(h, np, &h->gemm_f32p[q][ta][tb][sp])) != BWPP_HIP_OK) return s;
+        }
+      }
     }
   for (int causal = 0; causal < 2; ++causal) {
     const char *cs = causal ? "_causal" : "";
@@ -370,6 +379,7 @@ BwppHipStatus bwpp_hip_create(BwppHip **out, int device, const char *code_object
   if (const char *gc = getenv("BWPP_ROW_GRID")) h->row_grid_cap = (uint32_t)strtoul(gc, nullptr, 10);
   if (const char *gw = getenv("BWPP_GEMM_WAVES")) h->gemm_waves = (uint32_t)strtoul(gw, nullptr, 10) == 4 ? 4 : 8;
   if (const char *sk = getenv("BWPP_GEMM_SPLITK")) h->gemm_splitk = atoi(sk) != 0 ? 1u : 0u;
+  if (const char *fp = getenv("BWPP_GEMM_F32_PIPE")) h->gemm_f32_pipe = (uint32_t)std::min(std::max(atoi(fp), 0), 3);
   if (const char *w8 = getenv("BWPP_ATTN_BWD_W8")) h->attn_w8_mask = (uint32_t)strtoul(w8, nullptr, 10) & 3u;
   if (const char *gm = getenv("BWPP_GEMM_GROUP_M")) {
     const uint32_t v = (uint32_t)strtoul(gm, nullptr, 10);
@@ -759,48 +769,67 @@ BwppHipStatus matmul_impl(BwppHip *h, const void *a, const void *b, void *c, con
   if (tiles > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "matmul: too many tiles");
   if (bf16 && full && h->gemm_waves == 8)
     return launch(h, h->gemm_bf16_w8[ta][tb], (uint32_t)tiles, 1, 1, 512, g);
-  // fp32 full tiles: split K into S ranges (multiples of BK) when that fills
-  // the chip better.  Each CU holds two 128 x 128
-  // blocks, so a launch of b blocks runs in ceil(b / slots) waves of blocks
-  // that each take time proportional to their K range; splitting adds a
-  // reduce pass over S + 1 planes of M x N floats.  S minimises
-  //   waves(S) * (K / S) * t_k + (S + 1) * M * N * 4 / bw + t_launch
-  // with t_k = 0.13 us per k of one block (measured: a 128 x 128 x 1024
-  // block takes ~134 us with two blocks per CU), bw = 5 TB/s, t_launch =
-  // 5 us.  The blocks write raw partial tiles into the workspace and the
-  // reduce pass adds them in order and applies the epilogue.
-  if (!bf16 && full && h->gemm_splitk && h->cus > 0 && p.K >= 2 * BK) {
-    const uint64_t slots = 2ull * (uint64_t)h->cus;
-    auto cost = [&](uint64_t S, uint32_t kchunk) {
-      const double waves = (double)((tiles * S + slots - 1) / slots);
-      double t = waves * kchunk * 0.13;
-      if (S > 1) t += (double)(S + 1) * p.M * p.N * 4.0 / 5e6 + 5.0;
+  // fp32 full tiles: one of three kernels, optionally with K split into S
+  // ranges (multiples of BK) whose raw partial tiles a reduce pass adds in
+  // order, applying the epilogue and the fused tail:
+  //   ring2 (bwpp_gemm_f32p): LDS-DMA ring, 2 stages, two blocks per CU;
+  //   ring4 (bwpp_gemm_f32q): LDS-DMA ring, 4 stages, one block per CU;
+  //   staged (bwpp_gemm_f32): register-staged double buffer, two blocks per
+  //     CU (BWPP_GEMM_F32_PIPE=0 only; the rings beat it on every measured
+  //     full-tile shape).
+  // A launch of b blocks runs in ceil(b / slots) waves of blocks, each
+  // taking time proportional to its K range.  The choice minimises
+  //   ring4:  ceil(b / cus) (k t4 + o4)
+  //   ring2:  ceil(b / (2 cus)) k t2 + o4      (staged: t = 0.13)
+  // plus (S + 1) M N 4 / bw + t_launch when split, with t4 = 0.064 us and
+  // t2 = 0.122 us per k of a 128 x 128 block, o4 = 3 us per block (the
+  // prologue and epilogue, which one block per CU does not overlap), bw =
+  // 5 TB/s, t_launch = 5 us (fitted on MI355X to 8192^3, 4096 x 4096 x 1024,
+  // 4096 x 3072 x 1024, 2048^3 and 4096 x 1024 x 1024).  A split is taken
+  // only when it models 5 % faster.
+  if (!bf16 && full) {
+    const int mode = (int)h->gemm_f32_pipe;  // 0 staged, 1 auto, 2 ring4, 3 ring2
+    const uint64_t cus = h->cus > 0 ? (uint64_t)h->cus : 256ull;
+    auto cost = [&](int kind, uint64_t S, uint32_t kchunk) {  // kind: 0 staged, 1 ring2, 2 ring4
+      double t = kind == 2 ? (double)((tiles * S + cus - 1) / cus) * (kchunk * 0.064 + 3.0)
+                           : (double)((tiles * S + 2 * cus - 1) / (2 * cus)) * kchunk * (kind ? 0.122 : 0.13) + 3.0;
+      if (S > 1) t = 1.05 * (t + (double)(S + 1) * p.M * p.N * 4.0 / 5e6 + 5.0);
       return t;
     };
+    int bestKind = mode == 0 ? 0 : mode == 3 ? 1 : 2;
     uint64_t bestS = 1;
     uint32_t bestChunk = p.K;
-    double best = cost(1, p.K);
-    for (uint64_t S = 2; S <= 16 && p.K / S >= BK; ++S) {
-      const uint32_t kchunk = (uint32_t)(((p.K + S - 1) / S + BK - 1) / BK * BK);
-      const uint64_t Se = (p.K + kchunk - 1) / kchunk;
-      const double c = cost(Se, kchunk);
-      if (c < 0.95 * best) {  // split only for a clear gain
-        best = c;
-        bestS = Se;
-        bestChunk = kchunk;
+    double best = 1e300;
+    for (int kind = 0; kind < 3; ++kind) {
+      if (mode == 0 ? kind != 0 : mode == 1 ? kind == 0 : kind != bestKind) continue;
+      for (uint64_t S = 1; S <= 16 && p.K / S >= BK; ++S) {
+        if (S > 1 && !h->gemm_splitk) break;
+        const uint32_t kchunk = (uint32_t)(((p.K + S - 1) / S + BK - 1) / BK * BK);
+        const uint64_t Se = (p.K + kchunk - 1) / kchunk;
+        if (Se != S) continue;
+        const double c = cost(kind, Se, kchunk);
+        if (c < best) {
+          best = c;
+          bestKind = kind;
+          bestS = Se;
+          bestChunk = kchunk;
+        }
       }
     }
+    const int ring4 = bestKind == 2;
     if (bestS > 1) {
       if ((s = ensure_ws(h, (size_t)bestS * p.M * p.N * sizeof(float))) != BWPP_HIP_OK) return s;
       g.ksplit = (uint32_t)bestS;
       g.kchunk = bestChunk;
       g.part = static_cast<float *>(h->ws);
-      if ((s = launch(h, h->gemm_f32_split[ta][tb], (uint32_t)(tiles * bestS), 1, 1, 256, g)) != BWPP_HIP_OK)
+      if ((s = launch(h, bestKind ? h->gemm_f32p[ring4][ta][tb][1] : h->gemm_f32_split[ta][tb],
+                      (uint32_t)(tiles * bestS), 1, 1, 256, g)) != BWPP_HIP_OK)
         return s;
       const uint64_t vecs = (uint64_t)p.M * (p.N / 4);
-      const uint64_t grid = std::min<uint64_t>((vecs + 255) / 256, 8ull * (uint64_t)h->cus);
+      const uint64_t grid = std::min<uint64_t>((vecs + 255) / 256, 8ull * cus);
       return launch(h, h->gemm_f32_reduce, (uint32_t)grid, 1, 1, 256, g);
     }
+    if (bestKind) return launch(h, h->gemm_f32p[ring4][ta][tb][0], (uint32_t)tiles, 1, 1, 256, g);
   }
   return launch(h, h->gemm[bf16 ? 1 : 0][ta][tb][full ? 1 : 0], (uint32_t)tiles, 1, 1, 256, g);
 }

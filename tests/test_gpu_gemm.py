@@ -339,3 +339,44 @@ def test_fused_tails_errors(be):
     c = torch.full((64, 64), 2.0, device="cuda")
     be.dispatch_matmul_fused(a, a, c, None, c, None, p, bwpp.FusionParams(1, 64, 0))
     assert np.array_equal(f32_host(c), np.eye(64, dtype=np.float32) + 2.0)
+
+
+@pytest.mark.parametrize("mode,family", [(0, "bwpp_gemm_f32_t"), (2, "bwpp_gemm_f32q_t"), (3, "bwpp_gemm_f32p_t")])
+@pytest.mark.parametrize("split", [0, 1])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_f32_full_tile_kernels(oracle, monkeypatch, mode, family, split, ta, tb):
+    """Each fp32 full-tile kernel forced through BWPP_GEMM_F32_PIPE (0 the
+    register-staged one, 2 the 4-stage LDS-DMA ring, 3 the 2-stage ring),
+    with split-K on (256 x 256 x 1024: four tiles, cut into K ranges) and
+    off, for every transpose pair, with bias + SiLU and with the residual
+    tail, against the oracle.  K = 32 (one tile: prologue and drain only)
+    and K = 96 (fewer tiles than ring stages) are included."""
+    torch = _torch()
+    monkeypatch.setenv("BWPP_GEMM_F32_PIPE", str(mode))
+    monkeypatch.setenv("BWPP_GEMM_SPLITK", str(split))
+    h = bwpp.HipBackend(0)
+    try:
+        h.set_stream(torch.cuda.current_stream())
+        for M, N, K in [(256, 256, 1024), (384, 128, 32), (128, 512, 96), (256, 128, 160)]:
+            a = synth.uniform((M, K), M + ta, 0, -1.0, 1.0)
+            b = synth.uniform((K, N), N + tb, 1, -1.0, 1.0)
+            bias = synth.uniform((N,), K, 2, -1.0, 1.0)
+            ad = f32_dev(np.ascontiguousarray(a.T) if ta else a)
+            bd = f32_dev(np.ascontiguousarray(b.T) if tb else b)
+            c = torch.full((M, N), 7.0, device="cuda")
+            h.dispatch_matmul(ad, bd, c, f32_dev(bias), bwpp.MatmulParams(M, N, K, 0, 0, N, 0, 3, ta, tb))
+            kern = h.last_kernel
+            want = oracle.matmul(a, b, bias, apply_silu=True, apply_bias=True)
+            assert rel_max_err(f32_host(c), want) <= F32_TOL, (M, N, K, kern)
+            if split and (M, N, K) == (256, 256, 1024):
+                assert kern == "bwpp_gemm_f32_splitk_reduce", kern
+            elif not split:
+                assert kern.startswith(family) and kern.endswith("_f"), kern
+            aux = synth.normal((M, N), M, 3)
+            c.fill_(7.0)
+            h.dispatch_matmul_fused(ad, bd, c, None, f32_dev(aux), None, bwpp.MatmulParams(M, N, K, 0, 0, N, 0, 0, ta, tb),
+                                    bwpp.FusionParams(1, N, N))
+            want = oracle.matmul(a, b, None, apply_silu=False, apply_bias=False)
+            assert rel_max_err(f32_host(c), np.add(want, aux, dtype=np.float32)) <= F32_TOL, (M, N, K, kern)
+    finally:
+        h.close()
