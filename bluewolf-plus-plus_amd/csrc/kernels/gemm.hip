@@ -881,9 +881,10 @@ __device__ __forceinline__ void gemm_f32(const BwppGemmArgs &a) {
 // three tiles in flight ahead of the MFMAs.  Operand tiles keep their memory
 // orientation in LDS, so the DMA copies rows as they are:
 //   K-contiguous (A, or B with TB): [128 rows][32 k], 128-byte rows of
-//     eight 16-byte chunks, logical chunk q of row r at q ^ (r & 7); the
-//     MFMA reads (lane l: row l % 32, chunk 2j + l / 32 of the 8-k chunk j)
-//     then hit distinct bank groups;
+//     eight 16-byte chunks, logical chunk q of row r at q ^ (r & 7) ^
+//     ((r >> 3) & 1); the MFMA reads (lane l: row l % 32, chunk 2j + l / 32
+//     of the 8-k chunk j) then hit distinct bank groups in every 16-lane
+//     pass of a ds_read_b128 (16 rows over 64 banks: r and r + 8 differ);
 //   MN-contiguous (B, or A with TA): [32 k][128], 16-byte column chunk c of
 //     k row k at c ^ (8 ((k >> 2) & 1)): lanes 32-63 read k + 4, which
 //     would otherwise sit on the banks of lanes 0-31.
@@ -899,6 +900,7 @@ constexpr int kF32Stage = 2 * kF32Tile;
 constexpr int kF32Cld = 128 + 4;        // epilogue C tile [128][132] fp32 in the ring
 
 __device__ __forceinline__ uint32_t f32_mnc_pos(uint32_t k, uint32_t c) { return c ^ (((k >> 2) & 1u) << 3); }
+__device__ __forceinline__ uint32_t f32_kc_swz(uint32_t row) { return (row & 7u) ^ ((row >> 3) & 1u); }
 
 // Global source of lane `lane`'s 16 bytes in 1-KiB DMA block `blk` of an
 // operand tile whose first k is 0 (the caller adds the k advance).
@@ -907,7 +909,7 @@ __device__ __forceinline__ const float *f32_dma_src(const float *g, uint32_t ld,
                                                     int lane) {
   if constexpr (KC) {
     const uint32_t row = blk * 8u + (uint32_t)lane / 8u, pc = (uint32_t)lane & 7u;
-    return g + (size_t)(r0 + row) * ld + 4u * (pc ^ (row & 7u));
+    return g + (size_t)(r0 + row) * ld + 4u * (pc ^ f32_kc_swz(row));
   } else {
     const uint32_t k = blk * 2u + (uint32_t)lane / 32u, pc = (uint32_t)lane & 31u;
     return g + (size_t)k * ld + r0 + 4u * f32_mnc_pos(k, pc);
@@ -921,7 +923,7 @@ __device__ __forceinline__ float4 f32_operand(const unsigned char *tile, uint32_
   const uint32_t l = (uint32_t)lane & 31u, h = (uint32_t)lane >> 5;
   if constexpr (KC) {
     const uint32_t row = rb + l, q = 2u * j + h;
-    return *reinterpret_cast<const float4 *>(tile + row * 128u + 16u * (q ^ (row & 7u)));
+    return *reinterpret_cast<const float4 *>(tile + row * 128u + 16u * (q ^ f32_kc_swz(row)));
   } else {
     const uint32_t k = 8u * j + 4u * h, col = rb + l;
     const float *t = reinterpret_cast<const float *>(tile) + k * 128u + 4u * f32_mnc_pos(k, col >> 2) + (col & 3u);
