@@ -1012,10 +1012,12 @@ __device__ __forceinline__ void gemm_f32_pipe(const BwppGemmArgs &a) {
 #pragma unroll
     for (int idx = 0; idx < 4 * FN * FM; ++idx) mfma_one(ac, bc, idx);
   };
-  auto read_one = [&](const unsigned char *st, int f) {  // chunk 0 operand f (A fragments, then B) into af/bf[0]
-    if (f < FM) af[0][f] = f32_operand<!TA>(st, (uint32_t)(wm * TM + f * 32), 0, lane);
-    else bf[0][f - FM] = f32_operand<TB>(st + kF32Tile, (uint32_t)(wn * TN + (f - FM) * 32), 0, lane);
+  // Operand f (A fragments, then B) of chunk j into af/bf[b].
+  auto read_op = [&](const unsigned char *st, uint32_t j, int f, int b) {
+    if (f < FM) af[b][f] = f32_operand<!TA>(st, (uint32_t)(wm * TM + f * 32), j, lane);
+    else bf[b][f - FM] = f32_operand<TB>(st + kF32Tile, (uint32_t)(wn * TN + (f - FM) * 32), j, lane);
   };
+  auto read_one = [&](const unsigned char *st, int f) { read_op(st, 0, f, 0); };
   // Chunk 3 of a tile after the barrier, with tile kt + S's refill DMAs and
   // the reads of chunk 0 of tile kt + 1 issued between its MFMAs, so the
   // matrix pipe restarts right after the barrier.
@@ -1047,14 +1049,20 @@ __device__ __forceinline__ void gemm_f32_pipe(const BwppGemmArgs &a) {
   __syncthreads();
   if (nk > 0) read_chunk(stage_ptr(0), 0, af[0], bf[0]);
 
-  auto head_chunks = [&](uint32_t kt) {  // chunks 0-2, each after the reads of the next chunk
+  // Chunks 0-2, the reads of chunk j + 1 issued one per MFMA slot among
+  // chunk j's MFMAs (a burst of reads from four waves in step queues at the
+  // LDS and holds up the in-order MFMA issue behind it).
+  auto head_chunks = [&](uint32_t kt) {
     const unsigned char *cur = stage_ptr(kt);
 #pragma unroll
     for (uint32_t j = 0; j < 3; ++j) {
-      __builtin_amdgcn_sched_barrier(0);
-      read_chunk(cur, j + 1, af[(j + 1) & 1], bf[(j + 1) & 1]);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_chunk(af[j & 1], bf[j & 1]);
+#pragma unroll
+      for (int idx = 0; idx < 4 * FN * FM; ++idx) {
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_one(af[j & 1], bf[j & 1], idx);
+        __builtin_amdgcn_sched_barrier(0);
+        if (idx < FM + FN) read_op(cur, j + 1, idx, (int)((j + 1) & 1));
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
   };
