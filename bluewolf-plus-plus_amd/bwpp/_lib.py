@@ -177,6 +177,7 @@ SIGNATURES = {
     "bwpp_hip_dispatch_silu_grad": (c_int, [_P, _P, _P, _P, c_uint64]),
     "bwpp_hip_dispatch_softmax_grad": (c_int, [_P, _P, _P, _P, SoftmaxParams]),
     "bwpp_hip_dispatch_rmsnorm_grad": (c_int, [_P, _P, _P, _P, _P, _P, _P, RmsnormParams]),
+    "bwpp_hip_dispatch_rmsnorm_grad_acc": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, RmsnormParams]),
     "bwpp_hip_dispatch_reduce_sum": (c_int, [_P, _P, _P, ReduceParams]),
     "bwpp_hip_dispatch_elementwise": (c_int, [_P, _P, _P, _P, ElementwiseParams]),
     "bwpp_synth_uniform_f32": (None, [_P, c_uint64, c_uint64, c_uint64, c_float, c_float]),

@@ -172,6 +172,11 @@ class HipBackend:
         self._check(self.lib.bwpp_hip_dispatch_rmsnorm_grad(
             self._h, _ptr(x), _ptr(gamma), _ptr(dy), _ptr(dx), _ptr(dgamma), _ptr(dbeta), params))
 
+    def dispatch_rmsnorm_grad_acc(self, x, gamma, dy, acc, dx, dgamma, dbeta, params: RmsnormParams):
+        """dx = acc + rmsnorm_grad(x, gamma, dy); acc may be dx itself."""
+        self._check(self.lib.bwpp_hip_dispatch_rmsnorm_grad_acc(
+            self._h, _ptr(x), _ptr(gamma), _ptr(dy), _ptr(acc), _ptr(dx), _ptr(dgamma), _ptr(dbeta), params))
+
     def dispatch_reduce_sum(self, x, out, params: ReduceParams):
         self._check(self.lib.bwpp_hip_dispatch_reduce_sum(self._h, _ptr(x), _ptr(out), params))
 

@@ -1563,12 +1563,39 @@ static void lower_nodes(Ctx *c, GCtx *gc, const uint8_t *needed, Bwd *bwd, int w
         dgam->known = 1;
         const Ref xr = operand(c, gc, rg->inputs[0]), gr = operand(c, gc, rg->inputs[1]),
                   dyr = operand(c, gc, rg->inputs[2]);
-        assign_pv(c, gc, rg->output, "dx");
+        /* The residual branch's gradient: when dX's only reader adds a
+         * matrix of dX's shape that is already computed (autodiff's sum of
+         * the two gradient contributions to a residual input), the add
+         * runs inside rmsnorm_grad as its fourth input. */
+        uint32_t dxv = rg->output;
+        int acc = -1;
+        if (c->opt->fuse_tails && gc->ncons[rg->output] == 1 && !is_needed(needed, gc, rg->output)) {
+          const uint32_t an = gc->cons[rg->output][0];
+          const BwppGraphNode *ad = &g->nodes[an];
+          if (!gc->skip[an] && ad->op == BWPP_GOP_ADD && ad->input_count == 2) {
+            const uint32_t r = ad->inputs[0] == rg->output ? ad->inputs[1] : ad->inputs[0];
+            const LVal *R = &gc->lv[r];
+            if (r != rg->output && R->known && R->pv >= 0 && !R->trans && !R->bcast && !R->bf16 &&
+                R->shape.rank >= 1 && shape_elems(&R->shape) == shape_elems(&dx->shape) &&
+                R->shape.n[R->shape.rank - 1] == dx->shape.n[dx->shape.rank - 1]) {
+              acc = (int)r;
+              gc->skip[an] = 1;
+              dx->fused = 1;
+              dxv = ad->output;
+              LVal *o = &gc->lv[dxv];
+              o->shape = dx->shape;
+              o->known = 1;
+              o->bf16 = 0;
+            }
+          }
+        }
+        assign_pv(c, gc, dxv, "dx");
         assign_pv(c, gc, rs, "dgamma");
-        char e[32];
+        char e[32], accs[80] = "";
         fmt_float(e, sizeof e, rg->attr.has_epsilon ? (double)rg->attr.epsilon : 1e-5);
-        emit(c, "op rmsnorm_grad out=%s,%s in=%s,%s,%s eps=%s\n", ref(dx->pv).s, ref(dgam->pv).s, xr.s, gr.s,
-             dyr.s, e);
+        if (acc >= 0) snprintf(accs, sizeof accs, ",%s", ref(gc->lv[acc].pv).s);
+        emit(c, "op rmsnorm_grad out=%s,%s in=%s,%s,%s%s eps=%s\n", ref(gc->lv[dxv].pv).s, ref(dgam->pv).s, xr.s,
+             gr.s, dyr.s, accs, e);
         gc->skip[i] = 2;  /* emitted */
       }
     }

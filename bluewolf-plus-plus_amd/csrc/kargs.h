@@ -117,6 +117,7 @@ typedef struct {
   uint32_t vec;     /* 1: a, b, out are 16-byte aligned (flat ops); 16-byte
                        rows (elementwise) */
   uint32_t ldb;     /* elementwise, full broadcast: row stride of b */
+  const float *acc; /* rmsnorm_grad: added to dx (row stride ld; may equal out) */
 } BwppGradArgs;
 
 #endif /* BWPP_KARGS_H */

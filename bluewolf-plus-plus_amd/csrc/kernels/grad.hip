@@ -67,7 +67,10 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_softmax_grad(const BwppGr
 }
 
 // Row-wise rmsnorm_grad with per-block column partials of dgamma / dbeta
-// (summed by bwpp_col_partials_sum).  gamma NULL means 1.
+// (summed by bwpp_col_partials_sum).  gamma NULL means 1; with g.acc,
+// dx = acc + the gradient (the residual branch's gradient added in the same
+// pass; acc may be dx itself, each element being read before it is written
+// by the same thread).
 extern "C" __global__ __launch_bounds__(256) void bwpp_rmsnorm_grad(const BwppGradArgs g) {
   __shared__ float red[4];
   extern __shared__ float colacc[];  // [2][cols] when partials are requested
@@ -79,6 +82,7 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_rmsnorm_grad(const BwppGr
     const float *x = g.a + (size_t)r * g.ld;
     const float *dy = g.b + (size_t)r * g.ld;
     float *dx = g.out + (size_t)r * g.ld;
+    const float *ac = g.acc ? g.acc + (size_t)r * g.ld : nullptr;
     float ss = 0.0f, t = 0.0f;
     for (uint32_t c = threadIdx.x; c < g.cols; c += 256) {
       const float xv = x[c];
@@ -94,7 +98,8 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_rmsnorm_grad(const BwppGr
       const float xh = x[c] * inv;
       const float d = dy[c];
       const float gd = g.gamma ? g.gamma[c] * d : d;
-      dx[c] = inv * (gd - xh * mdot);
+      const float v = inv * (gd - xh * mdot);
+      dx[c] = ac ? ac[c] + v : v;
       if (parts) {
         colacc[c] += d * xh;
         colacc[g.cols + c] += d;
@@ -136,6 +141,7 @@ __device__ __forceinline__ void rmsnorm_grad_wave(const BwppGradArgs &g) {
     const float *x = g.a + (size_t)r * g.ld;
     const float *dy = g.b + (size_t)r * g.ld;
     float *dx = g.out + (size_t)r * g.ld;
+    const float *ac = g.acc ? g.acc + (size_t)r * g.ld : nullptr;
     float4 xv[VPT], dv[VPT];
     float ss = 0.0f, t = 0.0f;
 #pragma unroll
@@ -168,6 +174,13 @@ __device__ __forceinline__ void rmsnorm_grad_wave(const BwppGradArgs &g) {
       o.y = inv * (gm[j].y * dv[j].y - h.y * mdot);
       o.z = inv * (gm[j].z * dv[j].z - h.z * mdot);
       o.w = inv * (gm[j].w * dv[j].w - h.w * mdot);
+      if (ac) {
+        const float4 a4 = *reinterpret_cast<const float4 *>(ac + c);
+        o.x = a4.x + o.x;
+        o.y = a4.y + o.y;
+        o.z = a4.z + o.z;
+        o.w = a4.w + o.w;
+      }
       *reinterpret_cast<float4 *>(dx + c) = o;
       ag[j].x += dv[j].x * h.x;
       ag[j].y += dv[j].y * h.y;

@@ -1297,12 +1297,20 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_softmax_grad(BwppHip *h, const float 
 extern "C" BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad(BwppHip *h, const float *x, const float *gamma,
                                                         const float *dy, float *dx, float *dgamma, float *dbeta,
                                                         BwppRmsnormParams p) {
+  return bwpp_hip_dispatch_rmsnorm_grad_acc(h, x, gamma, dy, nullptr, dx, dgamma, dbeta, p);
+}
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad_acc(BwppHip *h, const float *x, const float *gamma,
+                                                            const float *dy, const float *acc, float *dx,
+                                                            float *dgamma, float *dbeta, BwppRmsnormParams p) {
   BwppHipStatus s = enter(h);
   if (s != BWPP_HIP_OK) return s;
   if (!x || !dy || !dx) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "rmsnorm_grad: NULL x, dy or dx");
   const uint32_t ld = eff_ld(p.ld, p.cols);
   if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
   if (p.cols == 0) return BWPP_HIP_OK;
+  if (acc && acc != dx && overlaps(extent(acc, p.rows, p.cols, ld, 4), extent(dx, p.rows, p.cols, ld, 4)))
+    return fail(h, BWPP_HIP_ERR_ALIAS, "rmsnorm_grad: acc overlaps dx without being dx");
   const bool parts = dgamma || dbeta;
   if (parts && p.cols > 8192)
     return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "rmsnorm_grad: dgamma/dbeta need cols <= 8192 (got %u)", p.cols);
@@ -1311,6 +1319,7 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad(BwppHip *h, const float 
   g.b = dy;
   g.gamma = gamma;
   g.out = dx;
+  g.acc = acc;
   g.rows = p.rows;
   g.cols = p.cols;
   g.ld = ld;
@@ -1322,7 +1331,7 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad(BwppHip *h, const float 
   // barriers in the row loop), 4 rows per block per trip.
   int wv = -1;
   if (p.cols <= 2048 && p.cols % 4 == 0 && ld % 4 == 0 && aligned16(x) && aligned16(dy) && aligned16(dx) &&
-      (!gamma || aligned16(gamma)))
+      (!gamma || aligned16(gamma)) && (!acc || aligned16(acc)))
     wv = p.cols <= 256 ? 0 : p.cols <= 512 ? 1 : p.cols <= 1024 ? 2 : 3;
   uint32_t grid;
   if (wv >= 0) {

@@ -694,12 +694,17 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
     BwppSoftmaxParams sp = {(uint32_t)Y.rows(), (uint32_t)Y.cols(), (uint32_t)Y.row_stride()};
     s = BWPP_PLAN_CALL(bwpp_hip_dispatch_softmax_grad(h, f32(op.ins[0]), f32(op.ins[1]), f32(op.outs[0]), sp));
   } else if (k == "rmsnorm_grad") {
-    if (!need(3, 1)) return bad("in=X,gamma,dY out=dX[,dgamma[,dbeta]]");
+    // A fourth input is added to dX in the same pass (the residual branch's
+    // gradient, dX = acc + rmsnorm_grad).
+    if (!need(3, 1) || op.ins.size() > 4) return bad("in=X,gamma,dY[,acc] out=dX[,dgamma[,dbeta]]");
     const Value &X = val(op.ins[0]);
+    if (op.ins.size() > 3 && val(op.ins[3]).row_stride() != X.row_stride())
+      return bad("rmsnorm_grad: acc must have the row stride of X");
     BwppRmsnormParams rp = {(uint32_t)X.rows(), (uint32_t)X.cols(), (uint32_t)X.row_stride(), (float)num("eps", 1e-5)};
-    s = BWPP_PLAN_CALL(bwpp_hip_dispatch_rmsnorm_grad(h, f32(op.ins[0]), f32(op.ins[1]), f32(op.ins[2]), f32(op.outs[0]),
-                                       op.outs.size() > 1 ? f32(op.outs[1]) : nullptr,
-                                       op.outs.size() > 2 ? f32(op.outs[2]) : nullptr, rp));
+    s = BWPP_PLAN_CALL(bwpp_hip_dispatch_rmsnorm_grad_acc(
+        h, f32(op.ins[0]), f32(op.ins[1]), f32(op.ins[2]), op.ins.size() > 3 ? f32(op.ins[3]) : nullptr,
+        f32(op.outs[0]), op.outs.size() > 1 ? f32(op.outs[1]) : nullptr, op.outs.size() > 2 ? f32(op.outs[2]) : nullptr,
+        rp));
   } else if (k == "attention" || k == "attention_grad") {
     // q / k / v (and o, do, dq, dk, dv) are [batch*seq, heads*dim] row
     // blocks: head h of a row starts at column h*dim.

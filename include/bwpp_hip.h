@@ -459,6 +459,17 @@ BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad(BwppHip *h, const float *x, const f
                                              const float *dy, float *dx, float *dgamma,
                                              float *dbeta, BwppRmsnormParams params);
 
+/* bwpp_hip_dispatch_rmsnorm_grad with dx = acc + the gradient: the
+ * autodiff graph's add of the residual branch's gradient
+ * (graph_ir.c:1529-1545, ADD of the two gradient contributions to x) folded
+ * into the same pass, with one fp32 rounding like the separate add.  acc has
+ * dx's layout (row stride params.ld) and may be dx itself; NULL acc is
+ * bwpp_hip_dispatch_rmsnorm_grad. */
+BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad_acc(BwppHip *h, const float *x, const float *gamma,
+                                                 const float *dy, const float *acc, float *dx,
+                                                 float *dgamma, float *dbeta,
+                                                 BwppRmsnormParams params);
+
 /* BWPP_GOP_REDUCE_SUM / reduce_to_shape (graph_ir.c:1410-1455): axis 0 sums
  * over rows (out[cols]), any other axis along each row (out[rows]). */
 BwppHipStatus bwpp_hip_dispatch_reduce_sum(BwppHip *h, const float *x, float *out,

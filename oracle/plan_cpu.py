@@ -223,6 +223,8 @@ class CpuPlan:
             m(outs[0])[...] = o.softmax_grad(X[0], X[1])
         elif k == "rmsnorm_grad":
             dx, dg, db = o.rmsnorm_grad(X[0], X[1].reshape(-1), X[2], float(kv.get("eps", 1e-5)))
+            if len(X) > 3:  # residual gradient added in the same pass
+                dx = np.add(X[3].reshape(dx.shape), dx, dtype=np.float32)
             m(outs[0])[...] = dx
             if len(outs) > 1:
                 m(outs[1]).reshape(-1)[...] = dg

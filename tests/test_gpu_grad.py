@@ -102,6 +102,48 @@ def test_rmsnorm_grad_wave_rows(be, oracle, rows, cols, ld):
     assert rel_max_err(host(db), wdb) <= TOL
 
 
+@pytest.mark.parametrize("rows,cols,ld", [(1029, 512, 516), (4096, 1024, 1024), (7, 3000, 3000), (5, 37, 37)])
+def test_rmsnorm_grad_acc(be, oracle, rows, cols, ld):
+    """dx = acc + rmsnorm_grad: bit for bit the separate rmsnorm_grad
+    followed by the add (one fp32 rounding of each), on the wave-per-row
+    kernel (16-byte rows <= 2048 columns) and the generic one (3000 and 37
+    columns); acc may be dx itself (in place); the column sums are
+    unchanged; padding is untouched."""
+    torch = _torch()
+    x = synth.normal((rows, cols), rows, 0)
+    g = synth.uniform((cols,), cols, 1, 0.5, 1.5)
+    dy = synth.normal((rows, cols), rows, 2)
+    acc = synth.normal((rows, cols), rows, 3)
+    pad = lambda a: np.pad(a, ((0, 0), (0, ld - cols)))
+    prm = bwpp.RmsnormParams(rows, cols, ld, 1e-5)
+    xd, gd, dyd, accd = dev(pad(x)), dev(g), dev(pad(dy)), dev(pad(acc))
+    sep = torch.full((rows, ld), 5.0, device="cuda")
+    dg0, db0 = torch.zeros(cols, device="cuda"), torch.zeros(cols, device="cuda")
+    be.dispatch_rmsnorm_grad(xd, gd, dyd, sep, dg0, db0, prm)
+    want = np.add(acc, host(sep)[:, :cols], dtype=np.float32)
+    dx = torch.full((rows, ld), 5.0, device="cuda")
+    dg, db = torch.zeros(cols, device="cuda"), torch.zeros(cols, device="cuda")
+    be.dispatch_rmsnorm_grad_acc(xd, gd, dyd, accd, dx, dg, db, prm)
+    out = host(dx)
+    assert_bits_equal(out[:, :cols], want)
+    assert np.all(out[:, cols:] == 5.0)
+    assert_bits_equal(host(dg), host(dg0))
+    assert_bits_equal(host(db), host(db0))
+    wdx = oracle.rmsnorm_grad(x, g, dy, 1e-5)[0]
+    assert rel_max_err(out[:, :cols], np.add(acc, wdx, dtype=np.float32)) <= TOL
+    inplace = accd.clone()
+    be.dispatch_rmsnorm_grad_acc(xd, gd, dyd, inplace, inplace, None, None, prm)
+    assert_bits_equal(host(inplace)[:, :cols], want)
+
+
+def test_rmsnorm_grad_acc_alias(be):
+    torch = _torch()
+    buf = torch.zeros((9, 64), device="cuda")
+    x = torch.ones((8, 64), device="cuda")
+    with pytest.raises(bwpp.BwppError):  # acc overlaps dx one row apart
+        be.dispatch_rmsnorm_grad_acc(x, None, x, buf[1:], buf[:8], None, None, bwpp.RmsnormParams(8, 64, 64, 1e-5))
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 1), (7, 300), (4096, 1024), (1000, 3)])
 @pytest.mark.parametrize("axis", [0, 1])
 def test_reduce_sum(be, oracle, rows, cols, axis):

@@ -202,8 +202,9 @@ def test_grouped_projections_match_separate_gemms(bwppc, tmp_path):
 def test_fused_tails_match_separate_ops(bwppc, tmp_path):
     """x1 = x + ctx @ wo and out = x1 + h @ w2 (residual tails), h =
     silu(n2 @ w1) with the pre-activation kept for the backward (dual
-    output) and silu_grad(t, dO @ w2^T) (SiLU-gradient tail) give the same
-    step as the separate ops."""
+    output), silu_grad(t, dO @ w2^T) (SiLU-gradient tail) and the two
+    residual-gradient adds folded into rmsnorm_grad (its fourth input) give
+    the same step as the separate ops."""
     from blockref import block_inputs
     src = os.path.join(REFERENCE, "examples", "tiny_model.bwpp")
     B, T, D, H, HEADS = 2, 32, 48, 96, 3
@@ -213,8 +214,11 @@ def test_fused_tails_match_separate_ops(bwppc, tmp_path):
     plain = lower(bwppc, src, tmp_path, *dims, "--no-fuse-tails")
     for f in ("fuse=residual", "fuse=dual_silu", "fuse=silu_grad"):
         assert f in fused and f not in plain
+    n_in = lambda line: len(line.split(" in=")[1].split()[0].split(","))
+    acc = lambda t: [l for l in t.splitlines() if l.startswith("op rmsnorm_grad ") and n_in(l) == 4]
+    assert len(acc(fused)) == 2 and not acc(plain)
     n_ops = lambda t: sum(l.startswith("op ") for l in t.splitlines())
-    assert n_ops(plain) - n_ops(fused) == 4  # two adds, silu, silu_grad
+    assert n_ops(plain) - n_ops(fused) == 6  # two residual adds, silu, silu_grad, two gradient adds
     t = block_inputs(B, T, D, H, seed=12)
     runs = []
     for text in (fused, plain):
