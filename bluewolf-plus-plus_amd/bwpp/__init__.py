@@ -6,12 +6,13 @@ if the library or a code object is missing, HipBackend() raises.
 """
 from . import _lib, plan, synth
 from ._lib import (AttentionParams, CoreDType, DType, ElementwiseParams, Epilogue, Fusion,
-                   FusionParams, LibraryMissing, MatmulParams, ReduceParams, RmsnormParams,
-                   SoftmaxParams, Status, Tensor)
+                   FusionParams, LibraryMissing, MatmulParams, MeanSquareParams, ReduceParams,
+                   RmsnormParams, SoftmaxParams, Status, Tensor)
 from .backend import BwppError, HipBackend, tensor_of
 
 __all__ = ["HipBackend", "BwppError", "LibraryMissing", "Status", "DType",
            "Epilogue", "Fusion", "FusionParams", "MatmulParams", "SoftmaxParams", "RmsnormParams",
+           "MeanSquareParams",
            "AttentionParams", "ReduceParams", "ElementwiseParams", "CoreDType", "Tensor",
            "tensor_of", "synth", "plan",
            "load_library"]

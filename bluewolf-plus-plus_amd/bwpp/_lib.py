@@ -70,6 +70,10 @@ class RmsnormParams(Structure):
                 ("eps", c_float)]
 
 
+class MeanSquareParams(Structure):
+    _fields_ = [("rows", c_uint32), ("cols", c_uint32), ("ld", c_uint32)]
+
+
 class AttentionParams(Structure):
     _fields_ = [("M", c_uint32), ("N", c_uint32), ("K", c_uint32),
                 ("D", c_uint32), ("ldq", c_uint32), ("ldk", c_uint32),
@@ -178,6 +182,7 @@ SIGNATURES = {
     "bwpp_hip_dispatch_softmax_grad": (c_int, [_P, _P, _P, _P, SoftmaxParams]),
     "bwpp_hip_dispatch_rmsnorm_grad": (c_int, [_P, _P, _P, _P, _P, _P, _P, RmsnormParams]),
     "bwpp_hip_dispatch_rmsnorm_grad_acc": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, RmsnormParams]),
+    "bwpp_hip_dispatch_mean_square": (c_int, [_P, _P, _P, _P, _P, _P, MeanSquareParams]),
     "bwpp_hip_dispatch_reduce_sum": (c_int, [_P, _P, _P, ReduceParams]),
     "bwpp_hip_dispatch_elementwise": (c_int, [_P, _P, _P, _P, ElementwiseParams]),
     "bwpp_synth_uniform_f32": (None, [_P, c_uint64, c_uint64, c_uint64, c_float, c_float]),
@@ -222,7 +227,7 @@ def load():
 
 
 __all__ = ["Status", "DType", "Epilogue", "MatmulParams", "Fusion", "FusionParams", "SoftmaxParams",
-           "RmsnormParams", "AttentionParams", "ReduceParams", "ElementwiseParams", "Arena",
+           "RmsnormParams", "MeanSquareParams", "AttentionParams", "ReduceParams", "ElementwiseParams", "Arena",
            "CoreDType", "Tensor",
            "SIGNATURES", "load", "LIB_PATH", "LIB_DIR", "HEADER_PATH",
            "LibraryMissing", "byref", "c_void_p", "c_uint16"]

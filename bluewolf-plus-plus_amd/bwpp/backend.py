@@ -177,6 +177,11 @@ class HipBackend:
         self._check(self.lib.bwpp_hip_dispatch_rmsnorm_grad_acc(
             self._h, _ptr(x), _ptr(gamma), _ptr(dy), _ptr(acc), _ptr(dx), _ptr(dgamma), _ptr(dbeta), params))
 
+    def dispatch_mean_square(self, x, loss_scale, grad_scale, loss, dx, params):
+        """loss[0] = loss_scale * sum(x^2); dx = grad_scale * x (scales: device scalars or None = 1)."""
+        self._check(self.lib.bwpp_hip_dispatch_mean_square(
+            self._h, _ptr(x), _ptr(loss_scale), _ptr(grad_scale), _ptr(loss), _ptr(dx), params))
+
     def dispatch_reduce_sum(self, x, out, params: ReduceParams):
         self._check(self.lib.bwpp_hip_dispatch_reduce_sum(self._h, _ptr(x), _ptr(out), params))
 

@@ -1783,30 +1783,44 @@ BwppStatus bwpp_codegen_hip(const BwppGraph *graph, const BwppGraph *grad, const
       }
       Shape one;
       memset(&one, 0, sizeof one);
-      const int sq = new_pv(&c, "sq", &O->shape, O->batched, 0, "temp");
-      emit(&c, "op mul out=%s in=%s,%s bcast=full\n", ref(sq).s, ref(O->pv).s, ref(O->pv).s);
-      int sum_in = sq;
-      if (O->shape.rank >= 2) {
-        Shape rows = O->shape;
-        rows.rank = O->shape.rank - 1;
-        const int rs = new_pv(&c, "rowsum", &rows, O->batched, 0, "temp");
-        emit(&c, "op reduce_sum out=%s in=%s axis=1\n", ref(rs).s, ref(sq).s);
-        sum_in = rs;
-      }
-      const int total = new_pv(&c, "total", &one, 0, 0, "temp");
-      emit(&c, "op reduce_sum out=%s in=%s axis=1\n", ref(total).s, ref(sum_in).s);
       char kind[4 * DIM_LEN + 16];
-      snprintf(kind, sizeof kind, "const=1/%s", nexpr);
-      const int inv = new_pv(&c, "inv_n", &one, 0, 0, kind);
-      const int loss = new_pv(&c, "loss", &one, 0, 0, "output");
-      pv_is_out[loss] = 1;
-      emit(&c, "op mul out=%s in=%s,%s bcast=scalar\n", ref(loss).s, ref(total).s, ref(inv).s);
-      snprintf(kind, sizeof kind, "const=2/%s", nexpr);
-      const int two = new_pv(&c, "two_n", &one, 0, 0, kind);
       char dn[NAME_LEN + 8];
       snprintf(dn, sizeof dn, "d%s", oname);
-      seed_pv = new_pv(&c, dn, &O->shape, O->batched, 0, "temp");
-      emit(&c, "op mul out=%s in=%s,%s bcast=scalar\n", ref(seed_pv).s, ref(O->pv).s, ref(two).s);
+      if (opt->fuse_tails) {
+        /* one pass over the output: loss = (1/n) sum out^2 and the seed
+         * d<out> = (2/n) out (the graph ops below, fused) */
+        snprintf(kind, sizeof kind, "const=1/%s", nexpr);
+        const int inv = new_pv(&c, "inv_n", &one, 0, 0, kind);
+        snprintf(kind, sizeof kind, "const=2/%s", nexpr);
+        const int two = new_pv(&c, "two_n", &one, 0, 0, kind);
+        const int loss = new_pv(&c, "loss", &one, 0, 0, "output");
+        pv_is_out[loss] = 1;
+        seed_pv = new_pv(&c, dn, &O->shape, O->batched, 0, "temp");
+        emit(&c, "op mean_square out=%s,%s in=%s,%s,%s\n", ref(loss).s, ref(seed_pv).s, ref(O->pv).s, ref(inv).s,
+             ref(two).s);
+      } else {
+        const int sq = new_pv(&c, "sq", &O->shape, O->batched, 0, "temp");
+        emit(&c, "op mul out=%s in=%s,%s bcast=full\n", ref(sq).s, ref(O->pv).s, ref(O->pv).s);
+        int sum_in = sq;
+        if (O->shape.rank >= 2) {
+          Shape rows = O->shape;
+          rows.rank = O->shape.rank - 1;
+          const int rs = new_pv(&c, "rowsum", &rows, O->batched, 0, "temp");
+          emit(&c, "op reduce_sum out=%s in=%s axis=1\n", ref(rs).s, ref(sq).s);
+          sum_in = rs;
+        }
+        const int total = new_pv(&c, "total", &one, 0, 0, "temp");
+        emit(&c, "op reduce_sum out=%s in=%s axis=1\n", ref(total).s, ref(sum_in).s);
+        snprintf(kind, sizeof kind, "const=1/%s", nexpr);
+        const int inv = new_pv(&c, "inv_n", &one, 0, 0, kind);
+        const int loss = new_pv(&c, "loss", &one, 0, 0, "output");
+        pv_is_out[loss] = 1;
+        emit(&c, "op mul out=%s in=%s,%s bcast=scalar\n", ref(loss).s, ref(total).s, ref(inv).s);
+        snprintf(kind, sizeof kind, "const=2/%s", nexpr);
+        const int two = new_pv(&c, "two_n", &one, 0, 0, kind);
+        seed_pv = new_pv(&c, dn, &O->shape, O->batched, 0, "temp");
+        emit(&c, "op mul out=%s in=%s,%s bcast=scalar\n", ref(seed_pv).s, ref(O->pv).s, ref(two).s);
+      }
     } else {
       char dn[NAME_LEN + 8];
       snprintf(dn, sizeof dn, "d%s", oname);

@@ -118,6 +118,7 @@ typedef struct {
                        rows (elementwise) */
   uint32_t ldb;     /* elementwise, full broadcast: row stride of b */
   const float *acc; /* rmsnorm_grad: added to dx (row stride ld; may equal out) */
+  const float *s_loss, *s_grad; /* mean_square: device scalars (NULL = 1) */
 } BwppGradArgs;
 
 #endif /* BWPP_KARGS_H */

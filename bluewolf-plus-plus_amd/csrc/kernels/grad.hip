@@ -66,6 +66,44 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_softmax_grad(const BwppGr
   }
 }
 
+// Mean-square loss and its gradient in one pass over x: block b adds x^2
+// over its rows (rows b, b + grid, ...; thread order fixed) into partial
+// part_g[b] and, with out, writes dx = x * s_grad; bwpp_mean_square_final
+// then sums the partials in index order.  Deterministic for a given grid.
+extern "C" __global__ __launch_bounds__(256) void bwpp_mean_square_part(const BwppGradArgs g) {
+  __shared__ float red[4];
+  const float gs = g.s_grad ? *g.s_grad : 1.0f;
+  float acc = 0.0f;
+  for (uint32_t r = blockIdx.x; r < g.rows; r += gridDim.x) {
+    const float *x = g.a + (size_t)r * g.ld;
+    float *dx = g.out ? g.out + (size_t)r * g.ld : nullptr;
+    if (g.vec) {  // 16-byte rows
+      for (uint32_t c = 4u * threadIdx.x; c < g.cols; c += 1024u) {
+        const float4 v = *reinterpret_cast<const float4 *>(x + c);
+        acc += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+        if (dx) *reinterpret_cast<float4 *>(dx + c) = make_float4(v.x * gs, v.y * gs, v.z * gs, v.w * gs);
+      }
+    } else {
+      for (uint32_t c = threadIdx.x; c < g.cols; c += 256u) {
+        const float v = x[c];
+        acc += v * v;
+        if (dx) dx[c] = v * gs;
+      }
+    }
+  }
+  acc = block_sum256(acc, red);
+  if (threadIdx.x == 0) g.part_g[blockIdx.x] = acc;
+}
+
+// out2[0] = s_loss * (sum of the nparts partials), one block.
+extern "C" __global__ __launch_bounds__(256) void bwpp_mean_square_final(const BwppGradArgs g) {
+  __shared__ float red[4];
+  float acc = 0.0f;
+  for (uint32_t i = threadIdx.x; i < g.nparts; i += 256u) acc += g.part_g[i];
+  acc = block_sum256(acc, red);
+  if (threadIdx.x == 0) g.out2[0] = acc * (g.s_loss ? *g.s_loss : 1.0f);
+}
+
 // Row-wise rmsnorm_grad with per-block column partials of dgamma / dbeta
 // (summed by bwpp_col_partials_sum).  gamma NULL means 1; with g.acc,
 // dx = acc + the gradient (the residual branch's gradient added in the same

@@ -97,7 +97,8 @@ struct BwppHip {
   hipFunction_t attn_conv_to_f32 = nullptr, attn_conv_to_bf16 = nullptr;  // bf16 <-> fp32 operand copies
   hipFunction_t rmsnorm_grad_w[4] = {};  // wave-per-row rmsnorm_grad, 256 / 512 / 1024 / 2048 columns
   hipFunction_t silu_grad = nullptr, softmax_grad = nullptr, rmsnorm_grad = nullptr, col_partials_sum = nullptr,
-                reduce_sum_rows = nullptr, reduce_sum_cols = nullptr, elementwise = nullptr;
+                reduce_sum_rows = nullptr, reduce_sum_cols = nullptr, elementwise = nullptr,
+                mean_square_part = nullptr, mean_square_final = nullptr;
   // Library-owned device workspace (column partials), grown on demand and
   // freed by bwpp_hip_destroy.  Calls on one handle are stream-ordered, so
   // reuse across calls is safe.
@@ -192,6 +193,7 @@ BwppHipStatus resolve_all(BwppHip *h) {
       {"bwpp_silu_grad", &h->silu_grad},             {"bwpp_softmax_grad", &h->softmax_grad},
       {"bwpp_rmsnorm_grad", &h->rmsnorm_grad},       {"bwpp_col_partials_sum", &h->col_partials_sum},
       {"bwpp_reduce_sum_rows", &h->reduce_sum_rows}, {"bwpp_reduce_sum_cols", &h->reduce_sum_cols},
+      {"bwpp_mean_square_part", &h->mean_square_part}, {"bwpp_mean_square_final", &h->mean_square_final},
       {"bwpp_elementwise", &h->elementwise},         {"bwpp_gemm_f32_splitk_reduce", &h->gemm_f32_reduce},
       {"bwpp_rmsnorm_grad_w1", &h->rmsnorm_grad_w[0]}, {"bwpp_rmsnorm_grad_w2", &h->rmsnorm_grad_w[1]},
       {"bwpp_rmsnorm_grad_w4", &h->rmsnorm_grad_w[2]}, {"bwpp_rmsnorm_grad_w8", &h->rmsnorm_grad_w[3]},
@@ -1390,6 +1392,36 @@ extern "C" BwppHipStatus bwpp_hip_dispatch_reduce_sum(BwppHip *h, const float *x
   r.cols = p.cols;
   r.nparts = bands;
   return launch(h, h->col_partials_sum, (p.cols + 15) / 16, 1, 1, 256, r);
+}
+
+extern "C" BwppHipStatus bwpp_hip_dispatch_mean_square(BwppHip *h, const float *x, const float *loss_scale,
+                                                       const float *grad_scale, float *loss, float *dx,
+                                                       BwppMeanSquareParams p) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (!x || (!loss && !dx)) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "mean_square: NULL x or no output");
+  const uint32_t ld = eff_ld(p.ld, p.cols);
+  if ((s = check_rows(h, p.rows, p.cols, ld)) != BWPP_HIP_OK) return s;
+  if (dx && dx != x && overlaps(extent(dx, p.rows, p.cols, ld, 4), extent(x, p.rows, p.cols, ld, 4)))
+    return fail(h, BWPP_HIP_ERR_ALIAS, "mean_square: dx overlaps x without being x");
+  BwppGradArgs g = {};
+  g.a = x;
+  g.out = dx;
+  g.out2 = loss;
+  g.s_loss = loss_scale;
+  g.s_grad = grad_scale;
+  g.rows = p.rows;
+  g.cols = p.cols;
+  g.ld = ld;
+  g.vec = (p.cols % 4 == 0 && ld % 4 == 0 && aligned16(x) && (!dx || aligned16(dx))) ? 1u : 0u;
+  const uint32_t cap = h->cus > 0 ? 4u * (uint32_t)h->cus : 1024u;
+  const uint32_t grid = std::max<uint32_t>(1u, std::min<uint32_t>(p.rows, cap));
+  if ((s = ensure_ws(h, (size_t)grid * sizeof(float))) != BWPP_HIP_OK) return s;
+  g.part_g = static_cast<float *>(h->ws);
+  g.nparts = grid;
+  if ((s = launch(h, h->mean_square_part, grid, 1, 1, 256, g)) != BWPP_HIP_OK) return s;
+  if (!loss) return BWPP_HIP_OK;
+  return launch(h, h->mean_square_final, 1, 1, 1, 256, g);
 }
 
 extern "C" BwppHipStatus bwpp_hip_dispatch_elementwise(BwppHip *h, const float *a, const float *b, float *out,

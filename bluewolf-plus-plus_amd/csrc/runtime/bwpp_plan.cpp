@@ -18,8 +18,9 @@
 //   op KIND out=A[,B..] in=X[,Y..] [key=value ...]
 // Op kinds: matmul (ta, tb, epi, fuse), softmax, rmsnorm, layernorm,
 // add / sub / mul / div / copy / silu (bcast), reduce_sum, reduce_max,
-// reduce_max_mask (axis), silu_grad, softmax_grad, rmsnorm_grad,
-// attention, attention_grad (batch, heads, causal, scale, layout).
+// reduce_max_mask (axis), mean_square, silu_grad, softmax_grad,
+// rmsnorm_grad, attention, attention_grad (batch, heads, causal, scale,
+// layout).
 // Tensors are row-major; row operators see [rows, cols] with cols the last
 // dim and rows the product of the others; a view is a 2-D strided window
 // (offset and row stride ld in elements) into another tensor's storage.
@@ -670,6 +671,21 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
     BwppReduceParams rp = {(uint32_t)X.rows(), (uint32_t)X.cols(), (uint32_t)X.row_stride(),
                            (int32_t)num("axis", 1)};
     s = BWPP_PLAN_CALL(bwpp_hip_dispatch_reduce_sum(h, f32(op.ins[0]), f32(op.outs[0]), rp));
+  } else if (k == "mean_square") {
+    // loss = loss_scale * sum(X^2) (one element) and dX = grad_scale * X;
+    // the scales are one-element values (consts), absent = 1.
+    if (!need(1, 1) || op.ins.size() > 3 || op.outs.size() > 2)
+      return bad("in=X[,loss_scale[,grad_scale]] out=loss[,dX]");
+    const Value &X = val(op.ins[0]);
+    if (val(op.outs[0]).elems() != 1) return bad("mean_square: loss must have one element");
+    if (op.outs.size() > 1 && (val(op.outs[1]).elems() != X.elems() || val(op.outs[1]).row_stride() != X.row_stride()))
+      return bad("mean_square: dX must have X's shape and row stride");
+    for (size_t i = 1; i < op.ins.size(); ++i)
+      if (val(op.ins[i]).elems() != 1) return bad("mean_square: scales must have one element");
+    BwppMeanSquareParams mp = {(uint32_t)X.rows(), (uint32_t)X.cols(), (uint32_t)X.row_stride()};
+    s = BWPP_PLAN_CALL(bwpp_hip_dispatch_mean_square(h, f32(op.ins[0]), op.ins.size() > 1 ? f32(op.ins[1]) : nullptr,
+                                                     op.ins.size() > 2 ? f32(op.ins[2]) : nullptr, f32(op.outs[0]),
+                                                     op.outs.size() > 1 ? f32(op.outs[1]) : nullptr, mp));
   } else if (k == "reduce_max" || k == "reduce_max_mask") {
     // Graph ops BWPP_GOP_REDUCE_MAX (values; graph_ir.c:663-695) and
     // BWPP_GOP_REDUCE_MAX_MASK (bwpp_cpu_ref.c:146-190) along `axis`.

@@ -470,6 +470,24 @@ BwppHipStatus bwpp_hip_dispatch_rmsnorm_grad_acc(BwppHip *h, const float *x, con
                                                  float *dgamma, float *dbeta,
                                                  BwppRmsnormParams params);
 
+/* Mean-square training loss and its gradient, the loss the HIP target's
+ * `--train mean_square` appends (no reference counterpart: the reference
+ * compiler has no loss; the C5 configuration names loss = mean(out^2)):
+ * loss[0] = loss_scale * sum of x^2 over rows x cols, and dx = grad_scale * x
+ * when dx is non-NULL (dx may be x).  The scales are device scalars (NULL
+ * = 1), e.g. 1/n and 2/n.  One pass over x plus a one-block finish; the sum
+ * is taken in a fixed order (deterministic for a given device).  Either
+ * output may be NULL, not both. */
+typedef struct {
+  uint32_t rows;
+  uint32_t cols;
+  uint32_t ld; /* row stride of x and dx; 0 = cols */
+} BwppMeanSquareParams;
+
+BwppHipStatus bwpp_hip_dispatch_mean_square(BwppHip *h, const float *x, const float *loss_scale,
+                                            const float *grad_scale, float *loss, float *dx,
+                                            BwppMeanSquareParams params);
+
 /* BWPP_GOP_REDUCE_SUM / reduce_to_shape (graph_ir.c:1410-1455): axis 0 sums
  * over rows (out[cols]), any other axis along each row (out[rows]). */
 BwppHipStatus bwpp_hip_dispatch_reduce_sum(BwppHip *h, const float *x, float *out,

@@ -217,6 +217,13 @@ class CpuPlan:
                 m(outs[0]).reshape(-1)[...] = o.reduce_max(x, 0 if axis == 0 else 1)[0]
             else:
                 m(outs[0])[...] = o.reduce_max_mask(x, 0 if axis == 0 else 1)
+        elif k == "mean_square":  # loss = s_l * sum(x^2) (fp64 sum), dX = s_g * x (fp32 product)
+            x = np.ascontiguousarray(X[0], np.float32)
+            sl = float(X[1].reshape(-1)[0]) if len(X) > 1 else 1.0
+            sg = np.float32(X[2].reshape(-1)[0]) if len(X) > 2 else np.float32(1.0)
+            m(outs[0]).reshape(-1)[0] = np.float32(np.sum(x.astype(np.float64) ** 2) * sl)
+            if len(outs) > 1:
+                m(outs[1])[...] = (x * sg).reshape(m(outs[1]).shape)
         elif k == "silu_grad":
             m(outs[0])[...] = o.silu_grad(X[0], X[1]).reshape(m(outs[0]).shape)
         elif k == "softmax_grad":

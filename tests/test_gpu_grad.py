@@ -136,6 +136,44 @@ def test_rmsnorm_grad_acc(be, oracle, rows, cols, ld):
     assert_bits_equal(host(inplace)[:, :cols], want)
 
 
+@pytest.mark.parametrize("rows,cols,ld", [(4096, 1024, 1024), (333, 100, 104), (7, 3, 3), (1, 5, 5), (5000, 37, 37)])
+def test_mean_square(be, rows, cols, ld):
+    """loss = s_l * sum(x^2) against an fp64 sum, dX = s_g * x bit for bit
+    (one fp32 product), on the 16-byte path and the scalar one (odd
+    columns); dX in place (= x); either output alone; NULL scales = 1."""
+    torch = _torch()
+    x = synth.normal((rows, cols), rows + cols, 0, 0.0, 2.0)
+    n = rows * cols
+    sl = torch.tensor([1.0 / n], device="cuda")
+    sg = torch.tensor([2.0 / n], device="cuda")
+    xd = dev(np.pad(x, ((0, 0), (0, ld - cols)), constant_values=7.0))
+    prm = bwpp.MeanSquareParams(rows, cols, ld)
+    loss = torch.full((1,), 9.0, device="cuda")
+    dx = torch.full((rows, ld), 5.0, device="cuda")
+    be.dispatch_mean_square(xd, sl, sg, loss, dx, prm)
+    want = np.sum(x.astype(np.float64) ** 2) * np.float64(np.float32(1.0 / n))
+    assert abs(float(host(loss)[0]) - want) <= 1e-5 * want
+    out = host(dx)
+    assert_bits_equal(out[:, :cols], x * np.float32(2.0 / n))
+    assert np.all(out[:, cols:] == 5.0)
+    l2 = torch.full((1,), 9.0, device="cuda")
+    be.dispatch_mean_square(xd, None, None, l2, None, prm)  # loss alone, scales 1
+    assert abs(float(host(l2)[0]) - np.sum(x.astype(np.float64) ** 2)) <= 1e-5 * np.sum(x.astype(np.float64) ** 2)
+    inplace = xd.clone()
+    be.dispatch_mean_square(inplace, None, sg, None, inplace, prm)  # dX alone, in place
+    assert_bits_equal(host(inplace)[:, :cols], x * np.float32(2.0 / n))
+
+
+def test_mean_square_errors(be):
+    torch = _torch()
+    x = torch.ones((8, 64), device="cuda")
+    with pytest.raises(bwpp.BwppError):  # no output
+        be.dispatch_mean_square(x, None, None, None, None, bwpp.MeanSquareParams(8, 64, 64))
+    buf = torch.zeros((9, 64), device="cuda")
+    with pytest.raises(bwpp.BwppError):  # dX overlaps X one row apart
+        be.dispatch_mean_square(buf[:8], None, None, None, buf[1:], bwpp.MeanSquareParams(8, 64, 64))
+
+
 def test_rmsnorm_grad_acc_alias(be):
     torch = _torch()
     buf = torch.zeros((9, 64), device="cuda")

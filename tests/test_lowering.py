@@ -202,9 +202,11 @@ def test_grouped_projections_match_separate_gemms(bwppc, tmp_path):
 def test_fused_tails_match_separate_ops(bwppc, tmp_path):
     """x1 = x + ctx @ wo and out = x1 + h @ w2 (residual tails), h =
     silu(n2 @ w1) with the pre-activation kept for the backward (dual
-    output), silu_grad(t, dO @ w2^T) (SiLU-gradient tail) and the two
-    residual-gradient adds folded into rmsnorm_grad (its fourth input) give
-    the same step as the separate ops."""
+    output), silu_grad(t, dO @ w2^T) (SiLU-gradient tail), the two
+    residual-gradient adds folded into rmsnorm_grad (its fourth input) and
+    the mean-square loss with its seed gradient in one pass give the same
+    step as the separate ops (dout and every gradient bit for bit: only the
+    loss's sum order differs)."""
     from blockref import block_inputs
     src = os.path.join(REFERENCE, "examples", "tiny_model.bwpp")
     B, T, D, H, HEADS = 2, 32, 48, 96, 3
@@ -217,8 +219,10 @@ def test_fused_tails_match_separate_ops(bwppc, tmp_path):
     n_in = lambda line: len(line.split(" in=")[1].split()[0].split(","))
     acc = lambda t: [l for l in t.splitlines() if l.startswith("op rmsnorm_grad ") and n_in(l) == 4]
     assert len(acc(fused)) == 2 and not acc(plain)
+    assert "op mean_square out=loss,dout in=out,inv_n,two_n" in fused and "op mean_square" not in plain
     n_ops = lambda t: sum(l.startswith("op ") for l in t.splitlines())
-    assert n_ops(plain) - n_ops(fused) == 6  # two residual adds, silu, silu_grad, two gradient adds
+    # two residual adds, silu, silu_grad, two gradient adds; the loss's 5 ops -> 1
+    assert n_ops(plain) - n_ops(fused) == 6 + 4
     t = block_inputs(B, T, D, H, seed=12)
     runs = []
     for text in (fused, plain):
