@@ -1645,6 +1645,63 @@ void bwpp_lower_options_init(BwppLowerOptions *opt) {
   opt->fuse_tails = 1;
 }
 
+/* Plan value a copy touches: the value, or the base a view looks into. */
+static int pv_base(const Ctx *c, int pv) { return c->pv[pv].view_of >= 0 ? c->pv[pv].view_of : pv; }
+
+/* Runs of consecutive single-pair full copies (`op copy out=$A$ in=$B$
+ * bcast=full`) become one multi-pair copy of up to 4 pairs, one launch
+ * instead of one per pair (the weights into their concatenation, the
+ * concatenated gradient out to its blocks), as long as no pair writes a
+ * value (or the base of a view) that another pair of the run reads or
+ * writes. */
+static void merge_copies(Ctx *c) {
+  if (!c->ops) return;
+  char *outbuf = (char *)malloc(c->ops_len + 1);
+  if (!outbuf) {
+    fail(c, "out of memory");
+    return;
+  }
+  size_t olen = 0;
+  const char *s = c->ops;
+  int run_o[4], run_i[4], nrun = 0;
+  while (*s || nrun) {
+    const char *e = *s ? strchr(s, '\n') : NULL;
+    const size_t len = e ? (size_t)(e - s) + 1 : strlen(s);
+    int o = -1, i = -1, end = 0;
+    const int is_copy = *s && sscanf(s, "op copy out=$%d$ in=$%d$ bcast=full%n", &o, &i, &end) == 2 &&
+                        (s[end] == '\n' || s[end] == '\0');
+    int ok = is_copy && nrun < 4;
+    for (int k = 0; ok && k < nrun; ++k) {
+      const int bo = pv_base(c, o), bi = pv_base(c, i);
+      if (pv_base(c, run_o[k]) == bi || pv_base(c, run_i[k]) == bo || run_o[k] == o) ok = 0;
+    }
+    if (ok) {
+      run_o[nrun] = o;
+      run_i[nrun] = i;
+      ++nrun;
+      s += len;
+      continue;
+    }
+    if (nrun) {  /* flush the run */
+      olen += (size_t)sprintf(outbuf + olen, "op copy out=");
+      for (int k = 0; k < nrun; ++k) olen += (size_t)sprintf(outbuf + olen, "%s$%d$", k ? "," : "", run_o[k]);
+      olen += (size_t)sprintf(outbuf + olen, " in=");
+      for (int k = 0; k < nrun; ++k) olen += (size_t)sprintf(outbuf + olen, "%s$%d$", k ? "," : "", run_i[k]);
+      olen += (size_t)sprintf(outbuf + olen, " bcast=full\n");
+      nrun = 0;
+      continue;  /* the current line is looked at again */
+    }
+    memcpy(outbuf + olen, s, len);
+    olen += len;
+    s += len;
+  }
+  outbuf[olen] = '\0';
+  free(c->ops);
+  c->ops = outbuf;
+  c->ops_len = olen;
+  c->ops_cap = c->ops_len + 1;
+}
+
 static void render(Ctx *c, FILE *out) {
   /* final names: outputs, inputs, params and consts keep theirs (made
    * unique in that order), temps take what is left */
@@ -1904,6 +1961,7 @@ BwppStatus bwpp_codegen_hip(const BwppGraph *graph, const BwppGraph *grad, const
   }
 
 done:
+  if (!c.failed) merge_copies(&c);
   if (!c.failed) render(&c, out);
   gctx_free(&fc);
   if (gcx.g) gctx_free(&gcx);

@@ -121,4 +121,16 @@ typedef struct {
   const float *s_loss, *s_grad; /* mean_square: device scalars (NULL = 1) */
 } BwppGradArgs;
 
+/* Up to four strided copies in one launch (bwpp_copy_multi): segment s
+ * copies rows row0[s] .. row0[s+1]-1 of the launch's row space. */
+#define BWPP_COPY_MULTI_MAX 4
+typedef struct {
+  const float *src[BWPP_COPY_MULTI_MAX];
+  float *dst[BWPP_COPY_MULTI_MAX];
+  uint32_t ld_src[BWPP_COPY_MULTI_MAX], ld_dst[BWPP_COPY_MULTI_MAX], cols[BWPP_COPY_MULTI_MAX];
+  uint32_t row0[BWPP_COPY_MULTI_MAX + 1];
+  uint32_t n;   /* segments */
+  uint32_t vec; /* 1: every segment has 16-byte rows (cols, strides, pointers) */
+} BwppCopyArgs;
+
 #endif /* BWPP_KARGS_H */

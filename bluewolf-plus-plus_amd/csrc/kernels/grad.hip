@@ -273,7 +273,25 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_col_partials_sum(const Bw
   const uint32_t c = blockIdx.x * 16u + cl;
   float sg = 0.0f, sb = 0.0f;
   if (c < g.cols) {
-    for (uint32_t p = grp; p < g.nparts; p += 16) {
+    // Eight parts' loads issued before their adds (same order of addition
+    // as one at a time): the loop is bound by the L2 round trip, not by
+    // bandwidth, and a load-add-wait per part took 32 round trips at 512
+    // parts.
+    uint32_t p = grp;
+    for (; p + 16u * 7u < g.nparts; p += 16u * 8u) {
+      float a[8], b[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        a[i] = g.part_g[(size_t)(p + 16u * i) * g.cols + c];
+        b[i] = g.part_b[(size_t)(p + 16u * i) * g.cols + c];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        sg += a[i];
+        sb += b[i];
+      }
+    }
+    for (; p < g.nparts; p += 16u) {
       sg += g.part_g[(size_t)p * g.cols + c];
       sb += g.part_b[(size_t)p * g.cols + c];
     }
@@ -362,6 +380,27 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_elementwise(const BwppGra
         default: bv = g.b[0]; break;
       }
       orow[c] = ew1(g.op, ar ? ar[c] : 0.0f, bv);
+    }
+  }
+}
+
+// Several row-strided copies in one launch (the plan's multi-pair copy:
+// weights into their column blocks of a concatenation, or the blocks of a
+// concatenated gradient out to the separate outputs).  Block rows stride
+// over the segments' rows laid end to end.
+extern "C" __global__ __launch_bounds__(256) void bwpp_copy_multi(const BwppCopyArgs a) {
+  const uint32_t total = a.row0[a.n];
+  for (uint32_t r = blockIdx.x; r < total; r += gridDim.x) {
+    uint32_t sg = 0;
+    while (sg + 1 < a.n && r >= a.row0[sg + 1]) ++sg;
+    const uint32_t rr = r - a.row0[sg], cols = a.cols[sg];
+    const float *src = a.src[sg] + (size_t)rr * a.ld_src[sg];
+    float *dst = a.dst[sg] + (size_t)rr * a.ld_dst[sg];
+    if (a.vec) {
+      for (uint32_t c = threadIdx.x; c < cols / 4; c += 256)
+        reinterpret_cast<float4 *>(dst)[c] = reinterpret_cast<const float4 *>(src)[c];
+    } else {
+      for (uint32_t c = threadIdx.x; c < cols; c += 256) dst[c] = src[c];
     }
   }
 }

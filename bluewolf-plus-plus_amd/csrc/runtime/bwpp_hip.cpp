@@ -98,7 +98,7 @@ struct BwppHip {
   hipFunction_t rmsnorm_grad_w[4] = {};  // wave-per-row rmsnorm_grad, 256 / 512 / 1024 / 2048 columns
   hipFunction_t silu_grad = nullptr, softmax_grad = nullptr, rmsnorm_grad = nullptr, col_partials_sum = nullptr,
                 reduce_sum_rows = nullptr, reduce_sum_cols = nullptr, elementwise = nullptr,
-                mean_square_part = nullptr, mean_square_final = nullptr;
+                mean_square_part = nullptr, mean_square_final = nullptr, copy_multi = nullptr;
   // Library-owned device workspace (column partials), grown on demand and
   // freed by bwpp_hip_destroy.  Calls on one handle are stream-ordered, so
   // reuse across calls is safe.
@@ -194,6 +194,7 @@ BwppHipStatus resolve_all(BwppHip *h) {
       {"bwpp_rmsnorm_grad", &h->rmsnorm_grad},       {"bwpp_col_partials_sum", &h->col_partials_sum},
       {"bwpp_reduce_sum_rows", &h->reduce_sum_rows}, {"bwpp_reduce_sum_cols", &h->reduce_sum_cols},
       {"bwpp_mean_square_part", &h->mean_square_part}, {"bwpp_mean_square_final", &h->mean_square_final},
+      {"bwpp_copy_multi", &h->copy_multi},
       {"bwpp_elementwise", &h->elementwise},         {"bwpp_gemm_f32_splitk_reduce", &h->gemm_f32_reduce},
       {"bwpp_rmsnorm_grad_w1", &h->rmsnorm_grad_w[0]}, {"bwpp_rmsnorm_grad_w2", &h->rmsnorm_grad_w[1]},
       {"bwpp_rmsnorm_grad_w4", &h->rmsnorm_grad_w[2]}, {"bwpp_rmsnorm_grad_w8", &h->rmsnorm_grad_w[3]},
@@ -682,6 +683,30 @@ Extent extent(const void *p, uint64_t rows, uint64_t cols, uint64_t ld, uint64_t
   return e;
 }
 bool overlaps(const Extent &a, const Extent &b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; }
+
+// Whether two row-strided blocks of es-byte elements share an element:
+// exact when their row strides are equal (column blocks of one wider
+// matrix interleave without touching), by byte range otherwise.
+bool blocks_overlap(const void *pa, uint64_t ra, uint64_t ca, uint64_t lda, const void *pb, uint64_t rb, uint64_t cb,
+                    uint64_t ldb, uint64_t es) {
+  if (!overlaps(extent(pa, ra, ca, lda, es), extent(pb, rb, cb, ldb, es))) return false;
+  if (lda != ldb || lda == 0) return true;
+  intptr_t db = (intptr_t)pb - (intptr_t)pa;
+  if (db % (intptr_t)es) return true;
+  int64_t d = db / (intptr_t)es;  // b's first element, in elements from a's
+  if (d < 0) {                    // make a the earlier block
+    d = -d;
+    std::swap(ra, rb);
+    std::swap(ca, cb);
+  }
+  const uint64_t ld = lda, q = (uint64_t)d / ld, r = (uint64_t)d % ld;
+  // b's row i covers columns [r, r + cb) of a's row q + i, spilling into
+  // columns [0, r + cb - ld) of row q + i + 1 when r + cb > ld.
+  auto rows_meet = [&](uint64_t first, uint64_t count) { return count > 0 && first < ra; };
+  if (r < ca && rows_meet(q, rb)) return true;
+  if (r + cb > ld && rows_meet(q + 1, rb)) return true;
+  return false;
+}
 
 BwppHipStatus ensure_ws(BwppHip *h, size_t bytes);
 
@@ -1448,4 +1473,38 @@ BwppHipStatus bwpp_hip_copy_strided(BwppHip *h, const float *src, uint32_t ld_sr
     return fail(h, BWPP_HIP_ERR_INVALID_ARG, "copy: row strides (%u, %u) below cols (%u)", ld_src, ld_dst, cols);
   if (rows == 0 || cols == 0) return BWPP_HIP_OK;
   return elementwise_launch(h, nullptr, src, ld_src, dst, ld_dst, rows, cols, BWPP_HIP_OP_COPY, BWPP_HIP_BCAST_FULL);
+}
+
+BwppHipStatus bwpp_hip_copy_strided_multi(BwppHip *h, uint32_t n, const float *const *src, const uint32_t *ld_src,
+                                          float *const *dst, const uint32_t *ld_dst, const uint32_t *rows,
+                                          const uint32_t *cols) {
+  BwppHipStatus s = enter(h);
+  if (s != BWPP_HIP_OK) return s;
+  if (n == 0 || n > BWPP_COPY_MULTI_MAX) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "copy: %u segments (1..4)", n);
+  BwppCopyArgs a = {};
+  a.n = n;
+  a.vec = 1;
+  uint64_t total = 0;
+  for (uint32_t i = 0; i < n; ++i) {
+    if (!src[i] || !dst[i]) return fail(h, BWPP_HIP_ERR_INVALID_ARG, "copy: NULL pointer");
+    if (ld_src[i] < cols[i] || ld_dst[i] < cols[i])
+      return fail(h, BWPP_HIP_ERR_INVALID_ARG, "copy: row strides (%u, %u) below cols (%u)", ld_src[i], ld_dst[i],
+                  cols[i]);
+    for (uint32_t j = 0; j < n; ++j)
+      if (blocks_overlap(dst[i], rows[i], cols[i], ld_dst[i], src[j], rows[j], cols[j], ld_src[j], 4) ||
+          (j != i && blocks_overlap(dst[i], rows[i], cols[i], ld_dst[i], dst[j], rows[j], cols[j], ld_dst[j], 4)))
+        return fail(h, BWPP_HIP_ERR_ALIAS, "copy: segment %u's destination overlaps another segment", i);
+    a.src[i] = src[i];
+    a.dst[i] = dst[i];
+    a.ld_src[i] = ld_src[i];
+    a.ld_dst[i] = ld_dst[i];
+    a.cols[i] = cols[i];
+    a.row0[i] = (uint32_t)total;
+    total += cols[i] ? rows[i] : 0u;
+    if (cols[i] % 4 || ld_src[i] % 4 || ld_dst[i] % 4 || !aligned16(src[i]) || !aligned16(dst[i])) a.vec = 0;
+  }
+  if (total > 0xffffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "copy: too many rows");
+  a.row0[n] = (uint32_t)total;
+  if (total == 0) return BWPP_HIP_OK;
+  return launch(h, h->copy_multi, row_grid(h, (uint32_t)total), 1, 1, 256, a);
 }

@@ -17,7 +17,8 @@
 //   view NAME of=BASE offset=EXPR ld=EXPR shape=[EXPR,EXPR]
 //   op KIND out=A[,B..] in=X[,Y..] [key=value ...]
 // Op kinds: matmul (ta, tb, epi, fuse), softmax, rmsnorm, layernorm,
-// add / sub / mul / div / copy / silu (bcast), reduce_sum, reduce_max,
+// add / sub / mul / div / copy / silu (bcast; copy may take up to 4
+// in/out pairs, one launch), reduce_sum, reduce_max,
 // reduce_max_mask (axis), mean_square, silu_grad, softmax_grad,
 // rmsnorm_grad, attention, attention_grad (batch, heads, causal, scale,
 // layout).
@@ -638,6 +639,27 @@ BwppHipStatus run_op(BwppHipPlan &p, const Op &op) {
       s = BWPP_PLAN_CALL(k == "rmsnorm" ? bwpp_hip_dispatch_rmsnorm(h, f32(op.ins[0]), g, bt, f32(op.outs[0]), rp)
                          : bwpp_hip_dispatch_layernorm(h, f32(op.ins[0]), g, bt, f32(op.outs[0]), rp));
     }
+  } else if (k == "copy" && (op.ins.size() > 1 || op.outs.size() > 1)) {
+    // several copies in one launch: pair i copies in[i] into out[i]
+    // (full shapes, any row strides; at most 4 pairs)
+    if (op.ins.size() != op.outs.size() || op.ins.size() > BWPP_COPY_MULTI_MAX)
+      return bad("multi-pair copy: in=X1,..,Xn out=Y1,..,Yn with n <= 4");
+    if (attr(op, "bcast", "full") != "full") return bad("multi-pair copy takes bcast=full");
+    const float *src[BWPP_COPY_MULTI_MAX];
+    float *dst[BWPP_COPY_MULTI_MAX];
+    uint32_t lds[BWPP_COPY_MULTI_MAX], ldd[BWPP_COPY_MULTI_MAX], rows[BWPP_COPY_MULTI_MAX], cols[BWPP_COPY_MULTI_MAX];
+    const uint32_t n = (uint32_t)op.ins.size();
+    for (uint32_t i = 0; i < n; ++i) {
+      const Value &X = val(op.ins[i]), &Y = val(op.outs[i]);
+      if (X.rows() != Y.rows() || X.cols() != Y.cols()) return bad("copy needs equal shapes");
+      src[i] = f32(op.ins[i]);
+      dst[i] = f32(op.outs[i]);
+      lds[i] = (uint32_t)X.row_stride();
+      ldd[i] = (uint32_t)Y.row_stride();
+      rows[i] = (uint32_t)Y.rows();
+      cols[i] = (uint32_t)Y.cols();
+    }
+    s = BWPP_PLAN_CALL(bwpp_hip_copy_strided_multi(h, n, src, lds, dst, ldd, rows, cols));
   } else if (k == "add" || k == "sub" || k == "mul" || k == "div" || k == "copy" || k == "silu") {
     const bool unary = k == "copy" || k == "silu";
     if (!need(unary ? 1 : 2, 1)) return bad("in=A,B (or in=B for copy / silu) out=C");

@@ -30,3 +30,12 @@ BwppHipStatus bwpp_hip_scratch_setup(int device, void **ptr, const char **why);
 // tensor and a strided view of another.
 BwppHipStatus bwpp_hip_copy_strided(BwppHip *h, const float *src, uint32_t ld_src, float *dst, uint32_t ld_dst,
                                     uint32_t rows, uint32_t cols);
+
+// n <= 4 such copies (segment i: src[i] -> dst[i], rows[i] x cols[i]) in
+// one launch.  The segments must not overlap one another's destinations.
+#ifndef BWPP_COPY_MULTI_MAX
+#define BWPP_COPY_MULTI_MAX 4
+#endif
+BwppHipStatus bwpp_hip_copy_strided_multi(BwppHip *h, uint32_t n, const float *const *src, const uint32_t *ld_src,
+                                          float *const *dst, const uint32_t *ld_dst, const uint32_t *rows,
+                                          const uint32_t *cols);

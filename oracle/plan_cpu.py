@@ -187,6 +187,10 @@ class CpuPlan:
             b = X[2].reshape(-1) if len(X) > 2 else None
             fn = o.rmsnorm if k == "rmsnorm" else o.layernorm
             m(outs[0])[...] = fn(np.ascontiguousarray(X[0]), g, b, float(kv.get("eps", 1e-5)))
+        elif k == "copy" and len(outs) > 1:  # pair i: in[i] -> out[i]
+            assert len(X) == len(outs) <= 4 and kv.get("bcast", "full") == "full"
+            for i, o_name in enumerate(outs):
+                m(o_name)[...] = X[i].reshape(m(o_name).shape)
         elif k in ("add", "sub", "mul", "div", "copy", "silu"):
             out = m(outs[0])
             bv = X[-1]

@@ -205,6 +205,67 @@ op copy out=back in=yc bcast=full
     p.close()
 
 
+@pytest.mark.parametrize("C", [6, 8])
+def test_multi_pair_copy(be, C):
+    """`op copy out=a,b,c in=x,y,z`: three copies in one launch, into
+    column blocks of a concatenation and back out of them (different row
+    strides per pair), on the scalar path (C = 6) and the 128-bit path
+    (C = 8); rows of unequal counts across the pairs."""
+    import torch
+    R = 7
+    text = f"""bwpp.plan 1
+dim R {R}
+dim C {C}
+value x f32 [R,C] input
+value y f32 [R,C] input
+value z f32 [R,C] input
+value w f32 [3,C] input
+value cat f32 [R,3*C] temp
+value whole f32 [R,3*C] output
+value bx f32 [R,C] output
+value bz f32 [R,C] output
+value w2 f32 [3,C] output
+view xc of=cat offset=0 ld=3*C shape=[R,C]
+view yc of=cat offset=C ld=3*C shape=[R,C]
+view zc of=cat offset=2*C ld=3*C shape=[R,C]
+op copy out=xc,yc,zc in=x,y,z bcast=full
+op copy out=whole in=cat bcast=full
+op copy out=bx,bz,w2 in=xc,zc,w bcast=full
+"""
+    x, y, z = (synth.normal((R, C), i, 0) for i in range(3))
+    w = synth.normal((3, C), 9, 0)
+    p = plan.Plan(be, text)
+    p.allocate()
+    for n, a in (("x", x), ("y", y), ("z", z), ("w", w)):
+        p.bind(n, torch.from_numpy(a).cuda())
+    p.run()
+    assert np.array_equal(p.host("whole", (R, 3 * C)), np.hstack([x, y, z]))
+    assert np.array_equal(p.host("bx", (R, C)), x)
+    assert np.array_equal(p.host("bz", (R, C)), z)
+    assert np.array_equal(p.host("w2", (3, C)), w)
+    p.close()
+
+
+def test_multi_pair_copy_overlap_is_an_error(be):
+    """Two pairs writing overlapping views of one tensor: refused at run."""
+    import torch
+    text = """bwpp.plan 1
+value x f32 [4,8] input
+value y f32 [4,8] input
+value cat f32 [4,12] output
+view a of=cat offset=0 ld=12 shape=[4,8]
+view b of=cat offset=4 ld=12 shape=[4,8]
+op copy out=a,b in=x,y bcast=full
+"""
+    p = plan.Plan(be, text)
+    p.allocate()
+    p.bind("x", torch.zeros((4, 8), device="cuda"))
+    p.bind("y", torch.zeros((4, 8), device="cuda"))
+    with pytest.raises(plan.PlanError, match="overlaps"):
+        p.run()
+    p.close()
+
+
 def test_plan_graph_replay(be):
     """bwpp_hip_plan_capture / replay: a captured training step replays
     bit-identical to the eager run, three times in a row with other eager
