@@ -83,6 +83,8 @@ typedef struct {
   void *dv;
   float *dsum;
   float scale; /* the plain score scale (fp32 MFMA path, which gets scale * log2(e) in scale_log2) */
+  uint32_t zigzag; /* fp32 MFMA causal kernels: tile order heavy ranks first, then the light ones
+                      lightest first (a one-wave grid then pairs heavy with light on each CU) */
 } BwppAttnArgs;
 
 /* Attention operand copies between the caller's strided bf16 layout

@@ -170,6 +170,18 @@ struct Slice {
   uint32_t bh, b, h;
 };
 
+// Rank (0 = heaviest causal work) of this block's tile among the q_tiles
+// tiles of its slice.  Blocks go out tile rank by tile rank; with zigzag
+// the second half of the ranks goes out in reverse, so when the whole grid
+// is resident at once (two blocks per CU, block b sharing a CU with block
+// b + grid / 2) each CU holds one heavy and one light tile.
+__device__ __forceinline__ uint32_t tile_rank(const BwppAttnArgs &a, uint32_t nbh) {
+  const uint32_t r = blockIdx.x / nbh;
+  if (!a.zigzag) return r;
+  const uint32_t half = (a.q_tiles + 1) / 2;
+  return r < half ? r : a.q_tiles - 1 - (r - half);
+}
+
 __device__ __forceinline__ Slice slice_of(const BwppAttnArgs &a, uint32_t nbh) {
   Slice s;
   s.bh = blockIdx.x % nbh;
@@ -187,7 +199,7 @@ __device__ __forceinline__ void attn_fwd(const BwppAttnArgs &a) {
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
   const int li = lane & 31, hi = lane >> 5;
   const uint32_t nbh = gridDim.x / a.q_tiles;
-  const uint32_t qt = a.q_tiles - 1 - blockIdx.x / nbh;  // heaviest (causal) first
+  const uint32_t qt = a.q_tiles - 1 - tile_rank(a, nbh);  // heaviest (causal) first
   const Slice sl = slice_of(a, nbh);
   const float *Q = static_cast<const float *>(a.q) + sl.b * a.q_bs + sl.h * a.q_hs;
   const float *K = static_cast<const float *>(a.k) + sl.b * a.k_bs + sl.h * a.k_hs;
@@ -273,7 +285,7 @@ __device__ __forceinline__ void attn_bwd_dq(const BwppAttnArgs &a) {
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
   const int li = lane & 31, hi = lane >> 5;
   const uint32_t nbh = gridDim.x / a.q_tiles;
-  const uint32_t qt = a.q_tiles - 1 - blockIdx.x / nbh;
+  const uint32_t qt = a.q_tiles - 1 - tile_rank(a, nbh);
   const Slice sl = slice_of(a, nbh);
   const float *Q = static_cast<const float *>(a.q) + sl.b * a.q_bs + sl.h * a.q_hs;
   const float *K = static_cast<const float *>(a.k) + sl.b * a.k_bs + sl.h * a.k_hs;
@@ -355,7 +367,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwppAttnArgs &a) {
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
   const int li = lane & 31, hi = lane >> 5;
   const uint32_t nbh = gridDim.x / a.q_tiles;  // q_tiles holds the key tiles here
-  const uint32_t kt = blockIdx.x / nbh;          // heaviest (causal) first
+  const uint32_t kt = tile_rank(a, nbh);         // heaviest (causal) first
   const Slice sl = slice_of(a, nbh);
   const float *Q = static_cast<const float *>(a.q) + sl.b * a.q_bs + sl.h * a.q_hs;
   const float *K = static_cast<const float *>(a.k) + sl.b * a.k_bs + sl.h * a.k_hs;
