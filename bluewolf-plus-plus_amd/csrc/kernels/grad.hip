@@ -137,7 +137,12 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_rmsnorm_grad(const BwppGr
       const float d = dy[c];
       const float gd = g.gamma ? g.gamma[c] * d : d;
       const float v = inv * (gd - xh * mdot);
-      dx[c] = ac ? ac[c] + v : v;
+      if (ac) {
+#pragma clang fp contract(off)
+        dx[c] = ac[c] + v;  // never contracted into the product
+      } else {
+        dx[c] = v;
+      }
       if (parts) {
         colacc[c] += d * xh;
         colacc[g.cols + c] += d;
@@ -159,11 +164,14 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_rmsnorm_grad(const BwppGr
 // waves stride over rows, each keeping its dgamma / dbeta column sums in
 // registers, and combine them once through LDS at the end into the block's
 // partial row (summed by bwpp_col_partials_sum).  Same arithmetic as
-// bwpp_rmsnorm_grad.
+// bwpp_rmsnorm_grad.  A row's loads (x, dy and acc) are all issued before
+// its first use; chunks past the row end re-read the row's last chunk and
+// are zeroed where they are used.
 template <int VPT>
 __device__ __forceinline__ void rmsnorm_grad_wave(const BwppGradArgs &g) {
   extern __shared__ float colacc[];  // [4 waves][2][cols] when partials are requested
-  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  // wave is uniform: through readfirstlane the row pointers stay in SGPRs.
+  const int lane = (int)threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const uint32_t cols = g.cols;
   const bool parts = g.part_g != nullptr;
   float4 gm[VPT], ag[VPT], ab[VPT];
@@ -175,25 +183,47 @@ __device__ __forceinline__ void rmsnorm_grad_wave(const BwppGradArgs &g) {
     ag[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     ab[j] = ag[j];
   }
-  for (uint32_t r = blockIdx.x * 4u + (uint32_t)wave; r < g.rows; r += gridDim.x * 4u) {
+  // One row's operands: x, dy and (when accumulating) acc.  acc is either
+  // dx itself or disjoint from it, so reading it ahead of the row's stores
+  // is exact: a lane reads each acc element before it writes that element.
+  struct Row {
+    float4 x[VPT], d[VPT], a[VPT];
+  };
+  const bool has_acc = g.acc != nullptr;
+  auto load = [&](uint32_t r, Row &v) {
     const float *x = g.a + (size_t)r * g.ld;
     const float *dy = g.b + (size_t)r * g.ld;
-    float *dx = g.out + (size_t)r * g.ld;
-    const float *ac = g.acc ? g.acc + (size_t)r * g.ld : nullptr;
-    float4 xv[VPT], dv[VPT];
-    float ss = 0.0f, t = 0.0f;
+    const float *ac = g.acc + (size_t)r * g.ld;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const uint32_t c = 4u * (uint32_t)(lane + 64 * j);
-      xv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-      dv[j] = xv[j];
-      if (c < cols) {
-        xv[j] = *reinterpret_cast<const float4 *>(x + c);
-        dv[j] = *reinterpret_cast<const float4 *>(dy + c);
-      }
-      ss += (xv[j].x * xv[j].x + xv[j].y * xv[j].y) + (xv[j].z * xv[j].z + xv[j].w * xv[j].w);
-      t += (xv[j].x * gm[j].x * dv[j].x + xv[j].y * gm[j].y * dv[j].y) +
-           (xv[j].z * gm[j].z * dv[j].z + xv[j].w * gm[j].w * dv[j].w);
+      const uint32_t cc = c < cols ? c : cols - 4u;
+      v.x[j] = *reinterpret_cast<const float4 *>(x + cc);
+      v.d[j] = *reinterpret_cast<const float4 *>(dy + cc);
+      if (has_acc) v.a[j] = *reinterpret_cast<const float4 *>(ac + cc);
+    }
+  };
+  auto process = [&](uint32_t r, Row &v) {
+    // No contraction anywhere in the row's arithmetic: the compiler may
+    // duplicate this body (with / without acc) and would be free to fuse
+    // different products in each copy; with plain roundings every copy
+    // gives the same bits, and dx = acc + gradient is exactly the two ops.
+#pragma clang fp contract(off)
+    float *dx = g.out + (size_t)r * g.ld;
+    float ss = 0.0f, t = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      // Zero the re-read chunks past the row end (component-wise selects:
+      // a float4-valued ?: can go through memory).
+      const bool in = 4u * (uint32_t)(lane + 64 * j) < cols;
+      auto keep = [in](float4 q) {
+        return make_float4(in ? q.x : 0.f, in ? q.y : 0.f, in ? q.z : 0.f, in ? q.w : 0.f);
+      };
+      v.x[j] = keep(v.x[j]);
+      v.d[j] = keep(v.d[j]);
+      ss += (v.x[j].x * v.x[j].x + v.x[j].y * v.x[j].y) + (v.x[j].z * v.x[j].z + v.x[j].w * v.x[j].w);
+      t += (v.x[j].x * gm[j].x * v.d[j].x + v.x[j].y * gm[j].y * v.d[j].y) +
+           (v.x[j].z * gm[j].z * v.d[j].z + v.x[j].w * gm[j].w * v.d[j].w);
     }
     ss = wave_sum(ss);
     t = wave_sum(t);
@@ -204,31 +234,33 @@ __device__ __forceinline__ void rmsnorm_grad_wave(const BwppGradArgs &g) {
       const uint32_t c = 4u * (uint32_t)(lane + 64 * j);
       if (c >= cols) continue;
       float4 h, o;
-      h.x = xv[j].x * inv;
-      h.y = xv[j].y * inv;
-      h.z = xv[j].z * inv;
-      h.w = xv[j].w * inv;
-      o.x = inv * (gm[j].x * dv[j].x - h.x * mdot);
-      o.y = inv * (gm[j].y * dv[j].y - h.y * mdot);
-      o.z = inv * (gm[j].z * dv[j].z - h.z * mdot);
-      o.w = inv * (gm[j].w * dv[j].w - h.w * mdot);
-      if (ac) {
-        const float4 a4 = *reinterpret_cast<const float4 *>(ac + c);
-        o.x = a4.x + o.x;
-        o.y = a4.y + o.y;
-        o.z = a4.z + o.z;
-        o.w = a4.w + o.w;
-      }
+      h.x = v.x[j].x * inv;
+      h.y = v.x[j].y * inv;
+      h.z = v.x[j].z * inv;
+      h.w = v.x[j].w * inv;
+      o.x = inv * (gm[j].x * v.d[j].x - h.x * mdot);
+      o.y = inv * (gm[j].y * v.d[j].y - h.y * mdot);
+      o.z = inv * (gm[j].z * v.d[j].z - h.z * mdot);
+      o.w = inv * (gm[j].w * v.d[j].w - h.w * mdot);
+      o.x = has_acc ? v.a[j].x + o.x : o.x;  // acc: a separate rounded add
+      o.y = has_acc ? v.a[j].y + o.y : o.y;
+      o.z = has_acc ? v.a[j].z + o.z : o.z;
+      o.w = has_acc ? v.a[j].w + o.w : o.w;
       *reinterpret_cast<float4 *>(dx + c) = o;
-      ag[j].x += dv[j].x * h.x;
-      ag[j].y += dv[j].y * h.y;
-      ag[j].z += dv[j].z * h.z;
-      ag[j].w += dv[j].w * h.w;
-      ab[j].x += dv[j].x;
-      ab[j].y += dv[j].y;
-      ab[j].z += dv[j].z;
-      ab[j].w += dv[j].w;
+      ag[j].x += v.d[j].x * h.x;
+      ag[j].y += v.d[j].y * h.y;
+      ag[j].z += v.d[j].z * h.z;
+      ag[j].w += v.d[j].w * h.w;
+      ab[j].x += v.d[j].x;
+      ab[j].y += v.d[j].y;
+      ab[j].z += v.d[j].z;
+      ab[j].w += v.d[j].w;
     }
+  };
+  Row ra;
+  for (uint32_t r = blockIdx.x * 4u + (uint32_t)wave; r < g.rows; r += gridDim.x * 4u) {
+    load(r, ra);
+    process(r, ra);
   }
   if (!parts) return;  // block-uniform
   float *mine = colacc + (size_t)wave * 2 * cols;

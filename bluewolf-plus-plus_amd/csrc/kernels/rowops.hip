@@ -193,7 +193,12 @@ __device__ __forceinline__ void row_reg(const BwppRowArgs &a) {
   // Loads the row of group `grp` (rows past the end re-read the last row;
   // their results are never stored).
   auto load_row = [&](uint32_t grp, float4 *v) {
-    const uint32_t row = grp * G::kRows + sub;
+    // The row is wave-uniform (a row is owned by whole waves): through
+    // readfirstlane its base stays in SGPRs and the loads take the
+    // SGPR-base + 32-bit lane offset form, with no 64-bit address VGPRs
+    // (which the compiler otherwise recycled into the prefetch buffer,
+    // waiting for all memory operations at the loop head).
+    const uint32_t row = __builtin_amdgcn_readfirstlane(grp * G::kRows + sub);
     const float *xr = a.x + (size_t)(row < a.rows ? row : a.rows - 1) * a.ld;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
@@ -235,7 +240,7 @@ __device__ __forceinline__ void row_reg(const BwppRowArgs &a) {
 
   // Processes the row group `grp` held in v[] (reductions + stores).
   auto process = [&](float4(&v)[VPT], uint32_t grp) {
-    const uint32_t row = grp * G::kRows + sub;
+    const uint32_t row = __builtin_amdgcn_readfirstlane(grp * G::kRows + sub);  // wave-uniform
     const bool valid = row < a.rows;
     float *yr = a.y ? a.y + (size_t)(valid ? row : 0) * a.ld : nullptr;
     auto store = [&](int j, const float4 &o) {
