@@ -89,13 +89,23 @@ __device__ __forceinline__ void argmax_merge(float &v, uint32_t &i, float v2,
   }
 }
 
+// Wave-wide (max, first index of the max) for lane pairs whose v is never
+// NaN: the max first, then the smallest index among the lanes holding it
+// (the pairwise argmax_merge result, with one plain max and one unsigned
+// min per step instead of a compare-and-swap of both).
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, dpp_u32<kDppQuadXor1>(v));
+  v = min(v, dpp_u32<kDppQuadXor2>(v));
+  v = min(v, dpp_u32<kDppRowHalfMirror>(v));
+  v = min(v, dpp_u32<kDppRowMirror>(v));
+  v = min(v, xor_u32(v, 16));
+  v = min(v, xor_u32(v, 32));
+  return v;
+}
 __device__ __forceinline__ void wave_argmax(float &v, uint32_t &i) {
-  argmax_merge(v, i, dpp_f32<kDppQuadXor1>(v), dpp_u32<kDppQuadXor1>(i));
-  argmax_merge(v, i, dpp_f32<kDppQuadXor2>(v), dpp_u32<kDppQuadXor2>(i));
-  argmax_merge(v, i, dpp_f32<kDppRowHalfMirror>(v), dpp_u32<kDppRowHalfMirror>(i));
-  argmax_merge(v, i, dpp_f32<kDppRowMirror>(v), dpp_u32<kDppRowMirror>(i));
-  argmax_merge(v, i, xor_f32(v, 16), xor_u32(i, 16));
-  argmax_merge(v, i, xor_f32(v, 32), xor_u32(i, 32));
+  const float m = wave_max(v);
+  i = wave_min_u32(v == m ? i : 0xffffffffu);
+  v = m;
 }
 
 // 128-bit non-temporal global accesses for data streamed exactly once.

@@ -351,16 +351,33 @@ __device__ __forceinline__ void row_reg(const BwppRowArgs &a) {
     } else if constexpr (OP == OP_MAX || OP == OP_MAX_GRAD) {
       float m = -INFINITY;
       uint32_t mi = kNoIndex;
+      if constexpr (FULL) {
+        // Two passes over the registers: the lane's max (fmaxf skips NaN,
+        // -inf when the lane holds no number), then its first column
+        // holding that value (a backward scan, the last hit wins), which
+        // is the first strict-or-equal maximum of the one-pass rule below.
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) {
-        const uint32_t c = chunk_col(j);
+        for (int j = 0; j < VPT; ++j) m = fmaxf(fmaxf(m, fmaxf(v[j].x, v[j].y)), fmaxf(v[j].z, v[j].w));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float t = get(v[j], e);
-          if (FULL || c + e < cols) {
-            if (t > m || (mi == kNoIndex && t == m)) {
-              m = t;
-              mi = c + e;
+        for (int j = VPT - 1; j >= 0; --j) {
+          const uint32_t c = chunk_col(j);
+          mi = v[j].w == m ? c + 3u : mi;
+          mi = v[j].z == m ? c + 2u : mi;
+          mi = v[j].y == m ? c + 1u : mi;
+          mi = v[j].x == m ? c : mi;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+          const uint32_t c = chunk_col(j);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float t = get(v[j], e);
+            if (c + e < cols) {
+              if (t > m || (mi == kNoIndex && t == m)) {
+                m = t;
+                mi = c + e;
+              }
             }
           }
         }
