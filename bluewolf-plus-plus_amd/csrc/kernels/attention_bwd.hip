@@ -334,12 +334,19 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
         const bool edge = k0 + kR > a.N || (CAUSAL && (int64_t)k0 + kR - 1 > (int64_t)q0 + diag);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float p = __builtin_amdgcn_exp2f(s[r] * c - lse2);
-          if (edge) {
-            const uint32_t key = k0 + (uint32_t)acc_row(r, hi);
-            if (key >= a.N || (CAUSAL && (int64_t)key > (int64_t)qi + diag)) p = 0.0f;
-          }
+          const float p = __builtin_amdgcn_exp2f(s[r] * c - lse2);
           s[r] = p * (dp[r] - dsum);  // dS^T
+        }
+        // Keys past N or above the diagonal: p = 0.  One block-uniform
+        // branch around all 16 (per element the optimiser turned each test
+        // into a compare and two selects on every tile, a third of the
+        // tile's VALU work).
+        if (edge) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const uint32_t key = k0 + (uint32_t)acc_row(r, hi);
+            if (key >= a.N || (CAUSAL && (int64_t)key > (int64_t)qi + diag)) s[r] = 0.0f * (dp[r] - dsum);
+          }
         }
 #pragma unroll
         for (int kq = 0; kq < 2; ++kq) {
@@ -464,10 +471,27 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * r4 + e;
-            float p = __builtin_amdgcn_exp2f(s[r] * c - l4[e]);
-            if (edge && (int64_t)ni > (int64_t)(m0 + (uint32_t)(row + e)) + diag) p = 0.0f;
+            const float p = __builtin_amdgcn_exp2f(s[r] * c - l4[e]);
             s[r] = p;
             ds[r] = p * (dp[r] - d4[e]);
+          }
+        }
+        // Queries before this key's diagonal: p = 0, under one block-uniform
+        // branch (per element the test became compares and selects on
+        // every tile).
+        if (edge) {
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int row = 8 * r4 + 4 * hi;
+            const f32x4_t d4 = *reinterpret_cast<const f32x4_t *>(&rowv[st][1][sb * kR + row]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = 4 * r4 + e;
+              if ((int64_t)ni > (int64_t)(m0 + (uint32_t)(row + e)) + diag) {
+                s[r] = 0.0f;
+                ds[r] = 0.0f * (dp[r] - d4[e]);
+              }
+            }
           }
         }
 #pragma unroll
