@@ -237,17 +237,21 @@ __device__ __forceinline__ void attn_fwd(const BwppAttnArgs &a) {
     if (!CAUSAL || (int64_t)k0 <= wlast) {  // wave-uniform
       f32x16 s = dot_tile<D>(lds[st][0], qreg, li, hi);
       const bool edge = k0 + kR > a.N || (CAUSAL && (int64_t)k0 + kR - 1 > (int64_t)q0 + diag);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] *= c;
+      // Keys past N or above the diagonal: -inf, under one block-uniform
+      // branch (per element the test became compares and selects on every
+      // tile).
+      if (edge) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t key = k0 + (uint32_t)acc_row(r, hi);
+          if (key >= a.N || (CAUSAL && (int64_t)key > (int64_t)qi + diag)) s[r] = -INFINITY;
+        }
+      }
       float mx = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float v = s[r] * c;
-        if (edge) {
-          const uint32_t key = k0 + (uint32_t)acc_row(r, hi);
-          if (key >= a.N || (CAUSAL && (int64_t)key > (int64_t)qi + diag)) v = -INFINITY;
-        }
-        s[r] = v;
-        mx = fmaxf(mx, v);
-      }
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
       mx = max32(mx);
       const float mnew = fmaxf(mrun, mx);
       const float mu = mnew == -INFINITY ? 0.0f : mnew;
@@ -341,12 +345,15 @@ __device__ __forceinline__ void attn_bwd_dq(const BwppAttnArgs &a) {
       const bool edge = k0 + kR > a.N || (CAUSAL && (int64_t)k0 + kR - 1 > (int64_t)q0 + diag);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float p = __builtin_amdgcn_exp2f(s[r] * c - lse2);
-        if (edge) {
-          const uint32_t key = k0 + (uint32_t)acc_row(r, hi);
-          if (key >= a.N || (CAUSAL && (int64_t)key > (int64_t)qi + diag)) p = 0.0f;
-        }
+        const float p = __builtin_amdgcn_exp2f(s[r] * c - lse2);
         s[r] = p * (dp[r] - dsum);  // dS^T
+      }
+      if (edge) {  // masked keys: p = 0 (one block-uniform branch)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t key = k0 + (uint32_t)acc_row(r, hi);
+          if (key >= a.N || (CAUSAL && (int64_t)key > (int64_t)qi + diag)) s[r] = 0.0f * (dp[r] - dsum);
+        }
       }
       acc_tile_t<D>(dq, lds[st][0], s, li, hi);  // dQ^T += K^T dS^T
     }
@@ -440,10 +447,24 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwppAttnArgs &a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * r4 + e;
-          float p = __builtin_amdgcn_exp2f(s[r] * c - l4[e]);
-          if (edge && (int64_t)ni > (int64_t)(m0 + (uint32_t)(row + e)) + diag) p = 0.0f;
+          const float p = __builtin_amdgcn_exp2f(s[r] * c - l4[e]);
           s[r] = p;
           ds[r] = p * (dp[r] - d4[e]);
+        }
+      }
+      if (edge) {  // queries before this key's diagonal: p = 0 (one block-uniform branch)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int row = 8 * r4 + 4 * hi;
+          const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&rowv[st][1][row]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * r4 + e;
+            if ((int64_t)ni > (int64_t)(m0 + (uint32_t)(row + e)) + diag) {
+              s[r] = 0.0f;
+              ds[r] = 0.0f * (dp[r] - d4[e]);
+            }
+          }
         }
       }
       acc_tile_t<D>(dv, lds[st][1], s, li, hi);   // dV^T += dO^T P
