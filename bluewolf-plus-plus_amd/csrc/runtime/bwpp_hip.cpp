@@ -950,12 +950,12 @@ BwppHipStatus attn_prepare(BwppHip *h, const void *q, const void *k, const void 
 // dim 64, 1: 128), or -1 for the generic path: they need K = D in {64, 128},
 // a finite scale and 16-byte rows (pointers, leading dims and slice strides
 // in multiples of 4 floats).
-// fp32 MFMA causal forward: zigzag tile order when the grid is resident in
+// fp32 MFMA causal passes: zigzag tile order when the grid is resident in
 // one go at two blocks per CU (more than one block per CU, at most two),
 // so the dispatcher's pairing of block b with b + grid / 2 on a CU joins a
-// heavy tile with a light one (C5: 512 blocks on 256 CUs, 63 -> 58 us; B2
-// H16 S2048 d64: 234 -> 190 us).  The backward passes keep heaviest-first:
-// with zigzag they ran 3-5 % slower.
+// heavy tile with a light one (forward, C5: 512 blocks on 256 CUs, 63 -> 58
+// us; B2 H16 S2048 d64: 234 -> 190 us; backward, with both passes at two
+// waves per SIMD: C5 187 -> 165 us, B2 H16 S2048 d64 686 -> 529 us).
 uint32_t attn_zigzag(const BwppHip *h, bool causal, uint64_t grid) {
   return causal && h->attn_zigzag && h->cus > 0 && grid > (uint64_t)h->cus && grid <= 2ull * (uint64_t)h->cus ? 1u
                                                                                                                 : 0u;
@@ -1147,10 +1147,12 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
     uint64_t grid = slices * f.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
     BwppHipStatus st;
+    f.zigzag = attn_zigzag(h, causal != 0, grid);  // read by the fp32 passes
     if (p.M > 0 && (st = launch(h, fdq, (uint32_t)grid, 1, 1, 64 * wq, f)) != BWPP_HIP_OK) return st;
     f.q_tiles = (p.N + 32 * wk - 1) / (32 * wk);  // key tiles
     grid = slices * f.q_tiles;
     if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
+    f.zigzag = attn_zigzag(h, causal != 0, grid);
     if (p.N > 0) return launch(h, fdkdv, (uint32_t)grid, 1, 1, 64 * wk, f);
     return BWPP_HIP_OK;
   };

@@ -84,6 +84,44 @@ def test_mfma_f32_fwd_bwd(be, oracle, B, H, M, N, D, causal):
         assert np.all(o[:, :, :M - N] == 0.0) and np.all(dq[:, :, :M - N] == 0.0)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_mfma_f32_causal_zigzag_order(be, oracle, monkeypatch, D):
+    """Causal fp32 passes on a grid that is resident in one go at two blocks
+    per CU (more blocks than CUs, at most twice as many: cus / 2 slices of
+    four 128-row tiles), where the forward, dQ and dK/dV passes send their
+    tiles out in zigzag order: the results equal the heaviest-first order
+    (BWPP_ATTN_ZIGZAG=0) bit for bit, and one slice matches the oracle."""
+    torch = _torch()
+    cus = be.cus
+    B, H, S = 2, max(1, cus // 4), 512
+    seed = 77 + D
+    q, k, v, dout = (synth.normal((B, H, S, D), seed, i) for i in range(4))
+    scale = 1.0 / np.sqrt(D)
+    prm = bwpp.AttentionParams(M=S, N=S, K=D, D=D, ldq=D, ldk=D, ldv=D, ldo=D, batch=B, heads=H,
+                               scale=scale, causal=1, dtype=int(bwpp.DType.F32))
+    outs = []
+    for zz in ("1", "0"):
+        monkeypatch.setenv("BWPP_ATTN_ZIGZAG", zz)
+        b2 = bwpp.HipBackend(0)
+        try:
+            b2.set_stream(torch.cuda.current_stream())
+            outs.append(_run_all(b2, q, k, v, dout, scale, True, prm))
+        finally:
+            b2.close()
+    for a, b in zip(*outs):
+        assert np.all(np.isfinite(a) | np.isneginf(a))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    o, _, lse, dq, dk, dv = outs[0]
+    s1 = (slice(1, 2), slice(H - 1, H))
+    want = oracle.attention_bh(q[s1], k[s1], v[s1], scale, True)
+    assert rel_max_err(o[s1], want) <= TOL
+    _check_lse(lse[s1], oracle.attention_lse(q[s1], k[s1], scale, True))
+    wq, wk, wv = oracle.attention_grad(q[s1], k[s1], v[s1], dout[s1], scale, True)
+    assert rel_max_err(dq[s1], wq) <= TOL
+    assert rel_max_err(dk[s1], wk) <= TOL
+    assert rel_max_err(dv[s1], wv) <= TOL
+
+
 @pytest.mark.parametrize("scale", [-0.3, 2.0])
 def test_mfma_f32_scales(be, oracle, scale):
     B, H, M, N, D = 1, 2, 100, 140, 64
