@@ -9,8 +9,8 @@
 // Layout of the work: a block of 8 waves (two per SIMD) owns a tile of 256
 // queries of one (batch, head) (causal: two such tiles, one after the
 // other); each wave owns 32 queries of the tile.  Keys stream through LDS in
-// tiles of 128 (K and V, 32 KiB each for d = 128) in a 2-stage ring, or of
-// 64 in a 4-stage ring when causal, filled by global -> LDS DMA.  Two waves per SIMD let one wave's softmax (VALU)
+// tiles of 128 (K and V, 32 KiB each for d = 128) in a 2-stage ring, filled
+// by global -> LDS DMA.  Two waves per SIMD let one wave's softmax (VALU)
 // run while the other's MFMAs issue; 32 queries per wave keep the
 // registers (Q^T operands, S^T tile, O^T accumulators) under 256 per wave.
 //
@@ -80,11 +80,11 @@ __device__ __forceinline__ uint32_t v_off(uint32_t r, uint32_t c) { return r * 2
 // One query tile (256 queries) of one (batch, head) slice.
 template <bool CAUSAL>
 __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const uint32_t bh, const uint32_t qt) {
-  // Key tiles: 128 keys in a 2-stage ring unmasked (half the barriers and
-  // DMA issues per key; 4 % faster at C4), 64 keys in a 4-stage ring when
-  // causal (the diagonal band then wastes less work on masked keys).
-  constexpr int kBKV = CAUSAL ? 64 : 128;
-  constexpr int kStages = CAUSAL ? 4 : 2;
+  // Key tiles: 128 keys in a 2-stage ring (half the barriers and DMA issues
+  // per key of 64-key tiles: 4 % faster at C4 unmasked, 5 % causal, where a
+  // masked tile skips the 32-key blocks its wave sees none of).
+  constexpr int kBKV = 128;
+  constexpr int kStages = 2;
   constexpr int D = 128;
   constexpr int KS = D / 16;  // k-steps of S over d
   constexpr int DB = D / 32;  // 32-wide d blocks of O^T
@@ -190,12 +190,25 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
   // One key tile.  MASK: some (key, query) pair of the tile is masked out.
   auto tile = [&](auto mask_tag, const unsigned char *Ks, uint32_t k0) {
     constexpr bool MASK = decltype(mask_tag)::value;
+    // Masked tiles: 32-key blocks past every key this wave's queries see
+    // are skipped (their scores are masked to -inf below, p = 0).
+    int kbmax = KB - 1;
+    if constexpr (MASK) {
+      int64_t kv = (int64_t)a.N - 1 - (int64_t)k0;
+      if (CAUSAL) {
+        const int64_t kc = (int64_t)(q0 + kQW - 1) + diag - (int64_t)k0;
+        kv = kc < kv ? kc : kv;
+      }
+      kbmax = kv < 0 ? -1 : (int)(kv / 32 < KB - 1 ? kv / 32 : KB - 1);
+      kbmax = __builtin_amdgcn_readfirstlane(kbmax);
+    }
     // S^T blocks: s[kb] = K[32 kb .. 32 kb + 31] . Q^T.
     f32x16_t s[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
+      if (MASK && kb > kbmax) continue;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const bf16x8_t kf =
@@ -205,13 +218,15 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
     }
     // Keep two K reads ahead of the MFMAs instead of hoisting all sixteen
     // (which would not fit the 256 registers of a two-wave-per-SIMD wave).
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    if constexpr (!MASK) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-    for (int i = 0; i < KB * KS - 2; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int i = 0; i < KB * KS - 2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
 
     // Online softmax for this lane's query (plus partner lane ^ 32).
     float mx = -INFINITY;
@@ -275,6 +290,7 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
     // O^T += V^T P^T over the blocks of 16 keys.
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
+      if (MASK && kb > kbmax) continue;
 #pragma unroll
       for (int kq = 0; kq < 2; ++kq) {
         const int r0 = 8 * kq;
@@ -297,26 +313,29 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
       }
     }
     // Two V^T operands (four transposing reads) ahead of the MFMAs.
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    if constexpr (!MASK) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int i = 0; i < 2 * KB * DB - 2; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      for (int i = 0; i < 2 * KB * DB - 2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   };
 
 #pragma unroll
   for (int st = 0; st < kStages - 1; ++st)
     if ((uint32_t)st < nkt) issue((uint32_t)st);
 
-  // Tiles before t_mask need no mask for any wave of the block; the rest
+  // Tiles before t_mask need no mask for any query of this wave; the rest
   // go through the masked variant.  Two loops (not one with a branch) keep
-  // a single copy of the O accumulators live.
+  // a single copy of the O accumulators live; every wave still passes each
+  // tile's barrier once, whichever loop it is in.
   uint32_t t_mask = a.N / kBKV;  // first tile with keys past N
   if (CAUSAL) {
-    // First tile holding a key past query qb0's limit qb0 + diag.
-    const int64_t first_hidden = (int64_t)qb0 + diag + 1;
+    // First tile holding a key past query q0's limit q0 + diag.
+    const int64_t first_hidden = (int64_t)q0 + diag + 1;
     const uint32_t tc = first_hidden <= 0 ? 0u : (uint32_t)min<int64_t>(first_hidden / kBKV, (int64_t)nkt);
     t_mask = min(t_mask, tc);
   }
