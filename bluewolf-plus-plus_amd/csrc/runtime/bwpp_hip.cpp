@@ -806,23 +806,34 @@ BwppHipStatus matmul_impl(BwppHip *h, const void *a, const void *b, void *c, con
   //   staged (bwpp_gemm_f32): register-staged double buffer, two blocks per
   //     CU (BWPP_GEMM_F32_PIPE=0 only; the rings beat it on every measured
   //     full-tile shape).
-  // A launch of b blocks runs in ceil(b / slots) waves of blocks, each
-  // taking time proportional to its K range.  The choice minimises
+  // A launch of b blocks runs in waves of blocks, each taking time
+  // proportional to its K range.  The choice minimises
   //   ring4:  ceil(b / cus) (k t4 + o4)
-  //   ring2:  ceil(b / (2 cus)) k t2 + o4      (staged: t = 0.13)
-  // plus (S + 1) M N 4 / bw + t_launch when split, with t4 = 0.064 us and
-  // t2 = 0.122 us per k of a 128 x 128 block, o4 = 3 us per block (the
-  // prologue and epilogue, which one block per CU does not overlap), bw =
-  // 5 TB/s, t_launch = 5 us (fitted on MI355X to 8192^3, 4096 x 4096 x 1024,
-  // 4096 x 3072 x 1024, 2048^3 and 4096 x 1024 x 1024).  A split is taken
-  // only when it models 5 % faster.
+  //   ring2:  floor(b / (2 cus)) k t2 + o4, plus for a last partial wave
+  //           k t1 when it holds at most one block per CU (such a block
+  //           has its CU to itself), else k t2      (staged: t2 = 0.13)
+  // plus (2 S - 1) M N 4 / bw + t_r when split (S - 1 more planes written
+  // and S read by the reduce), with t4 = 0.064 us, t2 = 0.119 us and t1 =
+  // 0.065 us per k of a 128 x 128 block, o4 = 3 us per block (the prologue
+  // and epilogue, which one block per CU does not overlap), bw = 6 TB/s,
+  // t_r = 2 us; fitted on MI355X to the twelve GEMMs of the C5 block step
+  // (from 1024 x 1024 x 4096 to 4096 x 4096 x 1024, with and without split)
+  // and checked on 2048^3 and 8192^3.
   if (!bf16 && full) {
     const int mode = (int)h->gemm_f32_pipe;  // 0 staged, 1 auto, 2 ring4, 3 ring2
     const uint64_t cus = h->cus > 0 ? (uint64_t)h->cus : 256ull;
     auto cost = [&](int kind, uint64_t S, uint32_t kchunk) {  // kind: 0 staged, 1 ring2, 2 ring4
-      double t = kind == 2 ? (double)((tiles * S + cus - 1) / cus) * (kchunk * 0.064 + 3.0)
-                           : (double)((tiles * S + 2 * cus - 1) / (2 * cus)) * kchunk * (kind ? 0.122 : 0.13) + 3.0;
-      if (S > 1) t = 1.05 * (t + (double)(S + 1) * p.M * p.N * 4.0 / 5e6 + 5.0);
+      const uint64_t b = tiles * S;
+      double t;
+      if (kind == 2) {
+        t = (double)((b + cus - 1) / cus) * (kchunk * 0.064 + 3.0);
+      } else {
+        const double tk = kind ? 0.119 : 0.13;
+        const uint64_t full = b / (2 * cus), rem = b % (2 * cus);
+        t = (double)full * kchunk * tk + 3.0;
+        if (rem > 0) t += kchunk * (rem <= cus ? 0.065 : tk);
+      }
+      if (S > 1) t += (double)(2 * S - 1) * p.M * p.N * 4.0 / 6e6 + 2.0;
       return t;
     };
     int bestKind = mode == 0 ? 0 : mode == 3 ? 1 : 2;
