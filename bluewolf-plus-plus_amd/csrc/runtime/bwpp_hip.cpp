@@ -146,6 +146,8 @@ BwppHipStatus bwpp_hip_set_error(BwppHip *h, BwppHipStatus s, const char *fmt, .
   return s;
 }
 
+const void *bwpp_hip_workspace(const BwppHip *h) { return h ? h->ws : nullptr; }
+
 namespace {
 
 BwppHipStatus resolve(BwppHip *h, const std::string &name, hipFunction_t *out) {

@@ -119,9 +119,11 @@ struct BwppHipPlan {
   bool allocated = false;
   bool check_only = false;  // run_op validates arguments and launches nothing
   std::string err;
-  // bwpp_hip_plan_capture: one run recorded as a HIP graph
+  // bwpp_hip_plan_capture: one run recorded as a HIP graph, and the
+  // handle's workspace address its kernels were recorded with
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  const void *graph_ws = nullptr;
 };
 
 namespace {
@@ -467,12 +469,18 @@ extern "C" BwppHipStatus bwpp_hip_plan_capture(BwppHipPlan *p) {
     drop_graph(p);
     return perr(p, BWPP_HIP_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
   }
+  p->graph_ws = bwpp_hip_workspace(p->h);
   return BWPP_HIP_OK;
 }
 
 extern "C" BwppHipStatus bwpp_hip_plan_replay(BwppHipPlan *p) {
   if (!p) return BWPP_HIP_ERR_INVALID_ARG;
   if (!p->exec) return perr(p, BWPP_HIP_ERR_INVALID_ARG, "no captured graph (capture after the last bind)");
+  // An op on the handle that needed a larger workspace freed the one the
+  // graph's kernels address: refuse rather than replay into freed memory.
+  if (bwpp_hip_workspace(p->h) != p->graph_ws)
+    return perr(p, BWPP_HIP_ERR_INVALID_ARG,
+                "the handle's workspace was reallocated after capture (a larger op ran on it): capture again");
   hipStream_t st = static_cast<hipStream_t>(bwpp_hip_get_stream(p->h));
   hipError_t e = hipGraphLaunch(p->exec, st);
   if (e != hipSuccess) return perr(p, BWPP_HIP_ERR_HIP, "hipGraphLaunch: %s", hipGetErrorString(e));

@@ -16,6 +16,11 @@ BwppHipStatus bwpp_hip_attention_grad_planned(BwppHip *h, const void *q, const v
 BwppHipStatus bwpp_hip_set_error(BwppHip *h, BwppHipStatus s, const char *fmt, ...)
     __attribute__((format(printf, 3, 4)));
 
+// Device address of the handle's grad / split-K workspace (NULL before its
+// first use).  It moves when an op needs more than its current size, so a
+// HIP graph recorded with the old address must not be replayed after that.
+const void *bwpp_hip_workspace(const BwppHip *h);
+
 // Size of the device-resident scratch array of bwpp_scratch.hip, which the
 // allocation-free attention backward uses for its per-query row sums.
 #define BWPP_HIP_NOALLOC_SCRATCH_BYTES (8u << 20)

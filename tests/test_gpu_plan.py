@@ -314,6 +314,57 @@ def test_plan_graph_replay(be):
         be.set_stream(torch.cuda.current_stream())
 
 
+def test_plan_replay_after_workspace_growth():
+    """A captured graph's kernels address the handle's workspace as it was
+    at capture.  A later op on the handle that needs a larger workspace
+    (here a split-K fp32 GEMM) reallocates it, and replay then refuses
+    instead of running on freed memory -- unless the new workspace landed
+    at the same address, where replay is valid; capturing again restores
+    replay, bit-identical to an eager run."""
+    import torch
+    from blockref import block_inputs, grad_shapes
+    B, T, D, H, HEADS = 2, 64, 128, 256, 2
+    shapes = dict(grad_shapes(B, T, D, H), loss=(1,))
+    h = bwpp.HipBackend(0)
+    side = torch.cuda.Stream()
+    h.set_stream(side)
+    try:
+        p = plan.Plan(h, plan.load_text("block_train", BATCH=B, T=T, D=D, H=H, HEADS=HEADS))
+        p.allocate()
+        for k, v in block_inputs(B, T, D, H, seed=23).items():
+            p.bind(k, torch.from_numpy(v).cuda())
+        torch.cuda.synchronize()
+        p.run()
+        want = {n: p.host(n, sh) for n, sh in shapes.items()}
+        p.capture()
+        # 1024 x 1024 x 4096, A^T B: split into K ranges, 16+ MiB of partial planes
+        M, N, K = 1024, 1024, 4096
+        a = torch.randn(K, M, device="cuda")
+        b = torch.randn(K, N, device="cuda")
+        c = torch.empty(M, N, device="cuda")
+        torch.cuda.synchronize()
+        h.dispatch_matmul(a, b, c, None, bwpp.MatmulParams(M, N, K, M, N, N, 0, 0, 1, 0))
+        assert h.last_kernel == "bwpp_gemm_f32_splitk_reduce", h.last_kernel
+        torch.cuda.synchronize()
+        try:
+            p.replay()
+        except plan.PlanError as e:
+            assert "workspace was reallocated" in str(e)
+        else:
+            torch.cuda.synchronize()
+            for n, sh in shapes.items():
+                assert np.array_equal(p.host(n, sh).view(np.uint32), want[n].view(np.uint32)), n
+        p.capture()
+        p.replay()
+        torch.cuda.synchronize()
+        for n, sh in shapes.items():
+            assert np.array_equal(p.host(n, sh).view(np.uint32), want[n].view(np.uint32)), n
+        p.close()
+    finally:
+        torch.cuda.synchronize()
+        h.close()
+
+
 def test_plan_capture_needs_a_stream(be):
     import torch
     be.set_stream(torch.cuda.default_stream())
