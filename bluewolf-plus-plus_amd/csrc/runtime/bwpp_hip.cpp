@@ -298,11 +298,15 @@ BwppHipStatus launch(BwppHip *h, hipFunction_t f, uint32_t gx, uint32_t gy, uint
 inline uint32_t eff_ld(uint32_t ld, uint32_t cols) { return ld ? ld : cols; }
 
 // Picks the register-resident configuration for one operator on rows of
-// `cols` floats, or -1 for the multi-pass fallback.  Rows up to 512 get one
-// wave each; longer rows get a block of 4 waves (8 for softmax from 4096
-// columns, and for every operator above 16384), with the float4 chunks per
-// thread doubled until the row fits (<= 16, i.e. 32768 columns).  These are
-// the fastest layouts measured on MI355X at 4096 columns.
+// `cols` floats, or -1 for the multi-pass fallback.  Rows up to 1024 get one
+// wave each (no cross-wave reduction, no barrier), and so do the norms' and
+// softmax's rows up to 1536; up to 2048 the norms and reduce_max take two
+// waves, and up to 3072 the norms take two waves of 8 chunks.  Longer rows
+// get a block of 4 waves (8 for softmax from 4096 columns, and for every
+// operator above 16384), with the float4 chunks per thread doubled until the
+// row fits (<= 16, i.e. 32768 columns).  These are the fastest layouts
+// measured on MI355X at 768 - 4096 columns (one wave per row: RMSNorm over
+// 4096 x 1024 9.2 -> 6.5 us, LayerNorm over 4096 x 768 15.2 -> 7.0 us).
 int pick_row_cfg(const BwppHip *h, RowOpId op, uint32_t cols, bool vec_ok) {
   if (!vec_ok) return -1;
   if (h->row_cfg_override >= 0 && h->row_cfg_override < kRowNCfg &&
@@ -310,6 +314,11 @@ int pick_row_cfg(const BwppHip *h, RowOpId op, uint32_t cols, bool vec_ok) {
     return h->row_cfg_override;
   if (cols <= 256) return find_cfg(1, 1);
   if (cols <= 512) return find_cfg(2, 1);
+  if (cols <= 1024) return find_cfg(4, 1);
+  const bool norm = op == ROW_RMSNORM || op == ROW_LAYERNORM;
+  if (cols <= 1536 && (norm || op == ROW_SOFTMAX)) return find_cfg(8, 1);
+  if (cols <= 2048 && op != ROW_SOFTMAX) return find_cfg(4, 2);
+  if (cols <= 3072 && norm) return find_cfg(8, 2);
   if (cols > 32768) return -1;
   const int wpr = (cols > 16384 || (op == ROW_SOFTMAX && cols >= 4096)) ? 8 : 4;
   int vpt = 1;
