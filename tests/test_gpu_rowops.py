@@ -143,6 +143,47 @@ def test_golden_row_vectors(be, golden):
         assert rel_max_err(host(y), golden[f"{name}/y"]) <= FP32_TOL, name
 
 
+# (cols, {op: (float4 chunks per thread, waves per row)}) of the default
+# layout choice: one wave per row up to 1024 columns (1536 for the norms
+# and softmax), two up to 2048 (not softmax) and, for the norms, two waves
+# of 8 chunks up to 3072; four beyond, eight for softmax from 4096.
+LAYOUTS = [
+    (1000, {"rmsnorm": (4, 1), "layernorm": (4, 1), "softmax": (4, 1), "max": (4, 1)}),
+    (1536, {"rmsnorm": (8, 1), "layernorm": (8, 1), "softmax": (8, 1), "max": (4, 2)}),
+    (2048, {"rmsnorm": (4, 2), "layernorm": (4, 2), "softmax": (2, 4), "max": (4, 2)}),
+    (3072, {"rmsnorm": (8, 2), "layernorm": (8, 2), "softmax": (4, 4), "max": (4, 4)}),
+    (4096, {"rmsnorm": (4, 4), "layernorm": (4, 4), "softmax": (2, 8), "max": (4, 4)}),
+]
+
+
+@pytest.mark.parametrize("cols,want", LAYOUTS)
+def test_default_layouts(be, oracle, cols, want):
+    """The layout each operator gets by default (kernel name of the launch),
+    with its result checked against the oracle."""
+    torch = _torch()
+    rows = 37
+    x, g, b = _inputs(rows, cols, cols + 1)
+    xd, y = dev(x), dev(np.zeros_like(x))
+    full = lambda vw: "f" if 256 * vw[0] * vw[1] == cols else "p"
+    name = lambda op, vw: f"bwpp_row_{op}_v{vw[0]}_w{vw[1]}_{full(vw)}"
+    be.dispatch_rmsnorm(xd, dev(g), None, y, bwpp.RmsnormParams(rows, cols, cols, 1e-6))
+    assert be.last_kernel == name("rmsnorm", want["rmsnorm"])
+    assert rel_max_err(host(y), oracle.rmsnorm(x, g, None, 1e-6)) <= FP32_TOL
+    be.dispatch_layernorm(xd, dev(g), dev(b), y, bwpp.RmsnormParams(rows, cols, cols, 1e-5))
+    assert be.last_kernel == name("layernorm", want["layernorm"])
+    assert rel_max_err(host(y), oracle.layernorm(x, g, b, 1e-5)) <= FP32_TOL
+    be.dispatch_softmax(xd, y, bwpp.SoftmaxParams(rows, cols, cols))
+    assert be.last_kernel == name("softmax", want["softmax"])
+    assert rel_max_err(host(y), oracle.softmax(x)) <= FP32_TOL
+    mv = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    ix = torch.zeros(rows, dtype=torch.int32, device="cuda")
+    be.dispatch_reduce_max(xd, mv, ix, bwpp.ReduceParams(rows, cols, cols, 1))
+    assert be.last_kernel == name("max", want["max"])
+    wm, wi = oracle.reduce_max(x, 1)
+    assert_bits_equal(host(mv), wm)
+    assert np.array_equal(host(ix), wi)
+
+
 @pytest.mark.parametrize("idx", range(len(ROW_CFGS)))
 @pytest.mark.parametrize("grid_cap", [0, 3])
 def test_every_row_config(oracle, monkeypatch, idx, grid_cap):
