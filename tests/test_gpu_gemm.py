@@ -380,3 +380,38 @@ def test_f32_full_tile_kernels(oracle, monkeypatch, mode, family, split, ta, tb)
             assert rel_max_err(f32_host(c), np.add(want, aux, dtype=np.float32)) <= F32_TOL, (M, N, K, kern)
     finally:
         h.close()
+
+
+# (M, N, K, trans_a, trans_b, kernel the cost model picks on 256 CUs): the
+# C5 block step's GEMM shapes; "split" = K cut into ranges (the launch ends
+# with the split-K reduce).
+C5_CHOICES = [
+    (4096, 3072, 1024, 0, 0, "bwpp_gemm_f32p_t00_f"),   # q/k/v: 2-stage ring, last wave half full
+    (4096, 1024, 1024, 0, 0, "bwpp_gemm_f32q_t00_f"),   # out-projection: one tile per CU
+    (4096, 4096, 1024, 0, 1, "bwpp_gemm_f32p_t01_f"),
+    (4096, 1024, 4096, 0, 0, "split"),
+    (1024, 4096, 4096, 1, 0, "split"),
+    (1024, 1024, 4096, 1, 0, "split"),
+]
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb,want", C5_CHOICES)
+def test_f32_kernel_choice_c5_shapes(be, M, N, K, ta, tb, want):
+    """The fp32 kernel / split-K choice on the C5 step's GEMM shapes (checked
+    by kernel name on a 256-CU part), with the result against a float64
+    product of the same operands."""
+    torch = _torch()
+    gen = torch.Generator(device="cuda").manual_seed(M + N + K + ta)
+    a = torch.rand((K, M) if ta else (M, K), device="cuda", generator=gen) - 0.5
+    b = torch.rand((N, K) if tb else (K, N), device="cuda", generator=gen) - 0.5
+    c = torch.full((M, N), 7.0, device="cuda")
+    be.dispatch_matmul(a, b, c, None, bwpp.MatmulParams(M, N, K, a.shape[1], b.shape[1], N, 0, 0, ta, tb))
+    kern = be.last_kernel
+    if be.cus == 256:
+        assert kern == ("bwpp_gemm_f32_splitk_reduce" if want == "split" else want), kern
+    ad = (a.t() if ta else a).double()
+    bd = (b.t() if tb else b).double()
+    ref = ad @ bd
+    err = ((c.double() - ref).abs().max() / ref.abs().max()).item()
+    assert err <= 1e-5, (kern, err)
+
