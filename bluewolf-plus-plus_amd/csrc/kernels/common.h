@@ -102,10 +102,15 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   v = min(v, xor_u32(v, 32));
   return v;
 }
+// The value returned is the winning lane's own element, not the max of the
+// max reduction: when the maximum is a zero, -0 and +0 compare equal and the
+// max picks either sign, while the strict fold keeps the first one's.
 __device__ __forceinline__ void wave_argmax(float &v, uint32_t &i) {
   const float m = wave_max(v);
-  i = wave_min_u32(v == m ? i : 0xffffffffu);
-  v = m;
+  const uint32_t w = wave_min_u32(v == m ? i : 0xffffffffu);
+  const uint64_t won = __ballot(v == m && i == w);
+  v = won ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)__builtin_ctzll(won))) : m;
+  i = w;
 }
 
 // 128-bit non-temporal global accesses for data streamed exactly once.

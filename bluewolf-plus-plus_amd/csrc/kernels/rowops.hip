@@ -354,18 +354,26 @@ __device__ __forceinline__ void row_reg(const BwppRowArgs &a) {
       if constexpr (FULL) {
         // Two passes over the registers: the lane's max (fmaxf skips NaN,
         // -inf when the lane holds no number), then its first column
-        // holding that value (a backward scan, the last hit wins), which
-        // is the first strict-or-equal maximum of the one-pass rule below.
+        // holding that value and the element there (a backward scan, the
+        // last hit wins), which is the first strict-or-equal maximum of the
+        // one-pass rule below (the element, not fmaxf's result, carries the
+        // sign of a zero maximum).
 #pragma unroll
         for (int j = 0; j < VPT; ++j) m = fmaxf(fmaxf(m, fmaxf(v[j].x, v[j].y)), fmaxf(v[j].z, v[j].w));
+        float mv = m;
 #pragma unroll
         for (int j = VPT - 1; j >= 0; --j) {
           const uint32_t c = chunk_col(j);
           mi = v[j].w == m ? c + 3u : mi;
+          mv = v[j].w == m ? v[j].w : mv;
           mi = v[j].z == m ? c + 2u : mi;
+          mv = v[j].z == m ? v[j].z : mv;
           mi = v[j].y == m ? c + 1u : mi;
+          mv = v[j].y == m ? v[j].y : mv;
           mi = v[j].x == m ? c : mi;
+          mv = v[j].x == m ? v[j].x : mv;
         }
+        m = mv;
       } else {
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {

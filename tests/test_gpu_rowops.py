@@ -255,6 +255,46 @@ def test_reduce_max_axis0(be, oracle, rows, cols):
     assert np.array_equal(host(ix), wi)
 
 
+def _signed_zero_rows(cols, seed):
+    """Rows whose maximum is a zero reached with both signs: -0 first, +0
+    first, the tie split across lanes, waves and the row's two halves, and a
+    row of one lone -0 among negatives."""
+    rng = np.random.default_rng(seed)
+    rows = []
+    for first, second in ((-0.0, 0.0), (0.0, -0.0)):
+        for a, b in ((0, 1), (0, cols // 2), (cols // 3, cols - 1), (1, 64 % cols), (cols - 2, cols - 1)):
+            if a == b or max(a, b) >= cols:
+                continue
+            r = -np.abs(rng.standard_normal(cols)).astype(np.float32) - 0.5
+            r[a], r[b] = first, second
+            rows.append(r)
+    r = -np.abs(rng.standard_normal(cols)).astype(np.float32) - 0.5
+    r[cols // 2] = -0.0
+    rows.append(r)
+    return np.ascontiguousarray(np.stack(rows), np.float32)
+
+
+@pytest.mark.parametrize("cols", [2, 5, 256, 300, 1024, 2000, 4096, 5000, 16384, 32769])
+def test_reduce_max_signed_zero_ties(be, oracle, cols):
+    """A zero maximum keeps the sign of the first zero (the reference's strict
+    fold, bwpp_cpu_ref.c:159-165): maxv bit-exact, argmax its index, along
+    rows (register paths with one and several waves per row, the fallback)
+    and along columns."""
+    torch = _torch()
+    x = _signed_zero_rows(cols, cols)
+    rows = x.shape[0]
+    for axis, xx in ((1, x), (0, np.ascontiguousarray(x.T))):
+        r, c = xx.shape
+        n = r if axis == 1 else c
+        mv = torch.zeros(n, dtype=torch.float32, device="cuda")
+        ix = torch.zeros(n, dtype=torch.int32, device="cuda")
+        be.dispatch_reduce_max(dev(xx), mv, ix, bwpp.ReduceParams(r, c, c, axis))
+        wm, wi = oracle.reduce_max(xx, axis)
+        assert_bits_equal(host(mv), wm, f"axis {axis}")
+        assert np.array_equal(host(ix), wi), f"axis {axis}"
+    assert rows > 2
+
+
 @pytest.mark.parametrize("axis", [0, 1])
 @pytest.mark.parametrize("rows,cols", [(2, 3), (17, 300), (8, 4096), (3, 16385)])
 def test_reduce_max_mask_and_grads(be, oracle, axis, rows, cols):
