@@ -328,14 +328,17 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
   for (int st = 0; st < kStages - 1; ++st)
     if ((uint32_t)st < nkt) issue((uint32_t)st);
 
-  // Tiles before t_mask need no mask for any query of this wave; the rest
-  // go through the masked variant.  Two loops (not one with a branch) keep
-  // a single copy of the O accumulators live; every wave still passes each
-  // tile's barrier once, whichever loop it is in.
+  // Tiles before t_mask need no mask for any query of the block; the rest
+  // go through the masked variant.  Two loops (not one with a branch, which
+  // made the compiler keep a second copy of the O accumulators and spill)
+  // with a block-uniform boundary: every wave passes every tile's barrier
+  // from the same loop.  Inside the masked loop the waves differ only in
+  // wave-uniform branches around MFMA work (the 32-key blocks and tiles
+  // their queries see none of).
   uint32_t t_mask = a.N / kBKV;  // first tile with keys past N
   if (CAUSAL) {
-    // First tile holding a key past query q0's limit q0 + diag.
-    const int64_t first_hidden = (int64_t)q0 + diag + 1;
+    // First tile holding a key past the block's first query's limit.
+    const int64_t first_hidden = (int64_t)qb0 + diag + 1;
     const uint32_t tc = first_hidden <= 0 ? 0u : (uint32_t)min<int64_t>(first_hidden / kBKV, (int64_t)nkt);
     t_mask = min(t_mask, tc);
   }
