@@ -401,7 +401,7 @@ BwppHipStatus bwpp_hip_dispatch_attention_grad(BwppHip *h, const void *q,
  * capture, tight serving loops, harnesses that forbid allocation).  The
  * per-query row sums rowsum(dout * o) live in a device-resident scratch
  * array of the library (8 MiB per GPU, held until the process ends)
- * instead of the handle's workspace, so batch * heads * M must stay below
+ * instead of the handle's workspace, so batch * heads * M may be at most
  * 2,097,151 query rows (UNSUPPORTED beyond, nothing launched).  bf16 rows
  * that are not 16-byte aligned (which need fp32 copies in the workspace)
  * are UNSUPPORTED too.  Every call on one GPU shares that GPU's scratch:

@@ -58,6 +58,27 @@ def test_noalloc_matches_workspace_entry(be, dtype, d, causal):
             assert torch.equal(a, b), (name, B, H, M, N)
 
 
+def test_noalloc_accepts_scratch_maximum(be):
+    """batch * heads * M = 2,097,151 query rows: their row sums (4 bytes
+    each) plus the 4-byte tail fill the 8 MiB scratch exactly, the largest
+    accepted size; results bit-identical to the workspace entry point."""
+    torch = _torch()
+    B, H, M, N, d = 1, 889, 2359, 16, 16  # 889 * 2359 = 2,097,151
+    assert B * H * M == 2_097_151
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q, do = (0.5 * torch.randn((B, H, M, d), device="cuda", generator=g) for _ in range(2))
+    k, v = (0.5 * torch.randn((B, H, N, d), device="cuda", generator=g) for _ in range(2))
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, M), device="cuda")
+    prm = bwpp.AttentionParams(M=M, N=N, K=d, D=d, ldq=d, ldk=d, ldv=d, ldo=d, batch=B, heads=H)
+    be.dispatch_attention_lse(q, k, v, o, lse, prm)
+    got = _grads(be.dispatch_attention_grad_noalloc, q, k, v, o, do, lse, prm)
+    want = _grads(be.dispatch_attention_grad, q, k, v, o, do, lse, prm)
+    for a, b, name in zip(got, want, ("dq", "dk", "dv")):
+        assert torch.isfinite(a).all(), name
+        assert torch.equal(a, b), name
+
+
 def test_noalloc_refuses_beyond_scratch(be):
     """batch * heads * M = 2,097,152 query rows need 8 MiB + 4 bytes of row
     sums: one row over the scratch maximum.  The buffers are real and
