@@ -115,3 +115,39 @@ def test_c_caller_runs():
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
     assert r.stdout.strip().endswith("OK")
+
+
+# ------------------------------------------------------ missing code objects
+def _lib_dir():
+    return os.path.join(ROOT, "bluewolf-plus-plus_amd", "lib")
+
+
+def test_create_with_missing_code_objects(tmp_path):
+    """bwpp_hip_create loads six code objects and resolves every kernel
+    before it returns (the reference's dispatch returns silently on a
+    missing pipeline, dispatch_stub.m:74-79): an empty directory, a
+    directory lacking one object, and an object holding other kernels each
+    give NO_KERNEL naming what is missing, and the library stays usable."""
+    import shutil
+    names = sorted(f for f in os.listdir(_lib_dir()) if f.endswith(".hsaco"))
+    assert len(names) == 6, names
+    empty = tmp_path / "empty"
+    empty.mkdir()
+    with pytest.raises(bwpp.BwppError) as e:
+        bwpp.HipBackend(0, code_object_dir=str(empty))
+    assert e.value.status == bwpp.Status.NO_KERNEL and "hipModuleLoad" in str(e.value)
+    part = tmp_path / "part"
+    part.mkdir()
+    for n in names:
+        if n != "bwpp_attention.hsaco":
+            shutil.copy(os.path.join(_lib_dir(), n), part / n)
+    with pytest.raises(bwpp.BwppError) as e:
+        bwpp.HipBackend(0, code_object_dir=str(part))
+    assert e.value.status == bwpp.Status.NO_KERNEL and "bwpp_attention.hsaco" in str(e.value)
+    # a loadable object with the wrong kernels: the load succeeds, resolution fails
+    shutil.copy(os.path.join(_lib_dir(), "bwpp_grad.hsaco"), part / "bwpp_attention.hsaco")
+    with pytest.raises(bwpp.BwppError) as e:
+        bwpp.HipBackend(0, code_object_dir=str(part))
+    assert e.value.status == bwpp.Status.NO_KERNEL and "not found" in str(e.value)
+    be = bwpp.HipBackend(0)  # the real objects still load
+    be.close()
