@@ -56,6 +56,16 @@ TABLE = {
     "norms.plan": ("norms.bwpp", ["--dim", "B=8192", "--dim", "N=4096"]),
 }
 
+# Programs of this repository's tests (tests/golden/bwpp/), lowered next to
+# their sources: plan file -> (program, arguments).
+TESTS = os.path.join(os.path.dirname(PKG), "tests", "golden", "bwpp")
+TEST_TABLE = {
+    # reduce_max along rows at config 2's shape, and its DSL autodiff
+    "reduce_max.plan": ("reduce_max.bwpp", ["--dim", "M=8192", "--dim", "K=1024", "--dim", "N=4096"]),
+    "reduce_max_train.plan": ("reduce_max.bwpp", ["--dim", "M=8192", "--dim", "K=1024", "--dim", "N=4096",
+                                                  "--train", "seed"]),
+}
+
 
 def build():
     subprocess.run(["make", "-C", HERE, "-s"], check=True)
@@ -64,8 +74,11 @@ def build():
 def emit(name, out_path):
     """Runs bwppc-hip for one table entry (the plan records its command
     line, with the two file arguments reduced to their names)."""
-    example, args = TABLE[name]
-    cmd = [BWPPC, os.path.join(EXAMPLES, example), out_path, *args]
+    if name in TABLE:
+        src_dir, (example, args) = EXAMPLES, TABLE[name]
+    else:
+        src_dir, (example, args) = TESTS, TEST_TABLE[name]
+    cmd = [BWPPC, os.path.join(src_dir, example), out_path, *args]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"{name}: {' '.join(cmd)}\n{r.stderr}")
@@ -81,10 +94,10 @@ def main():
     build()
     bad = []
     with tempfile.TemporaryDirectory() as td:
-        for name in TABLE:
+        for name in [*TABLE, *TEST_TABLE]:
             path = emit(name, os.path.join(td, name))
             text = open(path).read()
-            committed = os.path.join(PLANS, name)
+            committed = os.path.join(PLANS if name in TABLE else TESTS, name)
             if args.check:
                 if not os.path.exists(committed) or open(committed).read() != text:
                     bad.append(name)

@@ -376,3 +376,90 @@ def test_plan_capture_needs_a_stream(be):
         p.capture()
     assert "non-default stream" in str(e.value)
     p.close()
+
+
+# ---------------------------------------------- every committed plan, on GPU
+# Reduced sizes for each committed f32 plan not run above (config-size runs:
+# block_train, the bf16 attention plans and matmul_add_silu).
+_SMALL = {
+    "matmul": dict(M=96, K=80, N=112),
+    "matmul_add_bias_reshape": dict(M=96, K=80, N=112),
+    "multi_fn_bias": dict(M=96, K=80, N=112),
+    "norms": dict(B=64, N=300),
+    "block_fwd": dict(BATCH=2, T=64, D=128, H=256, HEADS=2),
+    "tiny_model_fwd": dict(BATCH=2, T=48, D=128, H=256, V=384, HEADS=2),
+    "attention_train": dict(B=2, H=3, T=100, D=64),
+}
+
+
+def _plan_inputs(cp, seed):
+    """Inputs N(0,1), weights N(0,0.1), gains U[0.5,1.5], by value kind."""
+    binds = {}
+    for i, (name, v) in enumerate(sorted(cp.vals.items())):
+        if v["kind"] not in ("input", "param"):
+            continue
+        shape = tuple(v["dims"])
+        if v["kind"] == "param" and len(shape) == 1 and name.startswith("g"):
+            binds[name] = synth.uniform(shape, seed, i, 0.5, 1.5)
+        elif v["kind"] == "param":
+            binds[name] = synth.normal(shape, seed, i, 0.0, 0.1)
+        else:
+            binds[name] = synth.normal(shape, seed, i)
+    return binds
+
+
+def _run_both(be, oracle, text, seed):
+    import torch
+    cp = CpuPlan(text, oracle)
+    binds = _plan_inputs(cp, seed)
+    for k, v in binds.items():
+        cp.bind(k, v)
+    cp.run()
+    p = plan.Plan(be, text)
+    p.allocate()
+    for k, v in binds.items():
+        p.bind(k, torch.from_numpy(np.ascontiguousarray(v)).cuda())
+    p.run()
+    outs = [n for n, v in cp.vals.items() if v["kind"] == "output"]
+    got = {n: p.host(n, cp.get(n).shape) for n in outs}
+    return cp, p, got
+
+
+@pytest.mark.parametrize("name", sorted(_SMALL))
+def test_committed_plan_on_gpu_matches_cpu_plan(be, oracle, name):
+    """Each committed plan the lowering emits from the reference's examples
+    (examples/*.bwpp), rebound to a reduced size, run by the executor on
+    the GPU against the same plan run op by op on the oracle: every output,
+    1e-4 relative max-norm."""
+    text = plan.load_text(name, **_SMALL[name])
+    cp, p, got = _run_both(be, oracle, text, len(name))
+    assert got
+    for n, g in got.items():
+        assert np.isfinite(g).all(), n
+        assert rel_max_err(g, cp.get(n)) <= TOL, n
+    p.close()
+
+
+def test_reduce_max_program_on_gpu(be, oracle):
+    """tests/golden/bwpp/reduce_max.bwpp lowered by bwppc-hip: y = x @ w,
+    out = reduce_max(y, 1), and with --train seed its DSL autodiff (mask of
+    the row maxima, times the broadcast dout, into both matmul gradients).
+    The forward's maxima are bit-exact against the oracle's reduce_max of
+    the GPU's own y; the whole plans against the CPU plan (1e-4)."""
+    import os
+    fx = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "bwpp")
+    dims = dict(M=300, K=96, N=500)
+    text = plan.load_text(os.path.join(fx, "reduce_max.plan"), **dims)
+    cp, p, got = _run_both(be, oracle, text, 31)
+    y = p.host("y", (dims["M"], dims["N"]))
+    want, _ = oracle.reduce_max(y, 1)
+    from conftest import assert_bits_equal
+    assert_bits_equal(got["out"].reshape(-1), want)
+    assert rel_max_err(got["out"], cp.get("out")) <= TOL
+    p.close()
+    text = plan.load_text(os.path.join(fx, "reduce_max_train.plan"), **dims)
+    cp, p, got = _run_both(be, oracle, text, 31)
+    assert set(got) == {"out", "dx", "dw"}
+    for n, g in got.items():
+        assert rel_max_err(g, cp.get(n)) <= TOL, n
+    p.close()

@@ -118,6 +118,39 @@ def test_tiny_model_forward_plan():
     assert rel_max_err(cp.get("probs"), want) <= 1e-5
 
 
+def test_reduce_max_program_plans(oracle):
+    """reduce_max.bwpp (y = x @ w; out = reduce_max(y, 1)) lowered with and
+    without --train seed: the forward against float64, the backward against
+    float64 autograd (unique maxima: torch's max gradient is the graph's
+    mask * dout there), and with exact ties (duplicated columns of w)
+    against the graph's rule, every tied column gets dout
+    (graph_ir.c:1798-1821, bwpp_cpu_ref.c:192-219)."""
+    import torch
+    M, K, N = 40, 24, 56
+    x, w = synth.normal((M, K), 4, 0), synth.normal((K, N), 4, 1)
+    dout = synth.normal((M, 1), 4, 2)
+    cp = _cpu(os.path.join(FIXTURES, "reduce_max.plan"), {"x": x, "w": w}, M=M, K=K, N=N)
+    y64 = x.astype(np.float64) @ w.astype(np.float64)
+    assert rel_max_err(cp.get("out"), y64.max(axis=1, keepdims=True)) <= 1e-5
+    cp = _cpu(os.path.join(FIXTURES, "reduce_max_train.plan"), {"x": x, "w": w, "dout": dout}, M=M, K=K, N=N)
+    tx, tw = (torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (x, w))
+    out = (tx @ tw).amax(dim=1, keepdim=True)
+    out.backward(torch.tensor(dout, dtype=torch.float64))
+    assert rel_max_err(cp.get("dx"), tx.grad.numpy()) <= 1e-5
+    assert rel_max_err(cp.get("dw"), tw.grad.numpy()) <= 1e-5
+    # exact ties: column 2j + 1 of w repeats column 2j
+    wt = w.copy()
+    wt[:, 1::2] = wt[:, 0::2]
+    cp = _cpu(os.path.join(FIXTURES, "reduce_max_train.plan"), {"x": x, "w": wt, "dout": dout}, M=M, K=K, N=N)
+    y = cp.get("out")
+    yfull = oracle.matmul(x, wt)
+    mask = (yfull == y).astype(np.float64)
+    assert (mask.sum(axis=1) == 2).all()  # each row's maximum is tied
+    dy = mask * dout.astype(np.float64)
+    assert rel_max_err(cp.get("dx"), dy @ wt.astype(np.float64).T) <= 1e-5
+    assert rel_max_err(cp.get("dw"), x.astype(np.float64).T @ dy) <= 1e-5
+
+
 def test_gemm_example_plans(oracle):
     """matmul, bias through a reshape and across inlined functions (fused
     as the GEMM epilogue), and norms (matmul -> softmax -> rmsnorm)."""
