@@ -54,6 +54,36 @@ def test_committed_plans_match_the_lowering():
     assert r.returncode == 0, r.stdout + r.stderr
 
 
+@needs_reference
+def test_inspection_flags(bwppc, tmp_path):
+    """--dot / --grad-dot / --mem-plan keep the reference CLI's names
+    (compiler/main.c:49-86): the forward and autodiff graphs as DOT
+    (bwpp_graph_dump_dot, main.c:133-157), and the memory plan of the
+    emitted launch plan (main.c:169-182), which is exactly what the library
+    reports for that plan at run time: the reference dump's lines
+    (mem_plan.c:176-193) with byte sizes, offsets and the arena total."""
+    src = os.path.join(REFERENCE, "examples", "tiny_model.bwpp")
+    mem, dot, gdot = tmp_path / "mem.txt", tmp_path / "g.dot", tmp_path / "grad.dot"
+    args = ["--entry", "block", "--dim", "T=64", "--dim", "D=128", "--dim", "H=256", "--batch", "2",
+            "--heads", "2", "--causal", "--attn-scale", "auto", "--train", "mean_square"]
+    text = lower(bwppc, src, tmp_path, *args, "--mem-plan", str(mem), "--dot", str(dot), "--grad-dot", str(gdot))
+    p = plan.Plan(None, text)
+    report = mem.read_text()
+    assert report == p.report()
+    assert report.startswith("buffers=") and f"arena_bytes={p.arena_bytes}" in report
+    lines = report.splitlines()
+    nbuf = int(lines[0].split()[0].split("=")[1])
+    assert sum(ln.startswith("buffer") for ln in lines[1:]) == nbuf
+    p.close()
+    fwd, grad = dot.read_text(), gdot.read_text()
+    assert fwd.startswith("digraph") and grad.startswith("digraph")
+    assert "rmsnorm" in fwd and "softmax_grad" in grad
+    # the flags leave the plan itself unchanged (up to its recorded command line)
+    plain = lower(bwppc, src, tmp_path, *args)
+    strip = lambda t: "\n".join(ln for ln in t.splitlines() if not ln.startswith("# generated"))
+    assert strip(text) == strip(plain)
+
+
 def test_committed_plans_pass_the_executor_checks():
     names = sorted(f for f in os.listdir(PLANS) if f.endswith(".plan"))
     assert "block_train.plan" in names and "attention_train_bf16.plan" in names
