@@ -691,9 +691,11 @@ def _extras_c4(be, torch, seed, iters, orc, out):
             entry["cpu"] = {"GFLOP_s": round(fl / (B * H) / dt / 1e9, 3), "cores": 1, "kind": "port",
                             "sample": "one (batch, head) slice (extrapolated rate)"}
         out["c4_attention_causal" if causal else "c4_attention"] = entry
-    # Attention backward at the C4 shape (bf16 matrix-core dQ and dK/dV
-    # passes after a forward that saves lse): 5 products of 2*S*S*d per
-    # slice (S and dP recomputed, dV, dQ, dK) = 2.5x the forward FLOP.
+    # Attention backward at the C4 shape (bf16 matrix-core passes after a
+    # forward that saves lse): 5 products of 2*S*S*d per slice (S, dP, dV,
+    # dK, dQ) = 2.5x the forward FLOP.  The default stored-dS scheme runs
+    # exactly these (D_m pass; dK/dV pass that also stores dS; dQ = dS K
+    # pass); with it off, the dQ pass recomputes S and dP (7 products).
     dout = _bf16(torch, synth.normal((B, H, S, d), seed, 3))
     lse = torch.empty((B, H, S), device="cuda")
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
@@ -705,7 +707,13 @@ def _extras_c4(be, torch, seed, iters, orc, out):
         us = _events_us(torch, lambda: be.dispatch_attention_grad(q, k, v, o, dout, lse, dq, dk, dv, p),
                         max(3, iters // 3), stats=st)
         fl = 2.5 * (full / 2 if causal else full)
-        entry = {"kernel": "bwpp_attn_bwd_bf16_mfma_d128" + ("_causal" if causal else "") + "_dq + " + be.last_kernel,
+        cs = "_causal" if causal else ""
+        last = be.last_kernel
+        if last.endswith("_dq_ds"):  # stored dS: D_m, 8-wave dK/dV + dS, dQ = dS K
+            kern = f"bwpp_attn_bwd_bf16_d128_dsum + bwpp_attn_bwd_bf16_mfma_d128{cs}_dkdv_w8_ds + {last}"
+        else:
+            kern = f"bwpp_attn_bwd_bf16_mfma_d128{cs}_dq + {last}"
+        entry = {"kernel": kern,
                  "us_per_launch": round(us, 1), **st, "TFLOP_s": round(fl / us / 1e6, 1),
                  "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
         if orc is not None:

@@ -85,6 +85,11 @@ typedef struct {
   float scale; /* the plain score scale (fp32 MFMA path, which gets scale * log2(e) in scale_log2) */
   uint32_t zigzag; /* fp32 MFMA causal kernels: tile order heavy ranks first, then the light ones
                       lightest first (a one-wave grid then pairs heavy with light on each CU) */
+  /* bf16 backward with a stored dS: dS^T per slice as [N][ld_dst] bf16
+   * (written by the dK/dV pass, read by the dQ pass), slice stride
+   * N * ld_dst elements. */
+  void *dst;
+  uint32_t ld_dst;
 } BwppAttnArgs;
 
 /* Attention operand copies between the caller's strided bf16 layout

@@ -43,6 +43,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef short v4s_t __attribute__((ext_vector_type(4)));
 typedef short v8s_t __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
@@ -98,6 +99,7 @@ __device__ __forceinline__ void g2lds16(const void *gptr, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(gptr) : "memory");
 }
 
+
 // Two [TR x D] bf16 tiles (rows r0..; a row past `rows` re-reads row
 // rows - 1, which the callers mask) loaded straight into an LDS stage in
 // 1 KiB blocks: lane l of block b fills physical chunk l % (D / 8) of tile
@@ -119,6 +121,15 @@ struct TileDmaB {
   }
   // lx, ly: LDS byte addresses of the two destination tiles; wv: the wave
   // index (uniform).
+  // One tile only.
+  __device__ __forceinline__ void issue1(const uint16_t *X, uint32_t ldx, uint32_t r0, uint32_t rows, uint32_t lx,
+                                         uint32_t wv) const {
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+      const uint32_t r = r0 + row[i], rr = r < rows ? r : rows - 1;
+      g2lds16(X + (size_t)rr * ldx + col[i], lx + (wv * BPW + (uint32_t)i) * 1024u);
+    }
+  }
   __device__ __forceinline__ void issue(const uint16_t *X, uint32_t ldx, const uint16_t *Y, uint32_t ldy,
                                         uint32_t r0, uint32_t rows, uint32_t lx, uint32_t ly, uint32_t wv) const {
 #pragma unroll
@@ -285,6 +296,40 @@ struct SliceB {
   }
 };
 
+// D_m = rowsum(dO * O) of query row qi (gf: the lane's half of dO's row):
+// lane halves 0 / 1 sum d = 16 ks + 8 hi .. +7 in order, then add.  The dQ
+// pass and the D_m pass both use it, so both give the same bits.
+template <int D>
+__device__ __forceinline__ float row_dsum(const bf16x8_t (&gf)[D / 16], const uint16_t *O, uint32_t ldo,
+                                          uint32_t qi, uint32_t M, int hi) {
+  bf16x8_t of[D / 16];
+  load_row<D>(of, O, ldo, qi, M, hi);
+  float part = 0.0f;
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part += (float)gf[ks][e] * (float)of[ks][e];
+  return sum32(part);
+}
+
+// D_m pass of the stored-dS scheme (which has no dQ pass before the dK / dV
+// pass): a wave per 32 query rows, kW waves per block, q_tiles blocks per
+// slice.
+template <int D, int kW>
+__device__ __forceinline__ void bwd_dsum(const BwppAttnArgs &a) {
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const int li = lane & 31, hi = lane >> 5;
+  const uint32_t bh = blockIdx.x / a.q_tiles, tile = blockIdx.x % a.q_tiles;
+  const uint32_t b = bh / a.heads, h = bh % a.heads;
+  const uint16_t *O = static_cast<const uint16_t *>(a.o) + b * a.o_bs + h * a.o_hs;
+  const uint16_t *dO = static_cast<const uint16_t *>(a.dout) + b * a.o_bs + h * a.o_hs;
+  const uint32_t qi = (tile * kW + (uint32_t)wave) * kR + (uint32_t)li;
+  bf16x8_t gf[D / 16];
+  load_row<D>(gf, dO, a.ldo, qi, a.M, hi);
+  const float dsum = row_dsum<D>(gf, O, a.ldo, qi, a.M, hi);
+  if (qi < a.M && hi == 0) a.dsum[(size_t)bh * a.M + qi] = dsum;
+}
+
 // dQ pass: a wave owns 32 queries and streams K / V tiles; also writes
 // D_m = rowsum(dO * O) for the dK / dV pass.
 template <int D, bool CAUSAL, int kW, int TR>
@@ -315,17 +360,7 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
   bf16x8_t qf[D / 16], gf[D / 16];
   load_row<D>(qf, Q, a.ldq, qi, a.M, hi);
   load_row<D>(gf, dO, a.ldo, qi, a.M, hi);
-  float dsum;
-  {
-    bf16x8_t of[D / 16];
-    load_row<D>(of, O, a.ldo, qi, a.M, hi);
-    float part = 0.0f;
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) part += (float)gf[ks][e] * (float)of[ks][e];
-    dsum = sum32(part);
-  }
+  const float dsum = row_dsum<D>(gf, O, a.ldo, qi, a.M, hi);
   if (qi < a.M && hi == 0) a.dsum[(size_t)sl.bh * a.M + qi] = dsum;
   // Queries past M: +inf makes every probability exp2(-inf) = 0.
   const float lse2 = qi < a.M ? a.lse[(size_t)sl.bh * a.M + qi] * kLog2e : INFINITY;
@@ -392,9 +427,145 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
   if (qi < a.M) store_t<D>(dQ, a.ldq, qi, dq, a.scale, hi);
 }
 
+// Stored dS^T layout: per slice, 2 KiB blocks of 32 keys x 32 queries,
+// [group of 4 query blocks][key block][query block in the group] (query
+// blocks padded to ld_dst / 32, a multiple of 4): the dQ pass's block (one
+// group) then reads one contiguous stream.  Inside a block the 8-byte
+// piece holding queries 4 qd .. +3 of key k sits at
+//   512 (qd / 2) + 16 (k ^ 4 (qd / 2)) + 8 (qd % 2),
+// so a wave of the dK / dV pass (lane = key, holding quads 2 x + hi of one
+// quad pair x per store) writes 512 contiguous bytes per store, the dQ
+// pass's DMA copies whole blocks, and its transposing reads (four keys x
+// eight quads per 32 lanes) hit 64 distinct banks: the XOR moves the four
+// quad pairs, which are 512 bytes apart, onto different 16-byte slots.
+struct DsBlk {
+  static constexpr uint32_t kBytes = 2048;
+  // Byte offset of block (key block kb, query block qb) of slice bh; n32
+  // key blocks, m32 query blocks per slice.
+  __device__ __forceinline__ static size_t at(uint32_t bh, uint32_t kb, uint32_t qb, uint32_t n32, uint32_t m32) {
+    return ((((size_t)bh * (m32 / 4u) + qb / 4u) * n32 + kb) * 4u + qb % 4u) * kBytes;
+  }
+  // Offset of key k's piece of quad hi (quad pair 0).
+  __device__ __forceinline__ static uint32_t piece(uint32_t k, uint32_t hi) { return 16u * k + 8u * hi; }
+  // The same piece in quad pair x: key bits 2-3 are offset bits 6-7.
+  __device__ __forceinline__ static uint32_t pair(uint32_t off, uint32_t x) { return 512u * x + (off ^ (64u * x)); }
+};
+
+// dQ pass of the stored-dS scheme: dQ = scale dS K with dS^T read from
+// a.dst (written by the dK / dV pass) instead of recomputed from S and dP.
+// A wave owns 32 queries (one query block); the block streams TR-key tiles
+// of K and the matching dS^T blocks through an NS-stage ring (the dS^T
+// stream comes from HBM, so NS - 1 tiles are in flight while one is used).
+// The same 32 x 32 blocks as in bwd_dq are visited (the dK / dV pass
+// stores exactly those), and each MFMA gets the same operands in the same
+// slots, so dQ is bit-identical to bwd_dq's but for the sign of all-zero
+// sums.
+template <bool CAUSAL, int TR, int NS>
+__device__ __forceinline__ void bwd_dq_ds(const BwppAttnArgs &a) {
+  constexpr int D = 128, DB = D / 32, kW = 4, TB = TR * D * 2, RB = D * 2;
+  constexpr int KB = TR / kR;                                           // key blocks per tile
+  constexpr uint32_t SB = (uint32_t)(KB * kW) * DsBlk::kBytes;          // dS^T bytes per tile
+  static_assert(SB == (uint32_t)TB, "a dS^T tile (TR keys x 128 queries) is as large as a K tile");
+  constexpr int SPW = (int)(SB / 1024u) / kW;                           // 1 KiB DMA pieces per wave
+  constexpr int LPT = TileDmaB<D, kW, TR>::BPW + SPW;                   // loads per wave per tile
+  static_assert(NS >= 2 && NS <= 5 && LPT * (NS - 2) < 64, "ring depth");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[NS][2][TB];  // [stage][K, dS^T]
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const int li = lane & 31, hi = lane >> 5;
+  const SliceB<CAUSAL> sl(a);
+  const uint32_t qt = a.q_tiles - 1 - sl.tile;  // heaviest (causal) first
+  const uint32_t qb = qt * (kW * kR), q0 = qb + (uint32_t)wave * kR, qi = q0 + (uint32_t)li;
+  const uint32_t n32 = (a.N + 31u) / 32u, m32 = a.ld_dst / 32u;
+  const uint16_t *K = static_cast<const uint16_t *>(a.k) + sl.b * a.k_bs + sl.h * a.k_hs;
+  // The block's query group: 8 KiB (its 4 query blocks) per key block.
+  const unsigned char *S = static_cast<const unsigned char *>(a.dst) + DsBlk::at(sl.bh, 0, qb / 32u, n32, m32);
+  uint16_t *dQ = static_cast<uint16_t *>(a.dq) + sl.b * a.q_bs + sl.h * a.q_hs;
+  const int64_t diag = (int64_t)a.N - (int64_t)a.M;
+
+  uint32_t kend = a.N;
+  if (CAUSAL) {
+    const int64_t last = (int64_t)min(a.M, qb + kW * kR) - 1 + diag;
+    kend = last < 0 ? 0u : (uint32_t)min<int64_t>(last + 1, (int64_t)a.N);
+  }
+  const uint32_t nt = (kend + TR - 1) / TR;
+  const int64_t wlast = (int64_t)q0 + kR - 1 + diag;
+  const Offsets<D> off(lane);
+  // Transposing reads of a dS^T block: 16-lane group g reads keys
+  // 4 (g / 2) + L / 4 (+ 8 for the high half) x quad 4 (g % 2) + L % 4, as
+  // tr_operand does on a row-major tile.
+  uint32_t slo, shi;
+  {
+    const uint32_t grp = (uint32_t)((lane >> 4) & 3), L = (uint32_t)(lane & 15);
+    const uint32_t rb = 4u * (grp >> 1) + (L >> 2), qd = 4u * (grp & 1u) + (L & 3u);
+    slo = DsBlk::pair(DsBlk::piece(rb, qd & 1u), qd >> 1);
+    shi = DsBlk::pair(DsBlk::piece(rb + 8u, qd & 1u), qd >> 1);
+  }
+  f32x16_t dq[DB];
+#pragma unroll
+  for (int blk = 0; blk < DB; ++blk) dq[blk] = f32x16_t{};
+
+  const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)&lds[0][0][0];
+  const TileDmaB<D, kW, TR> dma(wave, lane);
+  auto issue = [&](uint32_t t) {  // K tile t / its dS^T blocks into stage t % NS
+    const uint32_t sb = lds0 + (t % (uint32_t)NS) * (uint32_t)(2 * TB);
+    dma.issue1(K, a.ldk, t * TR, a.N, sb, wv);
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+      const uint32_t j = wv * (uint32_t)SPW + (uint32_t)i;  // 1 KiB piece of the tile
+      const uint32_t kb = min(t * (uint32_t)KB + j / 8u, n32 - 1u);  // past N: re-read the last block (masked)
+      g2lds16(S + (size_t)kb * (4u * DsBlk::kBytes) + (j % 8u) * 1024u + 16u * (uint32_t)lane,
+              sb + (uint32_t)TB + j * 1024u);
+    }
+  };
+  // Tile t's loads are done once at most (tiles issued after it) x LPT of
+  // this wave's loads are outstanding (they complete in order).
+  auto wait_tile = [&](uint32_t later) {
+    if (NS > 4 && later >= 3) wait_vmcnt<(NS > 4 ? 3 * LPT : 0)>();
+    else if (NS > 3 && later >= 2) wait_vmcnt<(NS > 3 ? 2 * LPT : 0)>();
+    else if (NS > 2 && later >= 1) wait_vmcnt<(NS > 2 ? LPT : 0)>();
+    else wait_vmcnt<0>();
+  };
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i)
+    if ((uint32_t)i < nt) issue((uint32_t)i);
+  for (uint32_t t = 0; t < nt; ++t) {
+    wait_tile(min(nt - 1u - t, (uint32_t)(NS - 2)));
+    __syncthreads();  // tile t in LDS; every wave is done with tile t - 1
+    if (t + NS - 1 < nt) issue(t + NS - 1);
+    const uint32_t st = t % (uint32_t)NS;
+#pragma unroll
+    for (int sb = 0; sb < KB; ++sb) {
+      const uint32_t k0 = t * TR + sb * kR;
+      const unsigned char *Kt = lds[st][0] + sb * kR * RB;
+      const unsigned char *Sb = lds[st][1] + (sb * kW + wave) * DsBlk::kBytes;
+      if ((TR == kR || k0 < kend) && (!CAUSAL || (int64_t)k0 <= wlast)) {
+        // Keys past N (their rows re-read row N - 1): dS = 0.
+        const bool edge = k0 + kR > a.N;
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq) {
+          const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Sb + slo + 256u * kq));
+          const v4s_t hv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Sb + shi + 256u * kq));
+          v8s_t x = {lo[0], lo[1], lo[2], lo[3], hv[0], hv[1], hv[2], hv[3]};
+          if (edge) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              if (k0 + 16u * kq + (uint32_t)acc_row(j, hi) >= a.N) x[j] = 0;
+          }
+          const bf16x8_t w = __builtin_bit_cast(bf16x8_t, x);
+#pragma unroll
+          for (int blk = 0; blk < DB; ++blk) dq[blk] = mfma16(tr_operand<D>(Kt, off, blk, kq), w, dq[blk]);
+        }
+      }
+    }
+  }
+  if (qi < a.M) store_t<D>(dQ, a.ldq, qi, dq, a.scale, hi);
+}
+
 // dK / dV pass: a wave owns 32 keys and streams Q / dO tiles with their
-// lse and D_m.
-template <int D, bool CAUSAL, int kW, int TR, bool VL = false>
+// lse and D_m.  WS: also stores dS^T (bf16, as it enters the dK product) to
+// a.dst for bwd_dq_ds.
+template <int D, bool CAUSAL, int kW, int TR, bool VL = false, bool WS = false>
 __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
   constexpr int DB = D / 32, TB = TR * D * 2, RB = D * 2;
   __shared__ __attribute__((aligned(16))) unsigned char lds[2][2][TB];  // [stage][Q, dO]
@@ -426,6 +597,45 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
   const uint32_t nt = a.M > mbeg ? (a.M - mbeg + TR - 1) / TR : 0u;
   const int64_t wfirst = (int64_t)k0w - diag;  // first query that sees any key of the wave
 
+  // The wave's dS^T blocks (DsBlk): key block k0w / 32 of the slice, query
+  // block m0 / 32; dso: this lane's piece offset for query quads 0 / 1
+  // (quad pair x: + 512 x, key bits 2-3 ^ x).
+  unsigned char *dsblk = nullptr;
+  uint32_t dso = 0, n32 = 0, m32 = 0;
+  if constexpr (WS) {
+    dsblk = static_cast<unsigned char *>(a.dst);
+    n32 = (a.N + 31u) / 32u;
+    m32 = a.ld_dst / 32u;
+    dso = DsBlk::piece(li, hi);
+  }
+  // A tile's dS^T pieces are stored at the start of the next tile (or after
+  // the loop): the wait for the next tile's DMA at the end of a tile also
+  // waits for every store issued before it, and a tile later the stores
+  // have drained.  pend_q: query block of each pending sub-block, or ~0.
+  constexpr int NSB = TR / kR;
+  uint4 pend[WS ? NSB : 1][2];
+  uint32_t pend_q[WS ? NSB : 1];
+#pragma unroll
+  for (int i = 0; i < (WS ? NSB : 1); ++i) pend_q[i] = ~0u;
+  auto flush = [&]() {
+    if constexpr (WS) {
+#pragma unroll
+      for (int i = 0; i < NSB; ++i)
+        if (pend_q[i] != ~0u) {
+          unsigned char *blk = dsblk + DsBlk::at(sl.bh, k0w / 32u, pend_q[i], n32, m32);
+#pragma unroll
+          for (int kq = 0; kq < 2; ++kq) {
+            // Streaming stores (nt): read once, by the dQ pass, and kept out
+            // of the way of the Q / dO tiles in L2 (the dQ pass 4 % faster).
+            __builtin_nontemporal_store(u32x2_t{pend[i][kq].x, pend[i][kq].y},
+                                        reinterpret_cast<u32x2_t *>(blk + DsBlk::pair(dso, 2 * kq)));
+            __builtin_nontemporal_store(u32x2_t{pend[i][kq].z, pend[i][kq].w},
+                                        reinterpret_cast<u32x2_t *>(blk + DsBlk::pair(dso, 2 * kq + 1)));
+          }
+          pend_q[i] = ~0u;
+        }
+    }
+  };
   bf16x8_t kf[D / 16], vf[D / 16];
   load_row<D>(kf, K, a.ldk, ni, a.N, hi);
   load_row<D>(vf, V, a.ldv, ni, a.N, hi);
@@ -473,6 +683,7 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
   __syncthreads();
   for (uint32_t t = 0; t < nt; ++t) {
     const int st = (int)(t & 1);
+    flush();
     if (t + 1 < nt) {
       issue(t + 1);
       fetch_rows(mbeg + (t + 1) * TR);
@@ -526,6 +737,13 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
 #pragma unroll
         for (int kq = 0; kq < 2; ++kq) {
           const bf16x8_t wp = acc_operand(s, kq), wd = acc_operand(ds, kq);
+          if constexpr (WS) {
+            // Elements 0-3 / 4-7 of wd: query quads 4 kq + hi / 4 kq + 2 + hi
+            // of key ni, i.e. quad pairs x = 2 kq / 2 kq + 1: two 512-byte
+            // stores per wave.  A wave past N has no block to write.
+            pend[sb][kq] = __builtin_bit_cast(uint4, wd);
+            if (kq == 1 && k0w < a.N) pend_q[sb] = m0 / 32u;
+          }
 #pragma unroll
           for (int blk = 0; blk < DB; ++blk) {
             dv[blk] = mfma16(tr_operand<D>(Gt, off, blk, kq), wp, dv[blk]);  // dV^T += dO^T P
@@ -538,6 +756,7 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
     wait_vmcnt<0>();
     __syncthreads();
   }
+  flush();
   if (ni < a.N) {
     store_t<D>(dK, a.ldk, ni, dk, a.scale, hi);
     store_t<D>(dV, a.ldv, ni, dv, 1.0f, hi);
@@ -581,3 +800,24 @@ extern "C" __global__ __launch_bounds__(512) void bwpp_attn_bwd_bf16_mfma_d128_d
 extern "C" __global__ __launch_bounds__(512) void bwpp_attn_bwd_bf16_mfma_d128_causal_dkdv_w8(const BwppAttnArgs a) {
   bwd_dkdv<128, true, 8, kR, true>(a);
 }
+
+// The stored-dS scheme (d = 128): D_m pass, dK / dV passes that also store
+// dS^T (4 and 8 waves), and the dQ = dS K pass.
+extern "C" __global__ __launch_bounds__(256) void bwpp_attn_bwd_bf16_d128_dsum(const BwppAttnArgs a) {
+  bwd_dsum<128, 4>(a);
+}
+#define BWPP_ATTN_BWD_BF16_DS(CAUSAL, SUFFIX)                                                        \
+  extern "C" __global__ __launch_bounds__(256) void bwpp_attn_bwd_bf16_mfma_d128##SUFFIX##_dkdv_ds(   \
+      const BwppAttnArgs a) {                                                                       \
+    bwd_dkdv<128, CAUSAL, kWK, kTR, false, true>(a);                                                \
+  }                                                                                                 \
+  extern "C" __global__ __launch_bounds__(512) void bwpp_attn_bwd_bf16_mfma_d128##SUFFIX##_dkdv_w8_ds( \
+      const BwppAttnArgs a) {                                                                       \
+    bwd_dkdv<128, CAUSAL, 8, kR, true, true>(a);                                                    \
+  }                                                                                                 \
+  extern "C" __global__ __launch_bounds__(256) void bwpp_attn_bwd_bf16_mfma_d128##SUFFIX##_dq_ds(     \
+      const BwppAttnArgs a) {                                                                       \
+    bwd_dq_ds<CAUSAL, kTR, 2>(a);                                                                   \
+  }
+BWPP_ATTN_BWD_BF16_DS(false, )
+BWPP_ATTN_BWD_BF16_DS(true, _causal)

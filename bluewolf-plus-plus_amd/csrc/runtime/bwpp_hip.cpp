@@ -94,6 +94,11 @@ struct BwppHip {
   hipFunction_t attn_bf16_dq[2][2] = {}, attn_bf16_dkdv[2][2] = {};
   hipFunction_t attn_bf16_dkdv_w8[2] = {};  // d = 128, 8 waves per block; [causal]
   uint32_t attn_w8_mask = 3u;  // BWPP_ATTN_BWD_W8: bit c set = 8-wave dK/dV pass allowed when causal == c
+  // bf16 d = 128 backward with a stored dS (D_m pass, dK/dV pass storing
+  // dS^T, dQ = dS K pass): [causal]
+  hipFunction_t attn_bf16_dsum = nullptr, attn_bf16_dkdv_ds[2] = {}, attn_bf16_dkdv_w8_ds[2] = {},
+                attn_bf16_dq_ds[2] = {};
+  uint64_t attn_ds_max = 8ull << 30;  // BWPP_ATTN_BWD_DS_MB: largest dS^T workspace in bytes (0: scheme off)
   hipFunction_t attn_conv_to_f32 = nullptr, attn_conv_to_bf16 = nullptr;  // bf16 <-> fp32 operand copies
   hipFunction_t rmsnorm_grad_w[4] = {};  // wave-per-row rmsnorm_grad, 256 / 512 / 1024 / 2048 columns
   hipFunction_t silu_grad = nullptr, softmax_grad = nullptr, rmsnorm_grad = nullptr, col_partials_sum = nullptr,
@@ -204,6 +209,13 @@ BwppHipStatus resolve_all(BwppHip *h) {
       {"bwpp_attn_conv_bf16_to_f32", &h->attn_conv_to_f32}, {"bwpp_attn_conv_f32_to_bf16", &h->attn_conv_to_bf16},
       {"bwpp_attn_bwd_bf16_mfma_d128_dkdv_w8", &h->attn_bf16_dkdv_w8[0]},
       {"bwpp_attn_bwd_bf16_mfma_d128_causal_dkdv_w8", &h->attn_bf16_dkdv_w8[1]},
+      {"bwpp_attn_bwd_bf16_d128_dsum", &h->attn_bf16_dsum},
+      {"bwpp_attn_bwd_bf16_mfma_d128_dkdv_ds", &h->attn_bf16_dkdv_ds[0]},
+      {"bwpp_attn_bwd_bf16_mfma_d128_causal_dkdv_ds", &h->attn_bf16_dkdv_ds[1]},
+      {"bwpp_attn_bwd_bf16_mfma_d128_dkdv_w8_ds", &h->attn_bf16_dkdv_w8_ds[0]},
+      {"bwpp_attn_bwd_bf16_mfma_d128_causal_dkdv_w8_ds", &h->attn_bf16_dkdv_w8_ds[1]},
+      {"bwpp_attn_bwd_bf16_mfma_d128_dq_ds", &h->attn_bf16_dq_ds[0]},
+      {"bwpp_attn_bwd_bf16_mfma_d128_causal_dq_ds", &h->attn_bf16_dq_ds[1]},
   };
   for (auto &e : singles)
     if ((s = resolve(h, e.name, e.slot)) != BWPP_HIP_OK) return s;
@@ -397,6 +409,7 @@ BwppHipStatus bwpp_hip_create(BwppHip **out, int device, const char *code_object
   if (const char *zz = getenv("BWPP_ATTN_ZIGZAG")) h->attn_zigzag = atoi(zz) != 0 ? 1u : 0u;
   if (const char *fp = getenv("BWPP_GEMM_F32_PIPE")) h->gemm_f32_pipe = (uint32_t)std::min(std::max(atoi(fp), 0), 3);
   if (const char *w8 = getenv("BWPP_ATTN_BWD_W8")) h->attn_w8_mask = (uint32_t)strtoul(w8, nullptr, 10) & 3u;
+  if (const char *dm = getenv("BWPP_ATTN_BWD_DS_MB")) h->attn_ds_max = (uint64_t)strtoull(dm, nullptr, 10) << 20;
   if (const char *gm = getenv("BWPP_GEMM_GROUP_M")) {
     const uint32_t v = (uint32_t)strtoul(gm, nullptr, 10);
     if (v > 0) h->gemm_group_m = v;
@@ -1141,16 +1154,28 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
       return fail(h, BWPP_HIP_ERR_ALIAS, "attention_grad: dq, dk and dv overlap");
   }
   const size_t dsum_bytes = (size_t)slices * p.M * sizeof(float) + 4;
+  const int bf = p.dtype == BWPP_HIP_BF16 ? 1 : 0, causal = p.causal ? 1 : 0;
+  const float scale = p.scale != 0.0f ? p.scale : 1.0f;
+  const int bf16v = attn_bf16_bwd_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
+  // Stored-dS scheme (bf16, d = 128, not the allocation-free entry): the
+  // dK / dV pass also stores dS^T (bf16 in 2 KiB blocks of 32 keys x 32
+  // queries, keys padded to 32, queries to whole 128-query blocks: ld_dst)
+  // and the dQ pass only multiplies it by K, so S and dP are computed once
+  // instead of in both passes.  It needs 2 * B*H * ceil32(N) * ld_dst bytes
+  // of workspace, up to attn_ds_max.
+  const uint64_t ld_dst = ((uint64_t)p.M + 127ull) / 128ull * 128ull;
+  const uint64_t ds_off = ((uint64_t)dsum_bytes + 255ull) & ~255ull;
+  const uint64_t ds_bytes = slices * (((uint64_t)p.N + 31ull) / 32ull * 32ull) * ld_dst * 2ull;
+  const bool use_ds = !dsum_buf && bf16v == 1 && p.M > 0 && p.N > 0 && ds_bytes <= h->attn_ds_max &&
+                      ld_dst <= 0xffffffffull;
   if (dsum_buf) {
     if (dsum_bytes > dsum_cap)
       return fail(h, BWPP_HIP_ERR_UNSUPPORTED,
                   "attention_grad_noalloc: batch*heads*M = %llu query rows need %zu bytes of scratch, above the "
                   "%zu-byte maximum", (unsigned long long)(slices * p.M), dsum_bytes, dsum_cap);
-  } else if ((s = ensure_ws(h, dsum_bytes)) != BWPP_HIP_OK) {
+  } else if ((s = ensure_ws(h, use_ds ? (size_t)(ds_off + ds_bytes) : dsum_bytes)) != BWPP_HIP_OK) {
     return s;
   }
-  const int bf = p.dtype == BWPP_HIP_BF16 ? 1 : 0, causal = p.causal ? 1 : 0;
-  const float scale = p.scale != 0.0f ? p.scale : 1.0f;
   g.scale_log2 = scale;
   g.lse = const_cast<float *>(lse);
   g.dout = dout;
@@ -1181,7 +1206,27 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   const int f32v = attn_f32_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
   if (f32v >= 0)
     return run_mfma(g, h->attn_f32_dq[f32v][causal], h->attn_f32_dkdv[f32v][causal]);
-  const int bf16v = attn_bf16_bwd_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
+  if (use_ds) {
+    BwppAttnArgs f = g;
+    f.scale = scale;
+    f.scale_log2 = scale * 1.4426950408889634f;
+    f.dst = static_cast<unsigned char *>(h->ws) + ds_off;
+    f.ld_dst = (uint32_t)ld_dst;
+    f.q_tiles = (p.M + 127) / 128;  // 4-wave blocks of the D_m and dQ passes
+    uint64_t grid = slices * f.q_tiles;
+    if (grid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
+    if ((s = launch(h, h->attn_bf16_dsum, (uint32_t)grid, 1, 1, 256, f)) != BWPP_HIP_OK) return s;
+    const bool w8 = ((h->attn_w8_mask >> causal) & 1u) && slices * ((p.N + 255ull) / 256ull) >= (uint64_t)h->cus;
+    const uint32_t wk = w8 ? 8u : kAttnWaves;
+    BwppAttnArgs fk = f;
+    fk.q_tiles = (p.N + 32 * wk - 1) / (32 * wk);  // key tiles
+    const uint64_t kgrid = slices * fk.q_tiles;
+    if (kgrid > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
+    if ((s = launch(h, w8 ? h->attn_bf16_dkdv_w8_ds[causal] : h->attn_bf16_dkdv_ds[causal], (uint32_t)kgrid, 1,
+                        1, 64 * wk, fk)) != BWPP_HIP_OK)
+      return s;
+    return launch(h, h->attn_bf16_dq_ds[causal], (uint32_t)grid, 1, 1, 256, f);
+  }
   if (bf16v >= 0) {
     // d = 128: the dK/dV pass with 8 waves (256 keys) per block (one block
     // per CU) when that grid still gives every CU a block; below that the

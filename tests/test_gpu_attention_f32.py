@@ -249,44 +249,45 @@ def test_bf16_grad_unaligned_rows(be, oracle, B, H, M, N, D, causal):
     _bf16_grad_case(be, oracle, B, H, M, N, D, causal, D + 4)
 
 
-def _backend_with(monkeypatch, w8_mask):
+def _backend_with(monkeypatch, w8_mask, ds=True):
+    """A backend with the 8-wave dK/dV pass allowed per w8_mask (bit 0
+    unmasked, bit 1 causal) and the stored-dS scheme on or off."""
     monkeypatch.setenv("BWPP_ATTN_BWD_W8", str(w8_mask))
+    if ds:
+        monkeypatch.delenv("BWPP_ATTN_BWD_DS_MB", raising=False)
+    else:
+        monkeypatch.setenv("BWPP_ATTN_BWD_DS_MB", "0")
     be = bwpp.HipBackend(0)
     be.set_stream(_torch().cuda.current_stream())
     return be
 
 
 W8_DKDV = "bwpp_attn_bwd_bf16_mfma_d128{}_dkdv_w8"
+DQ_DS = "bwpp_attn_bwd_bf16_mfma_d128{}_dq_ds"
 
 
 @pytest.mark.parametrize("M,N", [(40, 70), (70, 40)])
 @pytest.mark.parametrize("causal", [False, True])
-def test_bf16_grad_8wave(oracle, monkeypatch, M, N, causal):
+@pytest.mark.parametrize("ds", [False, True])
+def test_bf16_grad_8wave(oracle, monkeypatch, M, N, causal, ds):
     """d = 128 with one slice per CU: slices x ceil(N / 256) blocks give
     every CU one, so the runtime takes the 8-wave dK/dV pass (256 keys per
-    block, V rows in LDS) -- checked against the oracle, and the launch is
-    checked to have been that kernel."""
-    be = _backend_with(monkeypatch, 3)
+    block, V rows in LDS) -- checked against the oracle, with dS recomputed
+    in the dQ pass (the launch checked to have been the 8-wave pass, the
+    last one) and with dS stored (the last launch the dQ = dS K pass)."""
+    be = _backend_with(monkeypatch, 3, ds)
     try:
         _bf16_grad_case(be, oracle, 1, be.cus, M, N, 128, causal, 128)
-        assert be.last_kernel == W8_DKDV.format("_causal" if causal else "")
+        assert be.last_kernel == (DQ_DS if ds else W8_DKDV).format("_causal" if causal else "")
     finally:
         be.close()
 
 
-@pytest.mark.parametrize("causal", [False, True])
-def test_bf16_grad_8wave_matches_4wave(monkeypatch, causal):
-    """The 8-wave dK/dV pass against the 4-wave one (BWPP_ATTN_BWD_W8=0) at a
-    shape with several 256-key blocks per slice, M < N and partial tiles:
-    both add the same 32-query blocks in the same order, so dQ, dK, dV are
-    bit-identical."""
+def _grad_variants(monkeypatch, B, H, M, N, D, causal, variants, seed=5):
+    """dQ, dK, dV of one seeded bf16 problem from a backend per (w8_mask,
+    ds) variant, with the last kernel each launched."""
     torch = _torch()
-    be0 = _backend_with(monkeypatch, 3)
-    cus = be0.cus
-    be0.close()
-    # ceil(1000 / 256) = 4 key blocks per slice: cus / 4 slices fill the chip.
-    B, H, M, N, D = 1, max(1, cus // 4), 600, 1000, 128
-    gen = torch.Generator(device="cuda").manual_seed(5)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
     q = torch.randn(B, H, M, D, device="cuda", generator=gen).bfloat16()
     k = torch.randn(B, H, N, D, device="cuda", generator=gen).bfloat16()
     v = torch.randn(B, H, N, D, device="cuda", generator=gen).bfloat16()
@@ -294,8 +295,8 @@ def test_bf16_grad_8wave_matches_4wave(monkeypatch, causal):
     prm = bwpp.AttentionParams(M=M, N=N, K=D, D=D, ldq=D, ldk=D, ldv=D, ldo=D, batch=B, heads=H,
                                scale=D ** -0.5, causal=int(causal), dtype=int(bwpp.DType.BF16))
     outs = []
-    for mask in (3, 0):
-        be = _backend_with(monkeypatch, mask)
+    for mask, ds in variants:
+        be = _backend_with(monkeypatch, mask, ds)
         try:
             o = torch.empty_like(q)
             lse = torch.empty(B, H, M, device="cuda")
@@ -303,21 +304,64 @@ def test_bf16_grad_8wave_matches_4wave(monkeypatch, causal):
             g = [torch.full_like(t, 7.0) for t in (q, k, v)]
             be.dispatch_attention_grad(q, k, v, o, do, lse, *g, prm)
             torch.cuda.synchronize()
-            w8 = W8_DKDV.format("_causal" if causal else "")
-            assert (be.last_kernel == w8) == (mask == 3), be.last_kernel
-            outs.append(g)
+            outs.append((g, be.last_kernel))
         finally:
             be.close()
-    for a, b in zip(*outs):
-        assert torch.isfinite(a.float()).all()
-        assert torch.equal(a, b)
+    return outs
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_grad_8wave_matches_4wave(monkeypatch, causal):
+    """The 8-wave dK/dV pass against the 4-wave one (BWPP_ATTN_BWD_W8=0) at a
+    shape with several 256-key blocks per slice, M < N and partial tiles,
+    each with dS recomputed and with dS stored: all add the same 32-query
+    blocks in the same order, so dQ, dK, dV are bit-identical."""
+    be0 = _backend_with(monkeypatch, 3)
+    cus = be0.cus
+    be0.close()
+    # ceil(1000 / 256) = 4 key blocks per slice: cus / 4 slices fill the chip.
+    B, H, M, N, D = 1, max(1, cus // 4), 600, 1000, 128
+    outs = _grad_variants(monkeypatch, B, H, M, N, D, causal, [(3, False), (0, False), (3, True), (0, True)])
+    cs = "_causal" if causal else ""
+    assert [kern for _, kern in outs] == [W8_DKDV.format(cs), f"bwpp_attn_bwd_bf16_mfma_d128{cs}_dkdv",
+                                          DQ_DS.format(cs), DQ_DS.format(cs)]
+    ref = outs[0][0]
+    for g, _ in outs[1:]:
+        for a, b in zip(ref, g):
+            assert torch_isfinite_all(a)
+            assert _torch().equal(a, b)
+
+
+def torch_isfinite_all(t):
+    return bool(_torch().isfinite(t.float()).all())
+
+
+@pytest.mark.parametrize("B,H,M,N", [(1, 2, 97, 200), (2, 3, 130, 130), (1, 2, 190, 65), (1, 1, 1, 1),
+                                     (1, 2, 33, 2), (2, 1, 3, 40), (1, 4, 512, 384), (1, 2, 300, 1000)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_grad_stored_ds_matches_recompute(monkeypatch, B, H, M, N, causal):
+    """The stored-dS scheme (dK/dV pass stores dS^T, the dQ pass multiplies
+    it by K) against the two-pass scheme that recomputes S and dP in the dQ
+    pass (BWPP_ATTN_BWD_DS_MB=0), head dim 128: ragged M and N (tiles past
+    both ends, M > N causal with queries that see no key), 4-wave dK/dV
+    blocks.  Both form every dS the same way and feed the MFMAs the same
+    operands in the same order: dQ, dK, dV bit-identical (torch.equal; an
+    all-zero sum may differ in the sign of zero only)."""
+    outs = _grad_variants(monkeypatch, B, H, M, N, 128, causal, [(3, False), (3, True)], seed=11)
+    cs = "_causal" if causal else ""
+    assert outs[1][1] == DQ_DS.format(cs)
+    assert outs[0][1] != DQ_DS.format(cs)
+    for a, b in zip(outs[0][0], outs[1][0]):
+        assert torch_isfinite_all(a)
+        assert _torch().equal(a, b)
 
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_bf16_grad_c4_shape(be, oracle, causal):
     """Config 4's shape, the one the bench times: B8 H32 S2048 d128 bf16,
     scale 1/sqrt(128).  The forward saves lse through the flash kernel and
-    the backward takes the 8-wave dK/dV pass (both checked by kernel name);
+    the backward stores dS and ends with the dQ = dS K pass (both checked
+    by kernel name);
     O and dQ, dK, dV of two (b, h) slices against the oracle on the exact
     bf16 inputs.  Bar 2e-2."""
     torch = _torch()
@@ -334,7 +378,7 @@ def test_bf16_grad_c4_shape(be, oracle, causal):
     assert be.last_kernel == "bwpp_attn_bf16_d128" + cs
     dq, dk, dv = (torch.full_like(t, 7.0) for t in (q, k, v))
     be.dispatch_attention_grad(q, k, v, o, do, lse, dq, dk, dv, prm)
-    assert be.last_kernel == W8_DKDV.format(cs)
+    assert be.last_kernel == DQ_DS.format(cs)
     torch.cuda.synchronize()
     for b, h in ((0, 0), (B - 1, H - 1)):
         qs, ks, vs, dos = (synth.bf16_bits_to_f32(np.ascontiguousarray(x[b:b + 1, h:h + 1])) for x in bits)
