@@ -279,6 +279,149 @@ __device__ __forceinline__ void attn_fwd(const BwppAttnArgs &a) {
 }
 
 // ---------------------------------------------------------------- backward
+// D_m = rowsum(dO * O) of query row qi (greg: the lane's half of dO's row):
+// each lane half sums its D / 2 products in order, then the halves add.
+// The dQ pass and the D_m pass both use it, so both give the same bits.
+template <int D>
+__device__ __forceinline__ float row_dsum(const float (&greg)[D / 2], const float *O, uint32_t ldo, uint32_t qi,
+                                          uint32_t M, int hi) {
+  float orow[D / 2];
+  load_half_row<D>(orow, O, ldo, qi, M, hi);
+  float part = 0.0f;
+#pragma unroll
+  for (int i = 0; i < D / 2; ++i) part += greg[i] * orow[i];
+  return sum32(part);
+}
+
+// D_m pass of the stored-dS scheme: a wave per 32 query rows, q_tiles
+// blocks of kW waves per slice.
+template <int D>
+__device__ __forceinline__ void attn_bwd_dsum(const BwppAttnArgs &a) {
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const int li = lane & 31, hi = lane >> 5;
+  const uint32_t bh = blockIdx.x / a.q_tiles, tile = blockIdx.x % a.q_tiles;
+  const uint32_t b = bh / a.heads, h = bh % a.heads;
+  const float *O = static_cast<const float *>(a.o) + b * a.o_bs + h * a.o_hs;
+  const float *dO = static_cast<const float *>(a.dout) + b * a.o_bs + h * a.o_hs;
+  const uint32_t qi = (tile * kW + (uint32_t)wave) * kR + (uint32_t)li;
+  float greg[D / 2];
+  load_half_row<D>(greg, dO, a.ldo, qi, a.M, hi);
+  const float dsum = row_dsum<D>(greg, O, a.ldo, qi, a.M, hi);
+  if (qi < a.M && hi == 0) a.dsum[(size_t)bh * a.M + qi] = dsum;
+}
+
+// Stored fp32 dS^T (the stored-dS scheme): per slice, 4 KiB blocks of 32
+// keys x 32 queries, [group of 4 query blocks][key block][query block in
+// the group] (query blocks padded to ld_dst / 32, a multiple of 4), so the
+// dQ pass's block reads one contiguous stream.  Inside a block the 16-byte
+// piece holding queries 4 qd .. +3 of key k sits at
+//   1024 (qd / 2) + 32 (k ^ (qd / 2)) + 16 (qd % 2):
+// a wave of the dK / dV pass (lane = key, with quads 2 r4 + hi in its
+// accumulator registers 4 r4 .. +3) writes 1 KiB per store, and the dQ
+// pass's 4-byte reads (lanes = 32 queries of a wave at keys k and k + 4)
+// hit 64 distinct banks (the XOR spreads the four quad pairs, 1 KiB apart,
+// over the eight 32-byte bank groups with the + 4 key).
+struct DsBlk32 {
+  static constexpr uint32_t kBytes = 4096;
+  __device__ __forceinline__ static size_t at(uint32_t bh, uint32_t kb, uint32_t qb, uint32_t n32, uint32_t m32) {
+    return ((((size_t)bh * (m32 / 4u) + qb / 4u) * n32 + kb) * 4u + qb % 4u) * kBytes;
+  }
+  // Byte offset of (key k, query q) inside a block.
+  __device__ __forceinline__ static uint32_t elem(uint32_t k, uint32_t q) {
+    return 1024u * (q >> 3) + 32u * (k ^ (q >> 3)) + 4u * (q & 7u);
+  }
+};
+
+// dQ pass of the stored-dS scheme: dQ = scale dS K with dS^T read from
+// a.dst (written by the dK / dV pass) instead of recomputed from S and dP.
+// A wave owns 32 queries; the block streams K tiles and the matching 16 KiB
+// of dS^T blocks through the two-stage ring.  The same 32 x 32 blocks as in
+// attn_bwd_dq are visited (the dK / dV pass stores exactly those) and
+// every MFMA gets the same operands in the same order, so dQ is
+// bit-identical to attn_bwd_dq's but for the sign of all-zero sums.
+template <int D, bool CAUSAL>
+__device__ __forceinline__ void attn_bwd_dq_ds(const BwppAttnArgs &a) {
+  constexpr int ST = D + 4, SB = kW * (int)DsBlk32::kBytes;  // dS^T bytes per tile
+  constexpr int SPT = SB / 16 / (64 * kW);                      // float4 per thread per dS^T tile
+  constexpr int KPT = kR * (D / 4) / (64 * kW);                 // float4 per thread per K tile
+  __shared__ __attribute__((aligned(16))) float kt[2][kR * ST];
+  __shared__ __attribute__((aligned(16))) unsigned char dst[2][SB];
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const int li = lane & 31, hi = lane >> 5;
+  const uint32_t nbh = gridDim.x / a.q_tiles;
+  const uint32_t qt = a.q_tiles - 1 - tile_rank(a, nbh);
+  const Slice sl = slice_of(a, nbh);
+  const float *K = static_cast<const float *>(a.k) + sl.b * a.k_bs + sl.h * a.k_hs;
+  float *dQ = static_cast<float *>(a.dq) + sl.b * a.q_bs + sl.h * a.q_hs;
+  const int64_t diag = (int64_t)a.N - (int64_t)a.M;
+  const uint32_t qb = qt * (kW * kR), q0 = qb + (uint32_t)wave * kR, qi = q0 + (uint32_t)li;
+  const uint32_t n32 = (a.N + 31u) / 32u, m32 = a.ld_dst / 32u;
+  const unsigned char *S = static_cast<const unsigned char *>(a.dst) + DsBlk32::at(sl.bh, 0, qb / 32u, n32, m32);
+
+  uint32_t kend = a.N;
+  if (CAUSAL) {
+    const int64_t last = (int64_t)min(a.M, qb + kW * kR) - 1 + diag;
+    kend = last < 0 ? 0u : (uint32_t)min<int64_t>(last + 1, (int64_t)a.N);
+  }
+  const uint32_t nt = (kend + kR - 1) / kR;
+  const int64_t wlast = (int64_t)q0 + kR - 1 + diag;
+  // This lane's dS^T element offsets (query li, key acc_row(j, hi)).
+  uint32_t eoff[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) eoff[j] = (uint32_t)wave * DsBlk32::kBytes + DsBlk32::elem((uint32_t)acc_row(j, hi), (uint32_t)li);
+
+  f32x16 dq[D / 32];
+#pragma unroll
+  for (int blk = 0; blk < D / 32; ++blk) dq[blk] = f32x16{};
+
+  f32x4 kx[KPT], sx[SPT];
+  auto fetch = [&](uint32_t t) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int idx = (int)threadIdx.x + i * 64 * kW, r = idx / (D / 4), c = idx % (D / 4);
+      const uint32_t row = t * kR + (uint32_t)r;
+      kx[i] = row < a.N ? *reinterpret_cast<const f32x4 *>(K + (size_t)row * a.ldk + 4 * c)
+                        : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(S + (size_t)t * SB);
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) sx[i] = src[(int)threadIdx.x + i * 64 * kW];
+  };
+  auto stash = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int idx = (int)threadIdx.x + i * 64 * kW, r = idx / (D / 4), c = idx % (D / 4);
+      *reinterpret_cast<f32x4 *>(&kt[st][r * ST + 4 * c]) = kx[i];
+    }
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) reinterpret_cast<f32x4 *>(dst[st])[(int)threadIdx.x + i * 64 * kW] = sx[i];
+  };
+  if (nt > 0) {
+    fetch(0);
+    stash(0);
+  }
+  __syncthreads();
+  for (uint32_t t = 0; t < nt; ++t) {
+    const int st = (int)(t & 1);
+    const uint32_t k0 = t * kR;
+    if (t + 1 < nt) fetch(t + 1);
+    if (!CAUSAL || (int64_t)k0 <= wlast) {
+      f32x16 w;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) w[j] = *reinterpret_cast<const float *>(dst[st] + eoff[j]);
+      if (k0 + kR > a.N) {  // keys past N: dS = 0 (their K rows are zero)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (k0 + (uint32_t)acc_row(j, hi) >= a.N) w[j] = 0.0f;
+      }
+      acc_tile_t<D>(dq, kt[st], w, li, hi);  // dQ^T += K^T dS^T
+    }
+    if (t + 1 < nt) stash(st ^ 1);
+    __syncthreads();
+  }
+  if (qi < a.M) store_t<D>(dQ, a.ldq, qi, dq, a.scale, hi);
+}
+
 // dQ pass: a wave owns 32 queries and streams K / V tiles; it also writes
 // D_m = rowsum(dO * O) for the dK / dV pass.
 template <int D, bool CAUSAL>
@@ -311,15 +454,7 @@ __device__ __forceinline__ void attn_bwd_dq(const BwppAttnArgs &a) {
   float qreg[D / 2], greg[D / 2];
   load_half_row<D>(qreg, Q, a.ldq, qi, a.M, hi);
   load_half_row<D>(greg, dO, a.ldo, qi, a.M, hi);
-  float dsum;
-  {
-    float orow[D / 2];
-    load_half_row<D>(orow, O, a.ldo, qi, a.M, hi);
-    float part = 0.0f;
-#pragma unroll
-    for (int i = 0; i < D / 2; ++i) part += greg[i] * orow[i];
-    dsum = sum32(part);
-  }
+  const float dsum = row_dsum<D>(greg, O, a.ldo, qi, a.M, hi);
   if (qi < a.M && hi == 0) a.dsum[(size_t)sl.bh * a.M + qi] = dsum;
   // Queries past M: +inf makes every probability exp2(-inf) = 0.
   const float lse2 = qi < a.M ? a.lse[(size_t)sl.bh * a.M + qi] * kLog2e : INFINITY;
@@ -364,8 +499,8 @@ __device__ __forceinline__ void attn_bwd_dq(const BwppAttnArgs &a) {
 }
 
 // dK / dV pass: a wave owns 32 keys and streams Q / dO tiles with their
-// lse and D_m.
-template <int D, bool CAUSAL>
+// lse and D_m.  WS: also stores dS^T to a.dst for attn_bwd_dq_ds.
+template <int D, bool CAUSAL, bool WS = false>
 __device__ __forceinline__ void attn_bwd_dkdv(const BwppAttnArgs &a) {
   using Tiles = TilePair<D>;
   constexpr int ST = Tiles::ST;
@@ -467,6 +602,19 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwppAttnArgs &a) {
           }
         }
       }
+      if constexpr (WS) {
+        // Registers 4 r4 .. +3: queries of quad 2 r4 + hi (1 KiB per store;
+        // a wave past N has no block).
+        if (k0w < a.N) {
+          unsigned char *blk = static_cast<unsigned char *>(a.dst) +
+                               DsBlk32::at(sl.bh, k0w / 32u, m0 / 32u, (a.N + 31u) / 32u, a.ld_dst / 32u);
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4)
+            __builtin_nontemporal_store(f32x4{ds[4 * r4], ds[4 * r4 + 1], ds[4 * r4 + 2], ds[4 * r4 + 3]},
+                                        reinterpret_cast<f32x4 *>(blk + 1024u * r4 + 32u * ((uint32_t)li ^ r4) +
+                                                                  16u * (uint32_t)hi));
+        }
+      }
       acc_tile_t<D>(dv, lds[st][1], s, li, hi);   // dV^T += dO^T P
       acc_tile_t<D>(dk, lds[st][0], ds, li, hi);  // dK^T += Q^T dS
     }
@@ -501,6 +649,28 @@ BWPP_ATTN_F32(64, false, )
 BWPP_ATTN_F32(64, true, _causal)
 BWPP_ATTN_F32(128, false, )
 BWPP_ATTN_F32(128, true, _causal)
+
+// The stored-dS scheme: D_m pass, dK / dV pass that also stores dS^T, and
+// the dQ = dS K pass.
+#define BWPP_ATTN_F32_DS(D, CAUSAL, SUFFIX)                                                                 \
+  extern "C" __global__ __launch_bounds__(64 * kW) void bwpp_attn_bwd_f32_mfma_d##D##SUFFIX##_dkdv_ds(      \
+      const BwppAttnArgs a) {                                                                               \
+    attn_bwd_dkdv<D, CAUSAL, true>(a);                                                                      \
+  }                                                                                                         \
+  extern "C" __global__ __launch_bounds__(64 * kW) void bwpp_attn_bwd_f32_mfma_d##D##SUFFIX##_dq_ds(        \
+      const BwppAttnArgs a) {                                                                               \
+    attn_bwd_dq_ds<D, CAUSAL>(a);                                                                           \
+  }
+BWPP_ATTN_F32_DS(64, false, )
+BWPP_ATTN_F32_DS(64, true, _causal)
+BWPP_ATTN_F32_DS(128, false, )
+BWPP_ATTN_F32_DS(128, true, _causal)
+extern "C" __global__ __launch_bounds__(64 * kW) void bwpp_attn_bwd_f32_d64_dsum(const BwppAttnArgs a) {
+  attn_bwd_dsum<64>(a);
+}
+extern "C" __global__ __launch_bounds__(64 * kW) void bwpp_attn_bwd_f32_d128_dsum(const BwppAttnArgs a) {
+  attn_bwd_dsum<128>(a);
+}
 
 // bf16 <-> fp32 operand copies for running bf16 attention backward on the
 // fp32 kernels above: element (slice, r, c) of the strided bf16 tensor <->

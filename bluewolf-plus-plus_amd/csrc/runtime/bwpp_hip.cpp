@@ -98,6 +98,8 @@ struct BwppHip {
   // dS^T, dQ = dS K pass): [causal]
   hipFunction_t attn_bf16_dsum = nullptr, attn_bf16_dkdv_ds[2] = {}, attn_bf16_dkdv_w8_ds[2] = {},
                 attn_bf16_dq_ds[2] = {};
+  // The same for the fp32 matrix-core passes: [d128]; [d128][causal]
+  hipFunction_t attn_f32_dsum[2] = {}, attn_f32_dkdv_ds[2][2] = {}, attn_f32_dq_ds[2][2] = {};
   uint64_t attn_ds_max = 8ull << 30;  // BWPP_ATTN_BWD_DS_MB: largest dS^T workspace in bytes (0: scheme off)
   hipFunction_t attn_conv_to_f32 = nullptr, attn_conv_to_bf16 = nullptr;  // bf16 <-> fp32 operand copies
   hipFunction_t rmsnorm_grad_w[4] = {};  // wave-per-row rmsnorm_grad, 256 / 512 / 1024 / 2048 columns
@@ -210,6 +212,16 @@ BwppHipStatus resolve_all(BwppHip *h) {
       {"bwpp_attn_bwd_bf16_mfma_d128_dkdv_w8", &h->attn_bf16_dkdv_w8[0]},
       {"bwpp_attn_bwd_bf16_mfma_d128_causal_dkdv_w8", &h->attn_bf16_dkdv_w8[1]},
       {"bwpp_attn_bwd_bf16_d128_dsum", &h->attn_bf16_dsum},
+      {"bwpp_attn_bwd_f32_d64_dsum", &h->attn_f32_dsum[0]},
+      {"bwpp_attn_bwd_f32_d128_dsum", &h->attn_f32_dsum[1]},
+      {"bwpp_attn_bwd_f32_mfma_d64_dkdv_ds", &h->attn_f32_dkdv_ds[0][0]},
+      {"bwpp_attn_bwd_f32_mfma_d64_causal_dkdv_ds", &h->attn_f32_dkdv_ds[0][1]},
+      {"bwpp_attn_bwd_f32_mfma_d128_dkdv_ds", &h->attn_f32_dkdv_ds[1][0]},
+      {"bwpp_attn_bwd_f32_mfma_d128_causal_dkdv_ds", &h->attn_f32_dkdv_ds[1][1]},
+      {"bwpp_attn_bwd_f32_mfma_d64_dq_ds", &h->attn_f32_dq_ds[0][0]},
+      {"bwpp_attn_bwd_f32_mfma_d64_causal_dq_ds", &h->attn_f32_dq_ds[0][1]},
+      {"bwpp_attn_bwd_f32_mfma_d128_dq_ds", &h->attn_f32_dq_ds[1][0]},
+      {"bwpp_attn_bwd_f32_mfma_d128_causal_dq_ds", &h->attn_f32_dq_ds[1][1]},
       {"bwpp_attn_bwd_bf16_mfma_d128_dkdv_ds", &h->attn_bf16_dkdv_ds[0]},
       {"bwpp_attn_bwd_bf16_mfma_d128_causal_dkdv_ds", &h->attn_bf16_dkdv_ds[1]},
       {"bwpp_attn_bwd_bf16_mfma_d128_dkdv_w8_ds", &h->attn_bf16_dkdv_w8_ds[0]},
@@ -1157,17 +1169,19 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   const int bf = p.dtype == BWPP_HIP_BF16 ? 1 : 0, causal = p.causal ? 1 : 0;
   const float scale = p.scale != 0.0f ? p.scale : 1.0f;
   const int bf16v = attn_bf16_bwd_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
-  // Stored-dS scheme (bf16, d = 128, not the allocation-free entry): the
-  // dK / dV pass also stores dS^T (bf16 in 2 KiB blocks of 32 keys x 32
-  // queries, keys padded to 32, queries to whole 128-query blocks: ld_dst)
-  // and the dQ pass only multiplies it by K, so S and dP are computed once
-  // instead of in both passes.  It needs 2 * B*H * ceil32(N) * ld_dst bytes
-  // of workspace, up to attn_ds_max.
+  const int f32v = attn_f32_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
+  // Stored-dS scheme (bf16 with d = 128, or the fp32 passes; not the
+  // allocation-free entry): the dK / dV pass also stores dS^T (bf16 in
+  // 2 KiB / fp32 in 4 KiB blocks of 32 keys x 32 queries, keys padded to 32,
+  // queries to whole 128-query blocks: ld_dst) and the dQ pass only
+  // multiplies it by K, so S and dP are computed once instead of in both
+  // passes.  It needs es * B*H * ceil32(N) * ld_dst bytes of workspace, up
+  // to attn_ds_max.
   const uint64_t ld_dst = ((uint64_t)p.M + 127ull) / 128ull * 128ull;
   const uint64_t ds_off = ((uint64_t)dsum_bytes + 255ull) & ~255ull;
-  const uint64_t ds_bytes = slices * (((uint64_t)p.N + 31ull) / 32ull * 32ull) * ld_dst * 2ull;
-  const bool use_ds = !dsum_buf && bf16v == 1 && p.M > 0 && p.N > 0 && ds_bytes <= h->attn_ds_max &&
-                      ld_dst <= 0xffffffffull;
+  const uint64_t ds_bytes = slices * (((uint64_t)p.N + 31ull) / 32ull * 32ull) * ld_dst * (f32v >= 0 ? 4ull : 2ull);
+  const bool use_ds = !dsum_buf && (bf16v == 1 || f32v >= 0) && p.M > 0 && p.N > 0 &&
+                      ds_bytes <= h->attn_ds_max && ld_dst <= 0xffffffffull;
   if (dsum_buf) {
     if (dsum_bytes > dsum_cap)
       return fail(h, BWPP_HIP_ERR_UNSUPPORTED,
@@ -1203,7 +1217,28 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
     if (p.N > 0) return launch(h, fdkdv, (uint32_t)grid, 1, 1, 64 * wk, f);
     return BWPP_HIP_OK;
   };
-  const int f32v = attn_f32_variant(p, g, scale, {q, k, v, o, dout, dq, dk, dv});
+  if (use_ds && f32v >= 0) {
+    BwppAttnArgs f = g;
+    f.scale = scale;
+    f.scale_log2 = scale * 1.4426950408889634f;
+    f.dst = static_cast<unsigned char *>(h->ws) + ds_off;
+    f.ld_dst = (uint32_t)ld_dst;
+    f.q_tiles = (p.M + 32 * kAttnWaves - 1) / (32 * kAttnWaves);
+    const uint64_t grid = slices * f.q_tiles;
+    f.q_tiles = (p.N + 32 * kAttnWaves - 1) / (32 * kAttnWaves);  // key tiles
+    const uint64_t kgrid = slices * f.q_tiles;
+    if (grid > 0x7fffffffull || kgrid > 0x7fffffffull)
+      return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "attention_grad: grid too large");
+    f.q_tiles = (p.M + 32 * kAttnWaves - 1) / (32 * kAttnWaves);
+    if ((s = launch(h, h->attn_f32_dsum[f32v], (uint32_t)grid, 1, 1, 64 * kAttnWaves, f)) != BWPP_HIP_OK) return s;
+    BwppAttnArgs fk = f;
+    fk.q_tiles = (p.N + 32 * kAttnWaves - 1) / (32 * kAttnWaves);
+    fk.zigzag = attn_zigzag(h, causal != 0, kgrid);
+    if ((s = launch(h, h->attn_f32_dkdv_ds[f32v][causal], (uint32_t)kgrid, 1, 1, 64 * kAttnWaves, fk)) != BWPP_HIP_OK)
+      return s;
+    f.zigzag = attn_zigzag(h, causal != 0, grid);
+    return launch(h, h->attn_f32_dq_ds[f32v][causal], (uint32_t)grid, 1, 1, 64 * kAttnWaves, f);
+  }
   if (f32v >= 0)
     return run_mfma(g, h->attn_f32_dq[f32v][causal], h->attn_f32_dkdv[f32v][causal]);
   if (use_ds) {

@@ -122,6 +122,46 @@ def test_mfma_f32_causal_zigzag_order(be, oracle, monkeypatch, D):
     assert rel_max_err(dv[s1], wv) <= TOL
 
 
+@pytest.mark.parametrize("B,H,M,N,D", [(1, 1, 1, 1, 64), (1, 1, 31, 33, 64), (2, 3, 64, 64, 64), (1, 2, 97, 200, 64),
+                                       (1, 1, 200, 97, 64), (1, 1, 130, 130, 128), (2, 1, 65, 190, 128),
+                                       (1, 1, 190, 65, 128), (1, 4, 512, 512, 64)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_mfma_f32_grad_stored_ds_matches_recompute(monkeypatch, B, H, M, N, D, causal):
+    """The stored-dS scheme of the fp32 passes (the dK/dV pass stores dS^T,
+    the dQ pass multiplies it by K; the default) against the scheme that
+    recomputes S and dP in the dQ pass (BWPP_ATTN_BWD_DS_MB=0): both form
+    every dS the same way and feed the MFMAs the same operands in the same
+    order, so dQ, dK, dV are equal (an all-zero sum may differ in the sign
+    of zero only).  Ragged tiles on both sides, M > N causal (queries that
+    see no key), both head dims; the last launch is checked to be the
+    dQ = dS K pass."""
+    torch = _torch()
+    seed = 31 * B + M + 3 * N + D
+    q, k, v, dout = (synth.normal(sh, seed, i) for i, sh in
+                     enumerate([(B, H, M, D), (B, H, N, D), (B, H, N, D), (B, H, M, D)]))
+    scale = 1.0 / np.sqrt(D)
+    prm = bwpp.AttentionParams(M=M, N=N, K=D, D=D, ldq=D, ldk=D, ldv=D, ldo=D, batch=B, heads=H,
+                               scale=scale, causal=int(causal), dtype=int(bwpp.DType.F32))
+    cs = "_causal" if causal else ""
+    outs = []
+    for ds in (False, True):
+        if ds:
+            monkeypatch.delenv("BWPP_ATTN_BWD_DS_MB", raising=False)
+        else:
+            monkeypatch.setenv("BWPP_ATTN_BWD_DS_MB", "0")
+        b2 = bwpp.HipBackend(0)
+        try:
+            b2.set_stream(torch.cuda.current_stream())
+            outs.append(_run_all(b2, q, k, v, dout, scale, causal, prm))
+            want = f"bwpp_attn_bwd_f32_mfma_d{D}{cs}_" + ("dq_ds" if ds else "dkdv")
+            assert b2.last_kernel == want, b2.last_kernel
+        finally:
+            b2.close()
+    for a, b in zip(outs[0][3:], outs[1][3:]):
+        assert np.all(np.isfinite(a))
+        assert np.array_equal(a, b)
+
+
 @pytest.mark.parametrize("scale", [-0.3, 2.0])
 def test_mfma_f32_scales(be, oracle, scale):
     B, H, M, N, D = 1, 2, 100, 140, 64
