@@ -387,8 +387,12 @@ BwppHipStatus bwpp_hip_dispatch_attention_lse(BwppHip *h, const void *q,
  * for the upstream gradient dout, from q, k, v, o and the forward's lse.
  * dout / dq / dk / dv use the strides of o / q / k / v.  Outputs must not
  * overlap inputs or each other.  Uses the handle's workspace for
- * rowsum(dout * o).  Replaces the decomposed path of graph_ir.c:1722-1733
- * (softmax_grad over materialised probabilities). */
+ * rowsum(dout * o) and, for bf16 with K = D = 128 and for the fp32
+ * matrix-core shapes, for dS (2 or 4 bytes x batch * heads *
+ * ceil(N / 32) * 32 * ceil(M / 128) * 128, up to BWPP_ATTN_BWD_DS_MB MiB,
+ * default 8192; beyond that, or with 0, S and dP are recomputed instead,
+ * with the same results).  Replaces the decomposed path of
+ * graph_ir.c:1722-1733 (softmax_grad over materialised probabilities). */
 BwppHipStatus bwpp_hip_dispatch_attention_grad(BwppHip *h, const void *q,
                                                const void *k, const void *v,
                                                const void *o, const void *dout,
@@ -407,7 +411,9 @@ BwppHipStatus bwpp_hip_dispatch_attention_grad(BwppHip *h, const void *q,
  * are UNSUPPORTED too.  Every call on one GPU shares that GPU's scratch:
  * calls that overlap on one GPU (several streams, handles or threads) race
  * on it; calls ordered on one stream do not.  Results are bit-identical to
- * bwpp_hip_dispatch_attention_grad's. */
+ * bwpp_hip_dispatch_attention_grad's (but for the sign of a zero that is
+ * an all-zero sum: this entry recomputes S and dP in the dQ pass rather
+ * than storing dS). */
 BwppHipStatus bwpp_hip_dispatch_attention_grad_noalloc(
     BwppHip *h, const void *q, const void *k, const void *v, const void *o,
     const void *dout, const float *lse, void *dq, void *dk, void *dv,
