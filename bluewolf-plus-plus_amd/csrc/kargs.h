@@ -85,9 +85,10 @@ typedef struct {
   float scale; /* the plain score scale (fp32 MFMA path, which gets scale * log2(e) in scale_log2) */
   uint32_t zigzag; /* fp32 MFMA causal kernels: tile order heavy ranks first, then the light ones
                       lightest first (a one-wave grid then pairs heavy with light on each CU) */
-  /* bf16 backward with a stored dS: dS^T per slice as [N][ld_dst] bf16
-   * (written by the dK/dV pass, read by the dQ pass), slice stride
-   * N * ld_dst elements. */
+  /* Backward with a stored dS: dS^T written by the dK/dV pass and read by
+   * the dQ pass, in blocks of 32 keys x 32 queries (bf16: DsBlk in
+   * attention_bwd.hip, fp32: DsBlk32 in attention_f32.hip); ld_dst = the
+   * query count rounded up to 128. */
   void *dst;
   uint32_t ld_dst;
 } BwppAttnArgs;
