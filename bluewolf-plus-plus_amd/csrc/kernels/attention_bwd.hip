@@ -428,10 +428,12 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
 }
 
 // Stored dS^T layout: per slice, 2 KiB blocks of 32 keys x 32 queries,
-// [group of 4 query blocks][key block][query block in the group] (query
-// blocks padded to ld_dst / 32, a multiple of 4): the dQ pass's block (one
-// group) then reads one contiguous stream.  Inside a block the 8-byte
-// piece holding queries 4 qd .. +3 of key k sits at
+// [key block][query block] (query blocks padded to ld_dst / 32, a multiple
+// of 4): the dQ pass's blocks of one slice, which step through the key
+// blocks together, read neighbouring 8 KiB pieces of one key block's row
+// (4-7 % faster than giving each block a contiguous stream of its own).
+// Inside a block the 8-byte piece holding queries 4 qd .. +3 of key k sits
+// at
 //   512 (qd / 2) + 16 (k ^ 4 (qd / 2)) + 8 (qd % 2),
 // so a wave of the dK / dV pass (lane = key, holding quads 2 x + hi of one
 // quad pair x per store) writes 512 contiguous bytes per store, the dQ
@@ -443,7 +445,7 @@ struct DsBlk {
   // Byte offset of block (key block kb, query block qb) of slice bh; n32
   // key blocks, m32 query blocks per slice.
   __device__ __forceinline__ static size_t at(uint32_t bh, uint32_t kb, uint32_t qb, uint32_t n32, uint32_t m32) {
-    return ((((size_t)bh * (m32 / 4u) + qb / 4u) * n32 + kb) * 4u + qb % 4u) * kBytes;
+    return (((size_t)bh * n32 + kb) * m32 + qb) * kBytes;
   }
   // Offset of key k's piece of quad hi (quad pair 0).
   __device__ __forceinline__ static uint32_t piece(uint32_t k, uint32_t hi) { return 16u * k + 8u * hi; }
@@ -477,7 +479,7 @@ __device__ __forceinline__ void bwd_dq_ds(const BwppAttnArgs &a) {
   const uint32_t qb = qt * (kW * kR), q0 = qb + (uint32_t)wave * kR, qi = q0 + (uint32_t)li;
   const uint32_t n32 = (a.N + 31u) / 32u, m32 = a.ld_dst / 32u;
   const uint16_t *K = static_cast<const uint16_t *>(a.k) + sl.b * a.k_bs + sl.h * a.k_hs;
-  // The block's query group: 8 KiB (its 4 query blocks) per key block.
+  // The block's 4 query blocks (8 KiB, contiguous) of key block 0.
   const unsigned char *S = static_cast<const unsigned char *>(a.dst) + DsBlk::at(sl.bh, 0, qb / 32u, n32, m32);
   uint16_t *dQ = static_cast<uint16_t *>(a.dq) + sl.b * a.q_bs + sl.h * a.q_hs;
   const int64_t diag = (int64_t)a.N - (int64_t)a.M;
@@ -514,7 +516,7 @@ __device__ __forceinline__ void bwd_dq_ds(const BwppAttnArgs &a) {
     for (int i = 0; i < SPW; ++i) {
       const uint32_t j = wv * (uint32_t)SPW + (uint32_t)i;  // 1 KiB piece of the tile
       const uint32_t kb = min(t * (uint32_t)KB + j / 8u, n32 - 1u);  // past N: re-read the last block (masked)
-      g2lds16(S + (size_t)kb * (4u * DsBlk::kBytes) + (j % 8u) * 1024u + 16u * (uint32_t)lane,
+      g2lds16(S + (size_t)kb * m32 * DsBlk::kBytes + (j % 8u) * 1024u + 16u * (uint32_t)lane,
               sb + (uint32_t)TB + j * 1024u);
     }
   };

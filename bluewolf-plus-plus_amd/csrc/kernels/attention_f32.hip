@@ -311,10 +311,10 @@ __device__ __forceinline__ void attn_bwd_dsum(const BwppAttnArgs &a) {
 }
 
 // Stored fp32 dS^T (the stored-dS scheme): per slice, 4 KiB blocks of 32
-// keys x 32 queries, [group of 4 query blocks][key block][query block in
-// the group] (query blocks padded to ld_dst / 32, a multiple of 4), so the
-// dQ pass's block reads one contiguous stream.  Inside a block the 16-byte
-// piece holding queries 4 qd .. +3 of key k sits at
+// keys x 32 queries, [key block][query block] (query blocks padded to
+// ld_dst / 32, a multiple of 4; the order of the bf16 blocks in
+// attention_bwd.hip).  Inside a block the 16-byte piece holding queries
+// 4 qd .. +3 of key k sits at
 //   1024 (qd / 2) + 32 (k ^ (qd / 2)) + 16 (qd % 2):
 // a wave of the dK / dV pass (lane = key, with quads 2 r4 + hi in its
 // accumulator registers 4 r4 .. +3) writes 1 KiB per store, and the dQ
@@ -324,7 +324,7 @@ __device__ __forceinline__ void attn_bwd_dsum(const BwppAttnArgs &a) {
 struct DsBlk32 {
   static constexpr uint32_t kBytes = 4096;
   __device__ __forceinline__ static size_t at(uint32_t bh, uint32_t kb, uint32_t qb, uint32_t n32, uint32_t m32) {
-    return ((((size_t)bh * (m32 / 4u) + qb / 4u) * n32 + kb) * 4u + qb % 4u) * kBytes;
+    return (((size_t)bh * n32 + kb) * m32 + qb) * kBytes;
   }
   // Byte offset of (key k, query q) inside a block.
   __device__ __forceinline__ static uint32_t elem(uint32_t k, uint32_t q) {
@@ -335,7 +335,8 @@ struct DsBlk32 {
 // dQ pass of the stored-dS scheme: dQ = scale dS K with dS^T read from
 // a.dst (written by the dK / dV pass) instead of recomputed from S and dP.
 // A wave owns 32 queries; the block streams K tiles and the matching 16 KiB
-// of dS^T blocks through the two-stage ring.  The same 32 x 32 blocks as in
+// of dS^T blocks (its 4 query blocks of a key block) through the two-stage
+// ring.  The same 32 x 32 blocks as in
 // attn_bwd_dq are visited (the dK / dV pass stores exactly those) and
 // every MFMA gets the same operands in the same order, so dQ is
 // bit-identical to attn_bwd_dq's but for the sign of all-zero sums.
@@ -383,7 +384,7 @@ __device__ __forceinline__ void attn_bwd_dq_ds(const BwppAttnArgs &a) {
       kx[i] = row < a.N ? *reinterpret_cast<const f32x4 *>(K + (size_t)row * a.ldk + 4 * c)
                         : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    const f32x4 *src = reinterpret_cast<const f32x4 *>(S + (size_t)t * SB);
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(S + (size_t)t * m32 * DsBlk32::kBytes);
 #pragma unroll
     for (int i = 0; i < SPT; ++i) sx[i] = src[(int)threadIdx.x + i * 64 * kW];
   };
