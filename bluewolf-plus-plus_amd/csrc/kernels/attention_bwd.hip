@@ -610,34 +610,6 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
     m32 = a.ld_dst / 32u;
     dso = DsBlk::piece(li, hi);
   }
-  // A tile's dS^T pieces are stored at the start of the next tile (or after
-  // the loop): the wait for the next tile's DMA at the end of a tile also
-  // waits for every store issued before it, and a tile later the stores
-  // have drained.  pend_q: query block of each pending sub-block, or ~0.
-  constexpr int NSB = TR / kR;
-  uint4 pend[WS ? NSB : 1][2];
-  uint32_t pend_q[WS ? NSB : 1];
-#pragma unroll
-  for (int i = 0; i < (WS ? NSB : 1); ++i) pend_q[i] = ~0u;
-  auto flush = [&]() {
-    if constexpr (WS) {
-#pragma unroll
-      for (int i = 0; i < NSB; ++i)
-        if (pend_q[i] != ~0u) {
-          unsigned char *blk = dsblk + DsBlk::at(sl.bh, k0w / 32u, pend_q[i], n32, m32);
-#pragma unroll
-          for (int kq = 0; kq < 2; ++kq) {
-            // Streaming stores (nt): read once, by the dQ pass, and kept out
-            // of the way of the Q / dO tiles in L2 (the dQ pass 4 % faster).
-            __builtin_nontemporal_store(u32x2_t{pend[i][kq].x, pend[i][kq].y},
-                                        reinterpret_cast<u32x2_t *>(blk + DsBlk::pair(dso, 2 * kq)));
-            __builtin_nontemporal_store(u32x2_t{pend[i][kq].z, pend[i][kq].w},
-                                        reinterpret_cast<u32x2_t *>(blk + DsBlk::pair(dso, 2 * kq + 1)));
-          }
-          pend_q[i] = ~0u;
-        }
-    }
-  };
   bf16x8_t kf[D / 16], vf[D / 16];
   load_row<D>(kf, K, a.ldk, ni, a.N, hi);
   load_row<D>(vf, V, a.ldv, ni, a.N, hi);
@@ -685,7 +657,6 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
   __syncthreads();
   for (uint32_t t = 0; t < nt; ++t) {
     const int st = (int)(t & 1);
-    flush();
     if (t + 1 < nt) {
       issue(t + 1);
       fetch_rows(mbeg + (t + 1) * TR);
@@ -742,9 +713,18 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
           if constexpr (WS) {
             // Elements 0-3 / 4-7 of wd: query quads 4 kq + hi / 4 kq + 2 + hi
             // of key ni, i.e. quad pairs x = 2 kq / 2 kq + 1: two 512-byte
-            // stores per wave.  A wave past N has no block to write.
-            pend[sb][kq] = __builtin_bit_cast(uint4, wd);
-            if (kq == 1 && k0w < a.N) pend_q[sb] = m0 / 32u;
+            // stores per wave (streaming: read once, by the dQ pass, and
+            // kept out of the way of the Q / dO tiles in L2; the dQ pass
+            // 4 % faster).  A wave past N has no block to write.  (Holding
+            // them to the start of the next tile, out of the wait for that
+            // tile's DMA, changed nothing.)
+            if (k0w < a.N) {
+              const uint4 u = __builtin_bit_cast(uint4, wd);
+              unsigned char *blk = dsblk + DsBlk::at(sl.bh, k0w / 32u, m0 / 32u, n32, m32);
+              __builtin_nontemporal_store(u32x2_t{u.x, u.y}, reinterpret_cast<u32x2_t *>(blk + DsBlk::pair(dso, 2 * kq)));
+              __builtin_nontemporal_store(u32x2_t{u.z, u.w},
+                                          reinterpret_cast<u32x2_t *>(blk + DsBlk::pair(dso, 2 * kq + 1)));
+            }
           }
 #pragma unroll
           for (int blk = 0; blk < DB; ++blk) {
@@ -758,7 +738,6 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
     wait_vmcnt<0>();
     __syncthreads();
   }
-  flush();
   if (ni < a.N) {
     store_t<D>(dK, a.ldk, ni, dk, a.scale, hi);
     store_t<D>(dV, a.ldv, ni, dv, 1.0f, hi);
