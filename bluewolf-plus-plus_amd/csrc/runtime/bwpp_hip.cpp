@@ -1180,15 +1180,22 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   const uint64_t ld_dst = ((uint64_t)p.M + 127ull) / 128ull * 128ull;
   const uint64_t ds_off = ((uint64_t)dsum_bytes + 255ull) & ~255ull;
   const uint64_t ds_bytes = slices * (((uint64_t)p.N + 31ull) / 32ull * 32ull) * ld_dst * (f32v >= 0 ? 4ull : 2ull);
-  const bool use_ds = !dsum_buf && (bf16v == 1 || f32v >= 0) && p.M > 0 && p.N > 0 &&
-                      ds_bytes <= h->attn_ds_max && ld_dst <= 0xffffffffull;
+  bool use_ds = !dsum_buf && (bf16v == 1 || f32v >= 0) && p.M > 0 && p.N > 0 && ds_bytes <= h->attn_ds_max &&
+                ld_dst <= 0xffffffffull;
   if (dsum_buf) {
     if (dsum_bytes > dsum_cap)
       return fail(h, BWPP_HIP_ERR_UNSUPPORTED,
                   "attention_grad_noalloc: batch*heads*M = %llu query rows need %zu bytes of scratch, above the "
                   "%zu-byte maximum", (unsigned long long)(slices * p.M), dsum_bytes, dsum_cap);
-  } else if ((s = ensure_ws(h, use_ds ? (size_t)(ds_off + ds_bytes) : dsum_bytes)) != BWPP_HIP_OK) {
-    return s;
+  } else {
+    // A stored-dS workspace the device cannot give: recompute S and dP
+    // instead (the same results), with only the row sums in the workspace.
+    if (use_ds && (s = ensure_ws(h, (size_t)(ds_off + ds_bytes))) != BWPP_HIP_OK) {
+      if (s != BWPP_HIP_ERR_OUT_OF_MEMORY) return s;
+      use_ds = false;
+      h->err.clear();
+    }
+    if (!use_ds && (s = ensure_ws(h, dsum_bytes)) != BWPP_HIP_OK) return s;
   }
   g.scale_log2 = scale;
   g.lse = const_cast<float *>(lse);

@@ -390,8 +390,8 @@ BwppHipStatus bwpp_hip_dispatch_attention_lse(BwppHip *h, const void *q,
  * rowsum(dout * o) and, for bf16 with K = D = 128 and for the fp32
  * matrix-core shapes, for dS (2 or 4 bytes x batch * heads *
  * ceil(N / 32) * 32 * ceil(M / 128) * 128, up to BWPP_ATTN_BWD_DS_MB MiB,
- * default 8192; beyond that, or with 0, S and dP are recomputed instead,
- * with the same results).  Replaces the decomposed path of
+ * default 8192; beyond that, with 0, or when the device cannot allocate
+ * it, S and dP are recomputed instead, with the same results).  Replaces the decomposed path of
  * graph_ir.c:1722-1733 (softmax_grad over materialised probabilities). */
 BwppHipStatus bwpp_hip_dispatch_attention_grad(BwppHip *h, const void *q,
                                                const void *k, const void *v,

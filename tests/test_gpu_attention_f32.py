@@ -396,6 +396,40 @@ def test_bf16_grad_stored_ds_matches_recompute(monkeypatch, B, H, M, N, causal):
         assert _torch().equal(a, b)
 
 
+def test_bf16_grad_stored_ds_falls_back_when_device_memory_is_short(monkeypatch):
+    """One slice of 400,000 queries and keys (d = 128): its stored dS would
+    take ~320 GB, more than the device holds.  With the cap raised above
+    that, the workspace allocation fails and the call recomputes S and dP
+    instead of returning OUT_OF_MEMORY: the launches are the recompute
+    scheme's and the results equal those with the scheme turned off."""
+    torch = _torch()
+    monkeypatch.setenv("BWPP_ATTN_BWD_DS_MB", str(1 << 30))
+    B, H, S, D = 1, 1, 400_000, 128
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    q, k, v, do = (torch.randn(B, H, S, D, device="cuda", generator=gen).bfloat16() for _ in range(4))
+    prm = bwpp.AttentionParams(M=S, N=S, K=D, D=D, ldq=D, ldk=D, ldv=D, ldo=D, batch=B, heads=H,
+                               scale=D ** -0.5, causal=1, dtype=int(bwpp.DType.BF16))
+    outs = []
+    for cap in (str(1 << 30), "0"):
+        monkeypatch.setenv("BWPP_ATTN_BWD_DS_MB", cap)
+        be = bwpp.HipBackend(0)
+        try:
+            be.set_stream(torch.cuda.current_stream())
+            o = torch.empty_like(q)
+            lse = torch.empty(B, H, S, device="cuda")
+            be.dispatch_attention_lse(q, k, v, o, lse, prm)
+            g = [torch.empty_like(t) for t in (q, k, v)]
+            be.dispatch_attention_grad(q, k, v, o, do, lse, *g, prm)
+            torch.cuda.synchronize()
+            assert be.last_kernel == W8_DKDV.format("_causal"), be.last_kernel
+            outs.append(g)
+        finally:
+            be.close()
+    for a, b in zip(*outs):
+        assert torch_isfinite_all(a)
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_bf16_grad_c4_shape(be, oracle, causal):
     """Config 4's shape, the one the bench times: B8 H32 S2048 d128 bf16,
