@@ -17,6 +17,13 @@
 // global_load_lds while tile t is used, one barrier per tile) and works
 // through each tile in 32-row blocks.
 //
+// Two schemes.  Recompute: the dQ pass (which also writes D_m) forms S, dP
+// and dS itself, then the dK/dV pass forms them again (7 products for the
+// 5 the FLOP count has).  Stored dS (d = 128; the runtime's default when
+// the workspace allows): a D_m pass, the dK/dV pass storing the dS it forms
+// (DsBlk layout), and a dQ pass that only multiplies it by K.  Both visit
+// the same 32 x 32 blocks with the same operands: the same results.
+//
 // MFMA operands (32x32x16 bf16): lane l supplies A[l % 32][8 (l / 32) ..
 // +7] and B[8 (l / 32) .. +7][l % 32]; accumulator register r of lane l is
 // C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].

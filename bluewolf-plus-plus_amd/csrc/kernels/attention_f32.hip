@@ -9,7 +9,9 @@
 // inv = sum > 0 ? 1/sum : 0) generalised with a score scale and a
 // bottom-right aligned causal mask (key n visible to query m iff
 // n <= m + N - M); the backward is the closed form of the graph's
-// softmax_grad chain (compiler/graph_ir.c:1722-1733) fused per tile.
+// softmax_grad chain (compiler/graph_ir.c:1722-1733) fused per tile, either
+// in two passes that each form S and dP (recompute) or with the dK/dV pass
+// storing dS for a dQ = dS K pass (stored dS, after a D_m pass).
 //
 // Work layout.  A block is kW waves; each wave owns 32 rows (queries for
 // the forward and dQ kernels, keys for the dK/dV kernel) and the block

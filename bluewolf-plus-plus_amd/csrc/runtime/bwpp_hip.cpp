@@ -1204,9 +1204,9 @@ BwppHipStatus attn_grad_impl(BwppHip *h, const void *q, const void *k, const voi
   g.dk = dk;
   g.dv = dv;
   g.dsum = dsum_buf ? dsum_buf : static_cast<float *>(h->ws);
-  // Matrix-core passes (fp32 or bf16 kernels): dQ (also writes D_m =
-  // rowsum(dO * O)), then dK / dV.  wq / wk: waves (32 rows each) per block
-  // of the dQ / dK-dV kernel, as each was compiled.
+  // Matrix-core passes of the recompute scheme (fp32 or bf16 kernels): dQ
+  // (also writes D_m = rowsum(dO * O)), then dK / dV.  wq / wk: waves (32
+  // rows each) per block of the dQ / dK-dV kernel, as each was compiled.
   auto run_mfma = [&](BwppAttnArgs f, hipFunction_t fdq, hipFunction_t fdkdv, uint32_t wq = kAttnWaves,
                       uint32_t wk = kAttnWaves) -> BwppHipStatus {
     f.scale = scale;
