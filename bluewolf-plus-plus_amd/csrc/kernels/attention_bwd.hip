@@ -463,22 +463,22 @@ struct DsBlk {
 // dQ pass of the stored-dS scheme: dQ = scale dS K with dS^T read from
 // a.dst (written by the dK / dV pass) instead of recomputed from S and dP.
 // A wave owns 32 queries (one query block); the block streams TR-key tiles
-// of K and the matching dS^T blocks through an NS-stage ring (the dS^T
-// stream comes from HBM, so NS - 1 tiles are in flight while one is used).
+// of K and the matching dS^T blocks through the two-stage ring.  The pass
+// is bound by reading dS^T (a copy without its MFMAs takes as long); more
+// stages (32-key tiles in 3-5, or a third dS^T stage) or staging dS^T
+// through registers were slower.
 // The same 32 x 32 blocks as in bwd_dq are visited (the dK / dV pass
 // stores exactly those), and each MFMA gets the same operands in the same
 // slots, so dQ is bit-identical to bwd_dq's but for the sign of all-zero
 // sums.
-template <bool CAUSAL, int TR, int NS>
+template <bool CAUSAL, int TR>
 __device__ __forceinline__ void bwd_dq_ds(const BwppAttnArgs &a) {
   constexpr int D = 128, DB = D / 32, kW = 4, TB = TR * D * 2, RB = D * 2;
   constexpr int KB = TR / kR;                                           // key blocks per tile
   constexpr uint32_t SB = (uint32_t)(KB * kW) * DsBlk::kBytes;          // dS^T bytes per tile
   static_assert(SB == (uint32_t)TB, "a dS^T tile (TR keys x 128 queries) is as large as a K tile");
   constexpr int SPW = (int)(SB / 1024u) / kW;                           // 1 KiB DMA pieces per wave
-  constexpr int LPT = TileDmaB<D, kW, TR>::BPW + SPW;                   // loads per wave per tile
-  static_assert(NS >= 2 && NS <= 5 && LPT * (NS - 2) < 64, "ring depth");
-  __shared__ __attribute__((aligned(16))) unsigned char lds[NS][2][TB];  // [stage][K, dS^T]
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2][2][TB];  // [stage][K, dS^T]
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
   const int li = lane & 31, hi = lane >> 5;
   const SliceB<CAUSAL> sl(a);
@@ -516,8 +516,8 @@ __device__ __forceinline__ void bwd_dq_ds(const BwppAttnArgs &a) {
   const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)&lds[0][0][0];
   const TileDmaB<D, kW, TR> dma(wave, lane);
-  auto issue = [&](uint32_t t) {  // K tile t / its dS^T blocks into stage t % NS
-    const uint32_t sb = lds0 + (t % (uint32_t)NS) * (uint32_t)(2 * TB);
+  auto issue = [&](uint32_t t) {  // K tile t / its dS^T blocks into stage t % 2
+    const uint32_t sb = lds0 + (t & 1u) * (uint32_t)(2 * TB);
     dma.issue1(K, a.ldk, t * TR, a.N, sb, wv);
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
@@ -527,22 +527,14 @@ __device__ __forceinline__ void bwd_dq_ds(const BwppAttnArgs &a) {
               sb + (uint32_t)TB + j * 1024u);
     }
   };
-  // Tile t's loads are done once at most (tiles issued after it) x LPT of
-  // this wave's loads are outstanding (they complete in order).
-  auto wait_tile = [&](uint32_t later) {
-    if (NS > 4 && later >= 3) wait_vmcnt<(NS > 4 ? 3 * LPT : 0)>();
-    else if (NS > 3 && later >= 2) wait_vmcnt<(NS > 3 ? 2 * LPT : 0)>();
-    else if (NS > 2 && later >= 1) wait_vmcnt<(NS > 2 ? LPT : 0)>();
-    else wait_vmcnt<0>();
-  };
-#pragma unroll
-  for (int i = 0; i < NS - 1; ++i)
-    if ((uint32_t)i < nt) issue((uint32_t)i);
+  if (nt > 0) {
+    issue(0);
+    wait_vmcnt<0>();
+  }
+  __syncthreads();
   for (uint32_t t = 0; t < nt; ++t) {
-    wait_tile(min(nt - 1u - t, (uint32_t)(NS - 2)));
-    __syncthreads();  // tile t in LDS; every wave is done with tile t - 1
-    if (t + NS - 1 < nt) issue(t + NS - 1);
-    const uint32_t st = t % (uint32_t)NS;
+    if (t + 1 < nt) issue(t + 1);
+    const uint32_t st = t & 1u;
 #pragma unroll
     for (int sb = 0; sb < KB; ++sb) {
       const uint32_t k0 = t * TR + sb * kR;
@@ -567,6 +559,8 @@ __device__ __forceinline__ void bwd_dq_ds(const BwppAttnArgs &a) {
         }
       }
     }
+    wait_vmcnt<0>();  // tile t + 1 is in LDS (this wave's part; the barrier does the rest)
+    __syncthreads();
   }
   if (qi < a.M) store_t<D>(dQ, a.ldq, qi, dq, a.scale, hi);
 }
@@ -805,7 +799,7 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_attn_bwd_bf16_d128_dsum(c
   }                                                                                                 \
   extern "C" __global__ __launch_bounds__(256) void bwpp_attn_bwd_bf16_mfma_d128##SUFFIX##_dq_ds(     \
       const BwppAttnArgs a) {                                                                       \
-    bwd_dq_ds<CAUSAL, kTR, 2>(a);                                                                   \
+    bwd_dq_ds<CAUSAL, kTR>(a);                                                                   \
   }
 BWPP_ATTN_BWD_BF16_DS(false, )
 BWPP_ATTN_BWD_BF16_DS(true, _causal)
