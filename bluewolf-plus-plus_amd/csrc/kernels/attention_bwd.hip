@@ -321,19 +321,38 @@ __device__ __forceinline__ float row_dsum(const bf16x8_t (&gf)[D / 16], const ui
 
 // D_m pass of the stored-dS scheme (which has no dQ pass before the dK / dV
 // pass): a wave per 32 query rows, kW waves per block, q_tiles blocks per
-// slice.
+// slice.  The block's dO and O rows come into LDS with the coalesced DMA
+// (1 KiB per instruction; loading them per lane, 32 bytes of 32 rows per
+// instruction, ran at 4.5 TB/s) and each lane sums its half rows from
+// there in row_dsum's order, so D_m has the same bits as the dQ pass's.
 template <int D, int kW>
 __device__ __forceinline__ void bwd_dsum(const BwppAttnArgs &a) {
+  constexpr int RB = D * 2, TB = kW * kR * RB;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2][TB];  // [dO, O] rows of the block
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
-  const int li = lane & 31, hi = lane >> 5;
+  const int hi = lane >> 5;
   const uint32_t bh = blockIdx.x / a.q_tiles, tile = blockIdx.x % a.q_tiles;
   const uint32_t b = bh / a.heads, h = bh % a.heads;
   const uint16_t *O = static_cast<const uint16_t *>(a.o) + b * a.o_bs + h * a.o_hs;
   const uint16_t *dO = static_cast<const uint16_t *>(a.dout) + b * a.o_bs + h * a.o_hs;
-  const uint32_t qi = (tile * kW + (uint32_t)wave) * kR + (uint32_t)li;
-  bf16x8_t gf[D / 16];
-  load_row<D>(gf, dO, a.ldo, qi, a.M, hi);
-  const float dsum = row_dsum<D>(gf, O, a.ldo, qi, a.M, hi);
+  const uint32_t r0 = tile * (kW * kR), qi = r0 + (uint32_t)wave * kR + (uint32_t)(lane & 31);
+  const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)&lds[0][0];
+  const TileDmaB<D, kW, kW * kR> dma(wave, lane);
+  dma.issue(dO, a.ldo, O, a.ldo, r0, a.M, lds0, lds0 + (uint32_t)TB, wv);  // rows past M re-read row M - 1
+  wait_vmcnt<0>();
+  __syncthreads();
+  const Offsets<D> off(lane);
+  const unsigned char *gt = lds[0] + wave * kR * RB, *ot = lds[1] + wave * kR * RB;
+  float part = 0.0f;
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) {
+    const bf16x8_t g = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(gt + off.row(ks)));
+    const bf16x8_t o = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(ot + off.row(ks)));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part += (float)g[e] * (float)o[e];
+  }
+  const float dsum = sum32(part);
   if (qi < a.M && hi == 0) a.dsum[(size_t)bh * a.M + qi] = dsum;
 }
 
