@@ -91,6 +91,7 @@ typedef struct {
    * query count rounded up to 128. */
   void *dst;
   uint32_t ld_dst;
+  uint32_t items; /* persistent flash forward: (slice, query tile) items */
 } BwppAttnArgs;
 
 /* Attention operand copies between the caller's strided bf16 layout

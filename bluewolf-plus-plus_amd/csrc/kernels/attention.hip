@@ -408,6 +408,294 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
   __syncthreads();  // the block's next tile reuses smem
 }
 
+// Persistent form of the unmasked kernel: a block (one per CU) works
+// through a.items (slice, query tile) items, item k of block b being
+// k * G + b' (b' the XCD renumbering of b below, so each XCD's blocks take
+// the query tiles of a few slices together in every round).  Per item the
+// work is attn_bf16_d128_tile's; what differs is the item boundary: the
+// next item's first K / V stage is requested at the start of the current
+// item's last key tile (into the stage that tile does not use), its Q rows
+// as soon as the last tile's S products have read the current ones, and O
+// is staged through the last tile's stage -- so the next item's loads are
+// in flight during the last tile and the O epilogue instead of after them
+// (with one item per block they cost 2.7 us for Q, 1.3 us for the first
+// stage and 1.5 us for O of each 62 us item at C4).
+__device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
+  constexpr int kBKV = 128;
+  constexpr int D = 128;
+  constexpr int KS = D / 16;
+  constexpr int DB = D / 32;
+  constexpr int kTile = kBKV * D * 2;
+  constexpr int kStage = 2 * kTile;
+  constexpr int kOut = kBQ * D * 2;
+  static_assert(kOut <= kStage, "O is staged through one ring stage");
+  constexpr int kBlkPW = (kBKV / 4) / kFW;
+  constexpr int KB = kBKV / 32;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * kStage];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t lq = (uint32_t)(lane & 31), lh = (uint32_t)(lane >> 5);
+  const uint32_t G = gridDim.x, QT = a.q_tiles;
+  const uint32_t bp = G % 8u == 0 ? (blockIdx.x % 8u) * (G / 8u) + blockIdx.x / 8u : blockIdx.x;
+  const uint32_t nitems = bp < a.items ? (a.items - bp + G - 1) / G : 0u;
+  if (nitems == 0) return;
+  const uint32_t nkt = (a.N + kBKV - 1) / kBKV;  // key tiles of every item (N > 0)
+  const uint32_t t_mask = min(a.N / kBKV, nkt);   // first tile with keys past N
+
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)smem;
+  uint32_t dma_row[kBlkPW], dma_kcol[kBlkPW], dma_vcol[kBlkPW];
+#pragma unroll
+  for (int i = 0; i < kBlkPW; ++i) {
+    const uint32_t q = (uint32_t)(wave * kBlkPW + i) * 64u + (uint32_t)lane;
+    const uint32_t r = q >> 4, pc = q & 15u;
+    dma_row[i] = r;
+    dma_kcol[i] = 8u * (pc ^ (r & 15u));
+    dma_vcol[i] = 8u * (pc ^ (4u * (r & 3u)));
+  }
+  struct Item {
+    const uint16_t *Q, *K, *V;
+    uint16_t *O;
+    uint32_t bh, q0;
+  };
+  auto item = [&](uint32_t k) {
+    const uint32_t li = k * G + bp, bh = li / QT, qt = QT - 1 - li % QT;
+    const uint32_t b = bh / a.heads, h = bh % a.heads;
+    Item it;
+    it.Q = static_cast<const uint16_t *>(a.q) + b * a.q_bs + h * a.q_hs;
+    it.K = static_cast<const uint16_t *>(a.k) + b * a.k_bs + h * a.k_hs;
+    it.V = static_cast<const uint16_t *>(a.v) + b * a.v_bs + h * a.v_hs;
+    it.O = static_cast<uint16_t *>(a.o) + b * a.o_bs + h * a.o_hs;
+    it.bh = bh;
+    it.q0 = qt * kBQ + (uint32_t)wave * kQW;
+    return it;
+  };
+  auto issue = [&](const Item &it, uint32_t t, uint32_t stage) {
+    const uint32_t st = lds0 + stage * kStage + (uint32_t)(wave * kBlkPW) * 1024u;
+#pragma unroll
+    for (int i = 0; i < kBlkPW; ++i) {
+      uint32_t key = t * kBKV + dma_row[i];
+      key = key < a.N ? key : a.N - 1;
+      g2lds16_so(it.K, 2u * (key * a.ldk + dma_kcol[i]), st + (uint32_t)i * 1024u);
+      g2lds16_so(it.V, 2u * (key * a.ldv + dma_vcol[i]), st + kTile + (uint32_t)i * 1024u);
+    }
+  };
+  bf16x8_t qf[KS];
+  auto load_q = [&](const Item &it) {
+    const uint32_t qi = it.q0 + lq;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (qi < a.M) v = *reinterpret_cast<const uint4 *>(it.Q + (size_t)qi * a.ldq + 16 * ks + 8 * lh);
+      qf[ks] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  };
+
+  const uint32_t grp = (uint32_t)((lane >> 4) & 3), L = (uint32_t)(lane & 15);
+  uint32_t koff[KS], voff[DB];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = k_off(lq, 2u * ks + lh);
+  {
+    const uint32_t kbase = 4u * (grp >> 1) + (L >> 2);
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const uint32_t col = 32u * d + 16u * (grp & 1u) + 4u * (L & 3u);
+      voff[d] = kTile + v_off(kbase, col >> 3) + (col & 7u) * 2u;
+    }
+  }
+  const float c = a.scale_log2;
+
+  // First item: Q, then its first stage (the Q loads land first, as in
+  // attn_bf16_d128_tile).
+  Item cur = item(0);
+  load_q(cur);
+  wait_vmcnt<0>();
+  issue(cur, 0, 0);
+  uint32_t s0 = 0;  // ring stage of the current item's key tile 0
+
+  for (uint32_t k = 0; k < nitems; ++k) {
+    const bool has_next = k + 1 < nitems;
+    const Item nxt = item(has_next ? k + 1 : k);
+    const uint32_t qi = cur.q0 + lq;
+    f32x16_t o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[d][r] = 0.0f;
+    float mrow = -INFINITY, lrow = 0.0f;
+
+    auto tile = [&](auto mask_tag, const unsigned char *Ks, uint32_t k0, bool last) {
+      constexpr bool MASK = decltype(mask_tag)::value;
+      int kbmax = KB - 1;
+      if constexpr (MASK) {
+        const int64_t kv = (int64_t)a.N - 1 - (int64_t)k0;
+        kbmax = kv < 0 ? -1 : (int)(kv / 32 < KB - 1 ? kv / 32 : KB - 1);
+        kbmax = __builtin_amdgcn_readfirstlane(kbmax);
+      }
+      f32x16_t s[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
+        if (MASK && kb > kbmax) continue;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const bf16x8_t kf =
+              __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(Ks + koff[ks] + 32u * 256u * kb));
+          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb], 0, 0, 0);
+        }
+      }
+      if constexpr (!MASK) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+        for (int i = 0; i < KB * KS - 2; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      }
+      // The current Q rows are no longer needed: request the next item's.
+      if (last && has_next) load_q(nxt);
+
+      float mx = -INFINITY;
+      if constexpr (MASK) {
+        const int64_t lim64 = (int64_t)a.N - (int64_t)(k0 + 4u * lh);
+        const int lim = (int)(lim64 < -1 ? -1 : (lim64 > kBKV ? kBKV : lim64));
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float x = (32 * kb + 8 * (r >> 2) + (r & 3)) < lim ? s[kb][r] : -INFINITY;
+            s[kb][r] = x;
+            mx = fmaxf(mx, x);
+          }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+      }
+      {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+        mx = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])) * c;
+      }
+      float alpha = 1.0f;
+      if (mx > mrow + kLazy) {
+        alpha = __builtin_amdgcn_exp2f(mrow - mx);
+        mrow = mx;
+      }
+      const float muse = mrow == -INFINITY ? 0.0f : mrow;
+      float sum = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], c, -muse));
+          s[kb][r] = p;
+          sum += p;
+        }
+      {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false);
+        sum = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      }
+      lrow = lrow * alpha + sum;
+      if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+      }
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        if (MASK && kb > kbmax) continue;
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq) {
+          const int r0 = 8 * kq;
+          uint4 w;
+          w.x = pack_bf16x2(s[kb][r0 + 0], s[kb][r0 + 1]);
+          w.y = pack_bf16x2(s[kb][r0 + 2], s[kb][r0 + 3]);
+          w.z = pack_bf16x2(s[kb][r0 + 4], s[kb][r0 + 5]);
+          w.w = pack_bf16x2(s[kb][r0 + 6], s[kb][r0 + 7]);
+          const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, w);
+          constexpr uint32_t kRowB = 256u;
+          const uint32_t rstep = (32u * kb + 16u * kq) * kRowB;
+#pragma unroll
+          for (int d = 0; d < DB; ++d) {
+            const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Ks + voff[d] + rstep));
+            const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Ks + voff[d] + rstep + 8u * kRowB));
+            const v8s_t vv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), pf, o[d], 0, 0, 0);
+          }
+        }
+      }
+      if constexpr (!MASK) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 2 * KB * DB - 2; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      }
+    };
+
+    // Tile t lives in stage (s0 + t) % 2.  At tile t's barrier every wave is
+    // done with tile t - 1, whose stage then takes tile t + 1 -- or, at the
+    // last tile, the next item's tile 0.
+    auto step = [&](uint32_t t) {
+      wait_vmcnt<0>();
+      __syncthreads();
+      const uint32_t nst = (s0 + t + 1) & 1u;
+      if (t + 1 < nkt) issue(cur, t + 1, nst);
+      else if (has_next) issue(nxt, 0, nst);
+      return smem + __builtin_amdgcn_readfirstlane(((s0 + t) & 1u) * kStage);
+    };
+    for (uint32_t t = 0; t < t_mask; ++t) {
+      const unsigned char *Ks = step(t);
+      tile(std::integral_constant<bool, false>{}, Ks, t * kBKV, t + 1 == nkt);
+    }
+    for (uint32_t t = t_mask; t < nkt; ++t) {
+      const unsigned char *Ks = step(t);
+      tile(std::integral_constant<bool, true>{}, Ks, t * kBKV, t + 1 == nkt);
+    }
+    __syncthreads();
+
+    // O through the last tile's stage (the other one holds the next item's
+    // tile 0); the next item's tile 1 goes into this stage after its first
+    // barrier, which comes after these reads.
+    uint16_t *os = reinterpret_cast<uint16_t *>(smem + ((s0 + nkt - 1) & 1u) * kStage) + (size_t)wave * kQW * D;
+    if (a.lse && lh == 0 && qi < a.M)
+      a.lse[(size_t)cur.bh * a.M + qi] =
+          lrow > 0.0f ? ((mrow == -INFINITY ? 0.0f : mrow) + log2f(lrow)) * 0.69314718055994531f : -INFINITY;
+    {
+      const float inv = lrow > 0.0f ? 1.0f / lrow : 0.0f;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const uint32_t chunk = (4u * d + q4) ^ (lq & 15u);
+          uint2 w;
+          w.x = pack_bf16x2(o[d][4 * q4 + 0] * inv, o[d][4 * q4 + 1] * inv);
+          w.y = pack_bf16x2(o[d][4 * q4 + 2] * inv, o[d][4 * q4 + 3] * inv);
+          *reinterpret_cast<uint2 *>(os + lq * D + 8u * chunk + 4u * lh) = w;
+        }
+    }
+    __syncthreads();
+    constexpr int kRowChunks = D / 8;
+#pragma unroll 4
+    for (int it = 0; it < kQW * kRowChunks / 64; ++it) {
+      const int q = lane + it * 64;
+      const uint32_t ql = (uint32_t)(q / kRowChunks), cc = (uint32_t)(q % kRowChunks);
+      const uint32_t qo = cur.q0 + ql;
+      if (qo < a.M)
+        *reinterpret_cast<uint4 *>(cur.O + (size_t)qo * a.ldo + 8u * cc) =
+            *reinterpret_cast<const uint4 *>(os + ql * D + 8u * (cc ^ (ql & 15u)));
+    }
+    s0 = (s0 + nkt) & 1u;
+    cur = nxt;
+  }
+}
+
 // Work per block.  Blocks are dispatched round-robin over the 8 XCDs; the
 // renumbering below gives each XCD a contiguous run of (batch, head) slices
 // with all of their query tiles, so the blocks that stream the same K / V
@@ -733,6 +1021,12 @@ BWPP_ATTN_GENERIC(bwpp_attn_generic_bf16_causal, uint16_t, true)
 extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void
 bwpp_attn_bf16_d128(const BwppAttnArgs a) {
   attn_bf16_d128<false>(a);
+}
+// Persistent unmasked form (a.items (slice, query tile) items over one
+// block per CU).
+extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void
+bwpp_attn_bf16_d128_p(const BwppAttnArgs a) {
+  attn_bf16_d128_persist(a);
 }
 extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void
 bwpp_attn_bf16_d128_causal(const BwppAttnArgs a) {
