@@ -408,10 +408,11 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
   __syncthreads();  // the block's next tile reuses smem
 }
 
-// Persistent form of the unmasked kernel: a block (one per CU) works
-// through a.items (slice, query tile) items, item k of block b being
+// Persistent form of the kernel: a block (one per CU) works through its
+// items -- unmasked: (slice, query tile) items, item k of block b being
 // k * G + b' (b' the XCD renumbering of b below, so each XCD's blocks take
-// the query tiles of a few slices together in every round).  Per item the
+// the query tiles of a few slices together in every round); causal: the
+// same over pairs of query tiles, as attn_bf16_d128 pairs them.  Per item the
 // work is attn_bf16_d128_tile's; what differs is the item boundary: the
 // next item's first K / V stage is requested at the start of the current
 // item's last key tile (into the stage that tile does not use), its Q rows
@@ -420,6 +421,7 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
 // in flight during the last tile and the O epilogue instead of after them
 // (with one item per block they cost 2.7 us for Q, 1.3 us for the first
 // stage and 1.5 us for O of each 62 us item at C4).
+template <bool CAUSAL>
 __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
   constexpr int kBKV = 128;
   constexpr int D = 128;
@@ -438,10 +440,14 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
   const uint32_t lq = (uint32_t)(lane & 31), lh = (uint32_t)(lane >> 5);
   const uint32_t G = gridDim.x, QT = a.q_tiles;
   const uint32_t bp = G % 8u == 0 ? (blockIdx.x % 8u) * (G / 8u) + blockIdx.x / 8u : blockIdx.x;
-  const uint32_t nitems = bp < a.items ? (a.items - bp + G - 1) / G : 0u;
+  // Unmasked: a.items (slice, query tile) items.  Causal: a.items pairs of
+  // query tiles QT - 1 - p and p of one slice, as attn_bf16_d128 pairs them
+  // (one item when they coincide); block b' takes pairs j G + b'.
+  const uint32_t P = (QT + 1) / 2;
+  const uint32_t nunits = bp < a.items ? (a.items - bp + G - 1) / G : 0u;
+  const uint32_t nitems = CAUSAL ? 2u * nunits : nunits;  // slots; a causal pair's second may be empty
   if (nitems == 0) return;
-  const uint32_t nkt = (a.N + kBKV - 1) / kBKV;  // key tiles of every item (N > 0)
-  const uint32_t t_mask = min(a.N / kBKV, nkt);   // first tile with keys past N
+  const int64_t diag = (int64_t)a.N - (int64_t)a.M;  // key n visible to query m iff n <= m + diag
 
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)smem;
   uint32_t dma_row[kBlkPW], dma_kcol[kBlkPW], dma_vcol[kBlkPW];
@@ -456,10 +462,28 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
   struct Item {
     const uint16_t *Q, *K, *V;
     uint16_t *O;
-    uint32_t bh, q0;
+    uint32_t bh, q0, qb0;
+  };
+  // Slot k: its slice and query tile; valid(k) is false only for the empty
+  // second slot of a causal pair whose two tiles coincide.
+  auto slot_tile = [&](uint32_t k, uint32_t &bh) {
+    if (!CAUSAL) {
+      const uint32_t li = k * G + bp;
+      bh = li / QT;
+      return QT - 1 - li % QT;
+    }
+    const uint32_t pi = (k >> 1) * G + bp, p = pi % P;
+    bh = pi / P;
+    return (k & 1u) ? p : QT - 1 - p;
+  };
+  auto valid = [&](uint32_t k) {
+    if (!CAUSAL || !(k & 1u)) return k < nitems;
+    const uint32_t p = ((k >> 1) * G + bp) % P;
+    return k < nitems && p != QT - 1 - p;
   };
   auto item = [&](uint32_t k) {
-    const uint32_t li = k * G + bp, bh = li / QT, qt = QT - 1 - li % QT;
+    uint32_t bh;
+    const uint32_t qt = slot_tile(k, bh);
     const uint32_t b = bh / a.heads, h = bh % a.heads;
     Item it;
     it.Q = static_cast<const uint16_t *>(a.q) + b * a.q_bs + h * a.q_hs;
@@ -467,8 +491,26 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
     it.V = static_cast<const uint16_t *>(a.v) + b * a.v_bs + h * a.v_hs;
     it.O = static_cast<uint16_t *>(a.o) + b * a.o_bs + h * a.o_hs;
     it.bh = bh;
-    it.q0 = qt * kBQ + (uint32_t)wave * kQW;
+    it.qb0 = qt * kBQ;
+    it.q0 = it.qb0 + (uint32_t)wave * kQW;
     return it;
+  };
+  // Key tiles an item needs, and its first tile with a masked (key, query).
+  auto key_tiles = [&](const Item &it) {
+    uint32_t kend = a.N;
+    if (CAUSAL) {
+      const int64_t lim = (int64_t)min(it.qb0 + kBQ, a.M) - 1 + diag + 1;
+      kend = lim <= 0 ? 0u : (uint32_t)min<int64_t>(lim, a.N);
+    }
+    return (kend + kBKV - 1) / kBKV;
+  };
+  auto first_masked = [&](const Item &it, uint32_t nkt) {
+    uint32_t tm = a.N / kBKV;
+    if (CAUSAL) {
+      const int64_t first_hidden = (int64_t)it.qb0 + diag + 1;
+      tm = min(tm, first_hidden <= 0 ? 0u : (uint32_t)min<int64_t>(first_hidden / kBKV, (int64_t)nkt));
+    }
+    return min(tm, nkt);
   };
   auto issue = [&](const Item &it, uint32_t t, uint32_t stage) {
     const uint32_t st = lds0 + stage * kStage + (uint32_t)(wave * kBlkPW) * 1024u;
@@ -491,18 +533,13 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
     }
   };
 
+  // Per-lane LDS read offsets of k-step 0 / d block 0 (as in
+  // attn_bf16_d128_tile); the others differ in chunk bits the swizzles XOR
+  // and never carry into: K operand of k-step ks at koff0 ^ 32 ks, V^T of d
+  // block d at voff0 ^ 64 d.  The tile recomputes them (see below).
   const uint32_t grp = (uint32_t)((lane >> 4) & 3), L = (uint32_t)(lane & 15);
-  uint32_t koff[KS], voff[DB];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) koff[ks] = k_off(lq, 2u * ks + lh);
-  {
-    const uint32_t kbase = 4u * (grp >> 1) + (L >> 2);
-#pragma unroll
-    for (int d = 0; d < DB; ++d) {
-      const uint32_t col = 32u * d + 16u * (grp & 1u) + 4u * (L & 3u);
-      voff[d] = kTile + v_off(kbase, col >> 3) + (col & 7u) * 2u;
-    }
-  }
+  const uint32_t koff0 = k_off(lq, lh);
+  const uint32_t voff0 = kTile + v_off(4u * (grp >> 1) + (L >> 2), 2u * (grp & 1u) + ((L & 3u) >> 1)) + (4u * (L & 1u)) * 2u;
   const float c = a.scale_log2;
 
   // First item: Q, then its first stage (the Q loads land first, as in
@@ -514,9 +551,12 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
   uint32_t s0 = 0;  // ring stage of the current item's key tile 0
 
   for (uint32_t k = 0; k < nitems; ++k) {
-    const bool has_next = k + 1 < nitems;
-    const Item nxt = item(has_next ? k + 1 : k);
+    if (!valid(k)) continue;
+    const uint32_t kn = valid(k + 1) ? k + 1 : k + 2;  // the next item's slot
+    const bool has_next = kn < nitems;
+    const Item nxt = item(has_next ? kn : k);
     const uint32_t qi = cur.q0 + lq;
+    const uint32_t nkt = key_tiles(cur), t_mask = first_masked(cur, nkt);
     f32x16_t o[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d)
@@ -526,9 +566,18 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
 
     auto tile = [&](auto mask_tag, const unsigned char *Ks, uint32_t k0, bool last) {
       constexpr bool MASK = decltype(mask_tag)::value;
+      // The offsets through an empty asm tied to the tile, so that their
+      // XORed forms stay inside the tile instead of occupying twelve
+      // registers across the whole item loop (the causal kernel spilled).
+      uint32_t ko = koff0, vo = voff0;
+      asm("" : "+v"(ko), "+v"(vo) : "s"(k0));
       int kbmax = KB - 1;
       if constexpr (MASK) {
-        const int64_t kv = (int64_t)a.N - 1 - (int64_t)k0;
+        int64_t kv = (int64_t)a.N - 1 - (int64_t)k0;
+        if (CAUSAL) {
+          const int64_t kc = (int64_t)(cur.q0 + kQW - 1) + diag - (int64_t)k0;
+          kv = kc < kv ? kc : kv;
+        }
         kbmax = kv < 0 ? -1 : (int)(kv / 32 < KB - 1 ? kv / 32 : KB - 1);
         kbmax = __builtin_amdgcn_readfirstlane(kbmax);
       }
@@ -541,7 +590,7 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           const bf16x8_t kf =
-              __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(Ks + koff[ks] + 32u * 256u * kb));
+              __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(Ks + (ko ^ (32u * ks)) + 32u * 256u * kb));
           s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb], 0, 0, 0);
         }
       }
@@ -559,7 +608,11 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
 
       float mx = -INFINITY;
       if constexpr (MASK) {
-        const int64_t lim64 = (int64_t)a.N - (int64_t)(k0 + 4u * lh);
+        int64_t lim64 = (int64_t)a.N - (int64_t)(k0 + 4u * lh);
+        if (CAUSAL) {
+          const int64_t c64 = (int64_t)qi + diag + 1 - (int64_t)(k0 + 4u * lh);
+          lim64 = c64 < lim64 ? c64 : lim64;
+        }
         const int lim = (int)(lim64 < -1 ? -1 : (lim64 > kBKV ? kBKV : lim64));
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
@@ -621,8 +674,9 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
           const uint32_t rstep = (32u * kb + 16u * kq) * kRowB;
 #pragma unroll
           for (int d = 0; d < DB; ++d) {
-            const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Ks + voff[d] + rstep));
-            const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Ks + voff[d] + rstep + 8u * kRowB));
+            const uint32_t vd = vo ^ (64u * d);
+            const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Ks + vd + rstep));
+            const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(Ks + vd + rstep + 8u * kRowB));
             const v8s_t vv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), pf, o[d], 0, 0, 0);
           }
@@ -654,16 +708,28 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
       const unsigned char *Ks = step(t);
       tile(std::integral_constant<bool, false>{}, Ks, t * kBKV, t + 1 == nkt);
     }
+    // A tile whose keys this wave's queries see none of goes through tile()
+    // too: no MFMA runs (kbmax = -1), the all -inf scores leave the running
+    // max, the sum and O exactly as they were, and the next item's Q rows
+    // are requested at one place (a second one, in a skip branch, made the
+    // compiler keep two versions of them and spill).
     for (uint32_t t = t_mask; t < nkt; ++t) {
       const unsigned char *Ks = step(t);
       tile(std::integral_constant<bool, true>{}, Ks, t * kBKV, t + 1 == nkt);
     }
     __syncthreads();
+    if (nkt == 0 && has_next) {
+      // No key tile: the next item's loads start here (after this item's
+      // own, unused, first-stage DMA into the same stage has landed).
+      wait_vmcnt<0>();
+      load_q(nxt);
+      issue(nxt, 0, s0);
+    }
 
     // O through the last tile's stage (the other one holds the next item's
     // tile 0); the next item's tile 1 goes into this stage after its first
     // barrier, which comes after these reads.
-    uint16_t *os = reinterpret_cast<uint16_t *>(smem + ((s0 + nkt - 1) & 1u) * kStage) + (size_t)wave * kQW * D;
+    uint16_t *os = reinterpret_cast<uint16_t *>(smem + ((s0 + nkt + 1) & 1u) * kStage) + (size_t)wave * kQW * D;
     if (a.lse && lh == 0 && qi < a.M)
       a.lse[(size_t)cur.bh * a.M + qi] =
           lrow > 0.0f ? ((mrow == -INFINITY ? 0.0f : mrow) + log2f(lrow)) * 0.69314718055994531f : -INFINITY;
@@ -1026,7 +1092,11 @@ bwpp_attn_bf16_d128(const BwppAttnArgs a) {
 // block per CU).
 extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void
 bwpp_attn_bf16_d128_p(const BwppAttnArgs a) {
-  attn_bf16_d128_persist(a);
+  attn_bf16_d128_persist<false>(a);
+}
+extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void
+bwpp_attn_bf16_d128_causal_p(const BwppAttnArgs a) {
+  attn_bf16_d128_persist<true>(a);
 }
 extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void
 bwpp_attn_bf16_d128_causal(const BwppAttnArgs a) {

@@ -110,31 +110,35 @@ def test_flash_bf16_d128(be, oracle, B, H, M, N, causal):
     assert rel_max_err(host(o), oracle.attention_bh(q, k, v, scale, causal)) <= BF16_TOL
 
 
-@pytest.mark.parametrize("M,N", [(2048, 2048), (1000, 1300), (1300, 700)])
-def test_flash_bf16_d128_persistent(oracle, monkeypatch, M, N):
-    """More (slice, query tile) items than CUs: the unmasked forward runs the
-    persistent kernel (one block per CU working through its items, the next
-    item's first K / V stage and Q rows requested during the current item's
-    last key tile).  Against the one-item-per-block kernel
-    (BWPP_ATTN_FLASH_PERSIST=0), O and lse are bit-identical -- with M and
-    N not multiples of the 256-query / 128-key tiles and an item count that
-    is not a multiple of the CU count -- and one slice matches the oracle."""
+@pytest.mark.parametrize("M,N", [(2048, 2048), (1000, 1300), (1300, 700), (1280, 1280)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_bf16_d128_persistent(oracle, monkeypatch, M, N, causal):
+    """More items than CUs ((slice, query tile) items; causal: pairs of query
+    tiles): the forward runs the persistent kernel (one block per CU working
+    through its items, the next item's first K / V stage and Q rows
+    requested during the current item's last key tile).  Against the
+    one-block-per-item kernels (BWPP_ATTN_FLASH_PERSIST=0), O and lse are
+    bit-identical -- with M and N not multiples of the 256-query / 128-key
+    tiles, an item count that is not a multiple of the CU count, M > N causal
+    (query tiles that see no key at all) and an odd tile count (a causal
+    pair with one tile) -- and one slice matches the oracle."""
     torch = pytest.importorskip("torch")
+    cs = "_causal" if causal else ""
     outs = []
-    for persist in ("1", "0"):
+    for persist in ("3", "0"):
         monkeypatch.setenv("BWPP_ATTN_FLASH_PERSIST", persist)
         b2 = bwpp.HipBackend(0)
         try:
             b2.set_stream(torch.cuda.current_stream())
-            H = b2.cus + 3  # items = H * ceil(M / 256) > CUs, not a multiple of them
+            H = 2 * b2.cus + 3  # items = H * ceil(M / 256) (causal: pairs) > CUs, not a multiple of them
             (qd, kd, vd), (q, k, v) = inputs(1, H, M, N, 128, 128, M + 7 * N, True)
             prm = bwpp.AttentionParams(M=M, N=N, K=128, D=128, ldq=128, ldk=128, ldv=128, ldo=128, batch=1,
-                                       heads=H, scale=128 ** -0.5, causal=0, dtype=int(bwpp.DType.BF16))
+                                       heads=H, scale=128 ** -0.5, causal=int(causal), dtype=int(bwpp.DType.BF16))
             o = torch.full((1, H, M, 128), 3.0, device="cuda").to(torch.bfloat16)
             lse = torch.full((1, H, M), 3.0, device="cuda")
             b2.dispatch_attention_lse(qd, kd, vd, o, lse, prm)
             torch.cuda.synchronize()
-            assert b2.last_kernel == ("bwpp_attn_bf16_d128_p" if persist == "1" else "bwpp_attn_bf16_d128")
+            assert b2.last_kernel == "bwpp_attn_bf16_d128" + cs + ("_p" if persist == "3" else "")
             outs.append((o, lse, q, k, v, H))
         finally:
             b2.close()
@@ -142,7 +146,7 @@ def test_flash_bf16_d128_persistent(oracle, monkeypatch, M, N):
     assert torch.equal(o1, o0) and torch.equal(l1, l0)
     h = H - 1
     got = host(o1[:, h:h + 1].contiguous())
-    want = oracle.attention_bh(q[:, h:h + 1], k[:, h:h + 1], v[:, h:h + 1], 128 ** -0.5, False)
+    want = oracle.attention_bh(q[:, h:h + 1], k[:, h:h + 1], v[:, h:h + 1], 128 ** -0.5, causal)
     assert rel_max_err(got, want) <= BF16_TOL
 
 
