@@ -166,6 +166,25 @@ __device__ __forceinline__ void load_row(bf16x8_t (&dst)[D / 16], const uint16_t
   }
 }
 
+// load_row for rows > 0 without the zeroing of rows past the end, and that
+// zeroing as a separate step, so that a caller can issue several loads
+// before the first wait (the select needs the loaded data).
+template <int D>
+__device__ __forceinline__ void load_row_raw(bf16x8_t (&dst)[D / 16], const uint16_t *X, uint32_t ld, uint32_t row,
+                                             uint32_t rows, int hi) {
+  const uint32_t rr = row < rows ? row : rows - 1;
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+    dst[ks] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t *>(X + (size_t)rr * ld + 16 * ks + 8 * hi));
+}
+template <int D>
+__device__ __forceinline__ void zero_past(bf16x8_t (&x)[D / 16], uint32_t row, uint32_t rows) {
+  if (row >= rows) {
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) x[ks] = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
+  }
+}
+
 // Per-lane LDS offsets: row reads (tile row li, k-step ks) and the two
 // transposing reads (tile rows 0-7 / 8-15 of a 16-row step) of d block blk.
 // Only the k-step 0 / d block 0 offsets are kept: the others differ in the
@@ -244,21 +263,51 @@ __device__ __forceinline__ f32x16_t dot_rows_lds(const unsigned char *tile, cons
   return acc;
 }
 
-// Stores a transposed accumulator set (register r of out[blk] = element
-// d = 32 blk + acc_row(r, hi) of row `row`) as bf16, times f, 8 bytes a piece.
+// Stores a wave's transposed accumulator set (lane li's register r of
+// acc[blk] = element d = 32 blk + acc_row(r, hi) of row row0 + li) as bf16,
+// times f, for the rows below `rows`.  The pieces go through the wave's own
+// 32 x 2D-byte LDS region `stage` (16-byte chunk c of row j at chunk
+// c ^ (j mod D/8): both the 8-byte writes and the 16-byte row reads are
+// bank-conflict-free) and leave as whole rows, 1 KiB of consecutive rows
+// per store instruction.  Stored straight from the accumulators, each
+// instruction wrote 16 bytes into each of 32 rows, and at C4 the dK / dV
+// pass's blocks spent 4.1 of their 144 us issuing them.  A wave's LDS
+// operations run in order, so the row reads see the writes without a wait
+// and the next call may reuse the region.
 template <int D>
-__device__ __forceinline__ void store_t(uint16_t *X, uint32_t ld, uint32_t row, const f32x16_t (&acc)[D / 32],
-                                        float f, int hi) {
-  uint16_t *dst = X + (size_t)row * ld + 4 * hi;
+__device__ __forceinline__ void store_rows(uint16_t *X, uint32_t ld, uint32_t row0, uint32_t rows,
+                                           const f32x16_t (&acc)[D / 32], float f, int lane, unsigned char *stage) {
+  constexpr int CH = D / 8, RB = 2 * D, RPI = 64 / CH;  // chunks per row, row bytes, rows per store
+  const int li = lane & 31, hi = lane >> 5;
 #pragma unroll
   for (int blk = 0; blk < D / 32; ++blk)
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
+      const int c = 4 * blk + r4;
       uint2 u;
       u.x = pack_bf16x2(acc[blk][4 * r4] * f, acc[blk][4 * r4 + 1] * f);
       u.y = pack_bf16x2(acc[blk][4 * r4 + 2] * f, acc[blk][4 * r4 + 3] * f);
-      *reinterpret_cast<uint2 *>(dst + 32 * blk + 8 * r4) = u;
+      *reinterpret_cast<uint2 *>(stage + li * RB + 16 * (c ^ (li & (CH - 1))) + 8 * hi) = u;
     }
+  const int ch = lane % CH;
+  // All row reads first: the empty asm that takes them all keeps each read
+  // out of its store's branch, where it would wait for its own round trip.
+  u32x4_t u[32 / RPI];
+#pragma unroll
+  for (int j = 0; j < 32 / RPI; ++j) {
+    const int r = j * RPI + lane / CH;
+    u[j] = *reinterpret_cast<const u32x4_t *>(stage + r * RB + 16 * (ch ^ (r & (CH - 1))));
+  }
+  static_assert(32 / RPI == 8 || 32 / RPI == 4, "4 or 8 row reads");
+  if constexpr (32 / RPI == 8)
+    asm volatile("" : "+v"(u[0]), "+v"(u[1]), "+v"(u[2]), "+v"(u[3]), "+v"(u[4]), "+v"(u[5]), "+v"(u[6]), "+v"(u[7]));
+  else
+    asm volatile("" : "+v"(u[0]), "+v"(u[1]), "+v"(u[2]), "+v"(u[3]));
+#pragma unroll
+  for (int j = 0; j < 32 / RPI; ++j) {
+    const int r = j * RPI + lane / CH;
+    if (row0 + (uint32_t)r < rows) *reinterpret_cast<u32x4_t *>(X + (size_t)(row0 + (uint32_t)r) * ld + 8 * ch) = u[j];
+  }
 }
 
 // The (batch, head) slice and the tile rank (0 .. a.q_tiles - 1, 0 the
@@ -450,7 +499,10 @@ __device__ __forceinline__ void bwd_dq(const BwppAttnArgs &a) {
     wait_vmcnt<0>();  // tile t + 1 is in LDS (this wave's part; the barrier does the rest)
     __syncthreads();
   }
-  if (qi < a.M) store_t<D>(dQ, a.ldq, qi, dq, a.scale, hi);
+  // The ring is free: every wave has passed the last tile's barrier.
+  static_assert(4 * TB >= kW * kR * RB, "one 32-row staging region per wave fits the ring");
+  store_rows<D>(dQ, a.ldq, qb + wv * (uint32_t)kR, a.M, dq, a.scale, (int)__lane_id(),
+                &lds[0][0][0] + wv * (uint32_t)(kR * RB));
 }
 
 // Stored dS^T layout: per slice, 2 KiB blocks of 32 keys x 32 queries,
@@ -581,7 +633,10 @@ __device__ __forceinline__ void bwd_dq_ds(const BwppAttnArgs &a) {
     wait_vmcnt<0>();  // tile t + 1 is in LDS (this wave's part; the barrier does the rest)
     __syncthreads();
   }
-  if (qi < a.M) store_t<D>(dQ, a.ldq, qi, dq, a.scale, hi);
+  // The ring is free: every wave has passed the last tile's barrier.
+  static_assert(4 * TB >= kW * kR * RB, "one 32-row staging region per wave fits the ring");
+  store_rows<D>(dQ, a.ldq, qb + wv * (uint32_t)kR, a.M, dq, a.scale, (int)__lane_id(),
+                &lds[0][0][0] + wv * (uint32_t)(kR * RB));
 }
 
 // dK / dV pass: a wave owns 32 keys and streams Q / dO tiles with their
@@ -630,19 +685,6 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
     m32 = a.ld_dst / 32u;
     dso = DsBlk::piece(li, hi);
   }
-  bf16x8_t kf[D / 16], vf[D / 16];
-  load_row<D>(kf, K, a.ldk, ni, a.N, hi);
-  load_row<D>(vf, V, a.ldv, ni, a.N, hi);
-  f32x16_t dk[DB], dv[DB];
-#pragma unroll
-  for (int blk = 0; blk < DB; ++blk) dk[blk] = dv[blk] = f32x16_t{};
-  const float c = a.scale_log2;
-  const Offsets<D> offs(lane);
-  if constexpr (VL) {
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) *reinterpret_cast<bf16x8_t *>(vrows[wave] + offs.row(ks)) = vf[ks];
-  }
-
   const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)&lds[0][0][0];
   const TileDmaB<D, kW, TR> dma(wave, lane);
@@ -668,9 +710,31 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
       rowv[st][1][threadIdx.x] = in ? rd : 0.0f;
     }
   };
+  // Prologue: the first Q / dO tile, its rows' lse / D_m and this wave's
+  // K and V rows are all requested before any of them is waited for, and
+  // the rows past N are zeroed only after that -- one memory round trip
+  // (a block exists only for N > 0).
+  // (Loaded one after the other, with load_row's zeroing select waiting
+  // for each, the prologue took 8.2 of a 144 us block at C4.)
   if (nt > 0) {
     issue(0);
     fetch_rows(mbeg);
+  }
+  bf16x8_t kf[D / 16], vf[D / 16];
+  load_row_raw<D>(kf, K, a.ldk, ni, a.N, hi);
+  load_row_raw<D>(vf, V, a.ldv, ni, a.N, hi);
+  zero_past<D>(kf, ni, a.N);
+  zero_past<D>(vf, ni, a.N);
+  f32x16_t dk[DB], dv[DB];
+#pragma unroll
+  for (int blk = 0; blk < DB; ++blk) dk[blk] = dv[blk] = f32x16_t{};
+  const float c = a.scale_log2;
+  const Offsets<D> offs(lane);
+  if constexpr (VL) {
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) *reinterpret_cast<bf16x8_t *>(vrows[wave] + offs.row(ks)) = vf[ks];
+  }
+  if (nt > 0) {
     stash_rows(0, mbeg);
     wait_vmcnt<0>();
   }
@@ -758,10 +822,15 @@ __device__ __forceinline__ void bwd_dkdv(const BwppAttnArgs &a) {
     wait_vmcnt<0>();
     __syncthreads();
   }
-  if (ni < a.N) {
-    store_t<D>(dK, a.ldk, ni, dk, a.scale, hi);
-    store_t<D>(dV, a.ldv, ni, dv, 1.0f, hi);
-  }
+  // Staging: the wave's own V rows (VL), or its part of the ring, which is
+  // free once every wave has passed the last tile's barrier.
+  static_assert(VL || 4 * TB >= kW * kR * RB, "one 32-row staging region per wave fits the ring");
+  // Wave-uniform values and the lane id are formed afresh here (SGPRs and
+  // mbcnt), so that nothing extra stays live in VGPRs across the tile loop.
+  unsigned char *stage = VL ? &vrows[0][0] + wv * (uint32_t)(kR * RB) : &lds[0][0][0] + wv * (uint32_t)(kR * RB);
+  const uint32_t r0 = kb + wv * (uint32_t)kR;
+  store_rows<D>(dK, a.ldk, r0, a.N, dk, a.scale, (int)__lane_id(), stage);
+  store_rows<D>(dV, a.ldv, r0, a.N, dv, 1.0f, (int)__lane_id(), stage);
 }
 
 }  // namespace
