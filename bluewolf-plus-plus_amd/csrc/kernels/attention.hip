@@ -42,6 +42,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef short v4s_t __attribute__((ext_vector_type(4)));
 typedef short v8s_t __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
 
 namespace {
@@ -374,7 +375,10 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
   // O = O^T / l, staged through LDS ([query][d] bf16 per wave, 256-byte
   // rows, 16-byte chunk c of row q at c ^ (q & 15)), then stored with
   // 16-byte row chunks.  Without the swizzle the 32 rows a staging write
-  // touches at one column all fall on the same banks.
+  // touches at one column all fall on the same banks.  The row stores are
+  // non-temporal: O is not read again by this kernel, and written back
+  // from the caches later it took bandwidth from the next launch (C4
+  // 542 -> 530 us unmasked, 318 -> 301 causal, back to back).
   uint16_t *os = reinterpret_cast<uint16_t *>(smem) + (size_t)wave * kQW * D;
   // Natural-log log-sum-exp of the scaled scores when asked for: the sum of
   // exp(scale s) is 2^mrow * lrow (mrow in log2 units).
@@ -402,8 +406,8 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
     const uint32_t ql = (uint32_t)(q / kRowChunks), cc = (uint32_t)(q % kRowChunks);
     const uint32_t qo = q0 + ql;
     if (qo < a.M)
-      *reinterpret_cast<uint4 *>(O + (size_t)qo * a.ldo + 8u * cc) =
-          *reinterpret_cast<const uint4 *>(os + ql * D + 8u * (cc ^ (ql & 15u)));
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4_t *>(os + ql * D + 8u * (cc ^ (ql & 15u))),
+                                  reinterpret_cast<u32x4_t *>(O + (size_t)qo * a.ldo + 8u * cc));
   }
   __syncthreads();  // the block's next tile reuses smem
 }
@@ -754,8 +758,8 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
       const uint32_t ql = (uint32_t)(q / kRowChunks), cc = (uint32_t)(q % kRowChunks);
       const uint32_t qo = cur.q0 + ql;
       if (qo < a.M)
-        *reinterpret_cast<uint4 *>(cur.O + (size_t)qo * a.ldo + 8u * cc) =
-            *reinterpret_cast<const uint4 *>(os + ql * D + 8u * (cc ^ (ql & 15u)));
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4_t *>(os + ql * D + 8u * (cc ^ (ql & 15u))),
+                                    reinterpret_cast<u32x4_t *>(cur.O + (size_t)qo * a.ldo + 8u * cc));
     }
     s0 = (s0 + nkt) & 1u;
     cur = nxt;

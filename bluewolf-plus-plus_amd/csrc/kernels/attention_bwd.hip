@@ -273,7 +273,9 @@ __device__ __forceinline__ f32x16_t dot_rows_lds(const unsigned char *tile, cons
 // instruction wrote 16 bytes into each of 32 rows, and at C4 the dK / dV
 // pass's blocks spent 4.1 of their 144 us issuing them.  A wave's LDS
 // operations run in order, so the row reads see the writes without a wait
-// and the next call may reuse the region.
+// and the next call may reuse the region.  The stores are non-temporal:
+// with plain stores the outputs sat dirty in the caches and were written
+// back while the next pass streamed dS (the dQ pass 473 -> 414 us at C4).
 template <int D>
 __device__ __forceinline__ void store_rows(uint16_t *X, uint32_t ld, uint32_t row0, uint32_t rows,
                                            const f32x16_t (&acc)[D / 32], float f, int lane, unsigned char *stage) {
@@ -306,7 +308,8 @@ __device__ __forceinline__ void store_rows(uint16_t *X, uint32_t ld, uint32_t ro
 #pragma unroll
   for (int j = 0; j < 32 / RPI; ++j) {
     const int r = j * RPI + lane / CH;
-    if (row0 + (uint32_t)r < rows) *reinterpret_cast<u32x4_t *>(X + (size_t)(row0 + (uint32_t)r) * ld + 8 * ch) = u[j];
+    if (row0 + (uint32_t)r < rows)
+      __builtin_nontemporal_store(u[j], reinterpret_cast<u32x4_t *>(X + (size_t)(row0 + (uint32_t)r) * ld + 8 * ch));
   }
 }
 
