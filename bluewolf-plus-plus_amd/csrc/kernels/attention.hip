@@ -234,21 +234,36 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
     if constexpr (MASK) {
       // Key of register r in block kb is k0 + 4 lh + (32 kb + 8 (r >> 2) +
       // (r & 3)); visible iff that offset is below `lim` (key < N and, when
-      // causal, key <= query + diag).
+      // causal, key <= query + diag).  Wave-uniform per block: blocks past
+      // kbmax are all masked (their scores stay out of the max, and their
+      // probabilities are 0 below), and a block whose last key every query
+      // of the wave sees needs no per-element test.
       int64_t lim64 = (int64_t)a.N - (int64_t)(k0 + 4u * lh);
       if (CAUSAL) {
         const int64_t c64 = (int64_t)qi + diag + 1 - (int64_t)(k0 + 4u * lh);
         lim64 = c64 < lim64 ? c64 : lim64;
       }
       const int lim = (int)(lim64 < -1 ? -1 : (lim64 > kBKV ? kBKV : lim64));
+      int64_t vis = (int64_t)a.N - 1 - (int64_t)k0;  // last key offset every query of the wave sees
+      if (CAUSAL) {
+        const int64_t vc = (int64_t)q0 + diag - (int64_t)k0;
+        vis = vc < vis ? vc : vis;
+      }
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+      for (int kb = 0; kb < KB; ++kb) {
+        if (kb > kbmax) continue;
+        if ((int64_t)(32 * kb + 31) <= vis) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float x = (32 * kb + 8 * (r >> 2) + (r & 3)) < lim ? s[kb][r] : -INFINITY;
-          s[kb][r] = x;
-          mx = fmaxf(mx, x);
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float x = (32 * kb + 8 * (r >> 2) + (r & 3)) < lim ? s[kb][r] : -INFINITY;
+            s[kb][r] = x;
+            mx = fmaxf(mx, x);
+          }
         }
+      }
     } else {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
@@ -269,13 +284,15 @@ __device__ __forceinline__ void attn_bf16_d128_tile(const BwppAttnArgs &a, const
     const float muse = mrow == -INFINITY ? 0.0f : mrow;
     float sum = 0.0f;
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
+    for (int kb = 0; kb < KB; ++kb) {
+      if (MASK && kb > kbmax) continue;  // p = 0: adds nothing, and its P.V is skipped
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], c, -muse));
         s[kb][r] = p;
         sum += p;
       }
+    }
     {
       const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false);
       sum = __uint_as_float(r[0]) + __uint_as_float(r[1]);
@@ -612,20 +629,34 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
 
       float mx = -INFINITY;
       if constexpr (MASK) {
+        // As in attn_bf16_d128_tile: blocks past kbmax are left out, and a
+        // block every query of the wave sees whole needs no element test.
         int64_t lim64 = (int64_t)a.N - (int64_t)(k0 + 4u * lh);
         if (CAUSAL) {
           const int64_t c64 = (int64_t)qi + diag + 1 - (int64_t)(k0 + 4u * lh);
           lim64 = c64 < lim64 ? c64 : lim64;
         }
         const int lim = (int)(lim64 < -1 ? -1 : (lim64 > kBKV ? kBKV : lim64));
+        int64_t vis = (int64_t)a.N - 1 - (int64_t)k0;
+        if (CAUSAL) {
+          const int64_t vc = (int64_t)cur.q0 + diag - (int64_t)k0;
+          vis = vc < vis ? vc : vis;
+        }
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
+        for (int kb = 0; kb < KB; ++kb) {
+          if (kb > kbmax) continue;
+          if ((int64_t)(32 * kb + 31) <= vis) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float x = (32 * kb + 8 * (r >> 2) + (r & 3)) < lim ? s[kb][r] : -INFINITY;
-            s[kb][r] = x;
-            mx = fmaxf(mx, x);
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float x = (32 * kb + 8 * (r >> 2) + (r & 3)) < lim ? s[kb][r] : -INFINITY;
+              s[kb][r] = x;
+              mx = fmaxf(mx, x);
+            }
           }
+        }
       } else {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
@@ -644,13 +675,15 @@ __device__ __forceinline__ void attn_bf16_d128_persist(const BwppAttnArgs &a) {
       const float muse = mrow == -INFINITY ? 0.0f : mrow;
       float sum = 0.0f;
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+      for (int kb = 0; kb < KB; ++kb) {
+        if (MASK && kb > kbmax) continue;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], c, -muse));
           s[kb][r] = p;
           sum += p;
         }
+      }
       {
         const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false);
         sum = __uint_as_float(r[0]) + __uint_as_float(r[1]);
