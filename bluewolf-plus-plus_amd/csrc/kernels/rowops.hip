@@ -191,15 +191,17 @@ __device__ __forceinline__ void row_reg(const BwppRowArgs &a) {
   auto in_full = [&](uint32_t c) { return FULL || c + 4u <= cols; };
 
   // Loads the row of group `grp` (rows past the end re-read the last row;
-  // their results are never stored).
-  auto load_row = [&](uint32_t grp, float4 *v) {
+  // their results are never stored), and for the max grad its dy with it.
+  auto load_row = [&](uint32_t grp, float4 *v, float &dyv) {
     // The row is wave-uniform (a row is owned by whole waves): through
     // readfirstlane its base stays in SGPRs and the loads take the
     // SGPR-base + 32-bit lane offset form, with no 64-bit address VGPRs
     // (which the compiler otherwise recycled into the prefetch buffer,
     // waiting for all memory operations at the loop head).
     const uint32_t row = __builtin_amdgcn_readfirstlane(grp * G::kRows + sub);
-    const float *xr = a.x + (size_t)(row < a.rows ? row : a.rows - 1) * a.ld;
+    const uint32_t rr = row < a.rows ? row : a.rows - 1;
+    const float *xr = a.x + (size_t)rr * a.ld;
+    if constexpr (OP == OP_MAX_GRAD) dyv = a.dy[rr];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const uint32_t c = chunk_col(j);
@@ -239,7 +241,7 @@ __device__ __forceinline__ void row_reg(const BwppRowArgs &a) {
   }
 
   // Processes the row group `grp` held in v[] (reductions + stores).
-  auto process = [&](float4(&v)[VPT], uint32_t grp) {
+  auto process = [&](float4(&v)[VPT], uint32_t grp, float dyv) {
     const uint32_t row = __builtin_amdgcn_readfirstlane(grp * G::kRows + sub);  // wave-uniform
     const bool valid = row < a.rows;
     float *yr = a.y ? a.y + (size_t)(valid ? row : 0) * a.ld : nullptr;
@@ -397,7 +399,7 @@ __device__ __forceinline__ void row_reg(const BwppRowArgs &a) {
           if (a.argmax) a.argmax[row] = (mi == kNoIndex) ? -1 : (int32_t)mi;
         }
       } else {
-        const float gv = valid ? a.dy[row] : 0.0f;
+        const float gv = valid ? dyv : 0.0f;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
           const uint32_t c = chunk_col(j);
@@ -433,25 +435,26 @@ __device__ __forceinline__ void row_reg(const BwppRowArgs &a) {
   uint32_t grp = blockIdx.x;
   if (grp >= ngroups) return;  // block-uniform
   float4 va[VPT], vb[VPT];
-  load_row(grp, va);
+  float da = 0.0f, db = 0.0f;
+  load_row(grp, va, da);
   for (;;) {
     uint32_t next = grp + gridDim.x;
     if (next >= ngroups) {
-      process(va, grp);
+      process(va, grp, da);
       break;
     }
-    if (kPrefetch) load_row(next, vb);
-    process(va, grp);
-    if (!kPrefetch) load_row(next, vb);
+    if (kPrefetch) load_row(next, vb, db);
+    process(va, grp, da);
+    if (!kPrefetch) load_row(next, vb, db);
     grp = next;
     next = grp + gridDim.x;
     if (next >= ngroups) {
-      process(vb, grp);
+      process(vb, grp, db);
       break;
     }
-    if (kPrefetch) load_row(next, va);
-    process(vb, grp);
-    if (!kPrefetch) load_row(next, va);
+    if (kPrefetch) load_row(next, va, da);
+    process(vb, grp, db);
+    if (!kPrefetch) load_row(next, va, da);
     grp = next;
   }
 }
