@@ -323,19 +323,20 @@ __device__ __forceinline__ void gemm_bf16(const BwppGemmArgs &a) {
 // Register-free staging: every operand byte goes global -> LDS with
 // global_load_lds (16 bytes per lane; the lanes of one instruction fill
 // 1 KiB of LDS in lane order, each lane from its own global address), into
-// a ring of kStages stages of BK = 32.  Three K tiles are in flight while
-// the fourth is multiplied.
-//   K-contiguous operand ("KC": A, or B with TB): LDS [256 rows][32 k],
+// a ring of STAGES stages of BK = 32 (the 8-wave kernels: three, two K
+// tiles in flight while the third is multiplied).
+//   K-contiguous operand ("KC": A, or B with TB): LDS [rows][32 k],
 //     64-byte rows of four 16-byte chunks, chunk c of row r at
 //     c ^ ((r >> 2) & 3), so the 16 rows read by 16 lanes of a ds_read_b128
 //     hit 16 distinct 16-byte bank groups.
 //   MN-contiguous operand ("MNC": row-major B, or A with TA): LDS
-//     [32 k][256], 512-byte rows, chunk c of row k at c ^ (4 * (k & 3)); the
+//     [32 k][W], 2 W-byte rows, chunk c of row k at c ^ (4 * (k & 3)); the
 //     MFMA operand (8 consecutive k of one row/column per lane) is read with
 //     two ds_read_b64_tr_b16: in each 16-lane group, lane L fetches 4
 //     elements of k-row kb + L/4 at column c0 + 4 * (L % 4), and the
 //     hardware returns to lane j the 4 k-values of column c0 + j.
-// Needs M, N multiples of 256, K a multiple of 32, 16-byte aligned rows.
+// Needs M a multiple of 256, N of 256 (of 8 for the 384-wide tiles), K of
+// 32, and 16-byte aligned rows.
 
 typedef short v4s_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
@@ -347,15 +348,17 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-constexpr int kPipeStages = 4;
 constexpr int kPipeBK = 32;
-constexpr int kPipeTile = 256 * kPipeBK * 2;  // bytes of one operand tile
 
 __device__ __forceinline__ uint32_t kc_off(uint32_t row, uint32_t c) {
   return row * 64u + 16u * (c ^ ((row >> 2) & 3u));
 }
+// MN-contiguous tile W elements wide: 2 W-byte k-rows of W / 8 chunks (a
+// multiple of 16, so the XOR stays inside the row).
+template <int W>
 __device__ __forceinline__ uint32_t mnc_off(uint32_t k, uint32_t c) {
-  return k * 512u + 16u * (c ^ (4u * (k & 3u)));
+  static_assert(W % 128 == 0, "k-rows of a multiple of 16 chunks");
+  return k * (2u * W) + 16u * (c ^ (4u * (k & 3u)));
 }
 
 // 16 bytes per lane, global -> LDS (M0 holds the wave's LDS destination;
@@ -367,24 +370,59 @@ __device__ __forceinline__ void g2lds16(const void *gptr, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(gptr)
                : "memory");
 }
+// The same from a wave-uniform base (SGPRs) plus a 32-bit byte offset per
+// lane: one VGPR per lane instead of a 64-bit address.
+__device__ __forceinline__ void g2lds16_so(const void *sbase, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_addr), "v"(voff), "s"(sbase)
+               : "memory");
+}
 
 // Source of this lane's 16-byte chunk in 1 KiB block `blk` of an operand
-// tile whose first K index is 0 (the caller adds the K advance).
-template <bool MNC>
+// tile of W rows (KC) or W columns (MNC) whose first K index is 0 (the
+// caller adds the K advance).  CLAMP: rows (KC) or columns (MNC) from
+// `lim` on re-read the last ones (a tile that overhangs N; those results
+// are never stored).
+template <bool MNC, int W, bool CLAMP = false>
 __device__ __forceinline__ const uint16_t *tile_src(const uint16_t *g, uint32_t ld, uint32_t r0, uint32_t blk,
-                                                    int lane) {
+                                                    int lane, uint32_t lim = 0) {
   const uint32_t q = blk * 64u + (uint32_t)lane;
   if constexpr (!MNC) {
     const uint32_t row = q >> 2, c = (q & 3u) ^ ((row >> 2) & 3u);
-    return g + (size_t)(r0 + row) * ld + 8u * c;
+    uint32_t r = r0 + row;
+    if constexpr (CLAMP) r = min(r, lim - 1u);
+    return g + (size_t)r * ld + 8u * c;
   } else {
-    const uint32_t k = q >> 5, c = (q & 31u) ^ (4u * (k & 3u));
-    return g + (size_t)k * ld + r0 + 8u * c;
+    constexpr uint32_t kChunks = W / 8;
+    const uint32_t k = q / kChunks, c = (q % kChunks) ^ (4u * (k & 3u));
+    uint32_t col = r0 + 8u * c;
+    if constexpr (CLAMP) col = min(col, lim - 8u);
+    return g + (size_t)k * ld + col;
   }
 }
 
-// MFMA operand (8 bf16: rows rb + lane%32, k = 16*ks + 8*(lane/32) .. +7).
-template <bool MNC>
+// The same chunk as a byte offset from the tile's origin (row or column
+// r0 at K = 0), in 32-bit arithmetic: ld * 2 * (rows of a KC tile) must
+// stay below 2^32.
+template <bool MNC, int W, bool CLAMP = false>
+__device__ __forceinline__ uint32_t tile_off(uint32_t ld, uint32_t r0, uint32_t blk, int lane, uint32_t lim = 0) {
+  const uint32_t q = blk * 64u + (uint32_t)lane;
+  if constexpr (!MNC) {
+    const uint32_t row = q >> 2, c = (q & 3u) ^ ((row >> 2) & 3u);
+    uint32_t r = row;
+    if constexpr (CLAMP) r = min(r, lim - 1u - r0);
+    return 2u * (r * ld + 8u * c);
+  } else {
+    constexpr uint32_t kChunks = W / 8;
+    const uint32_t k = q / kChunks, c = (q % kChunks) ^ (4u * (k & 3u));
+    uint32_t col = 8u * c;
+    if constexpr (CLAMP) col = min(col, lim - 8u - r0);
+    return 2u * (k * ld + col);
+  }
+}
+
+// MFMA operand (8 bf16: rows rb + lane%32, k = 16*ks + 8*(lane/32) .. +7)
+// of a tile W rows (KC) or W columns (MNC) wide.
+template <bool MNC, int W>
 __device__ __forceinline__ bf16x8_t read_operand(const unsigned char *tile, uint32_t rb, int ks, int lane) {
   if constexpr (!MNC) {
     const uint32_t row = rb + (uint32_t)(lane & 31);
@@ -397,9 +435,9 @@ __device__ __forceinline__ bf16x8_t read_operand(const unsigned char *tile, uint
     const uint32_t sub = (col & 7u) * 2u;
     const uint32_t k0 = (uint32_t)(16 * ks) + 8u * (g >> 1) + (L >> 2);
     const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_v4s_t *)(tile + mnc_off(k0, c) + sub));
+        (lds_v4s_t *)(tile + mnc_off<W>(k0, c) + sub));
     const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_v4s_t *)(tile + mnc_off(k0 + 4u, c) + sub));
+        (lds_v4s_t *)(tile + mnc_off<W>(k0 + 4u, c) + sub));
     typedef short v8s_t __attribute__((ext_vector_type(8)));
     const v8s_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     return __builtin_bit_cast(bf16x8_t, v);
@@ -409,11 +447,14 @@ __device__ __forceinline__ bf16x8_t read_operand(const unsigned char *tile, uint
 template <bool V>
 using bool_tag = std::integral_constant<bool, V>;
 
-// WM x WN waves (4 or 8); each wave owns a (256/WM) x (256/WN) sub-tile.
+// 256 x BN output tile (BN 256 or 384), WM x WN waves (4 or 8); each wave
+// owns a (256/WM) x (BN/WN) sub-tile.  STAGES K tiles of 32 in the LDS
+// ring (STAGES - 1 in flight while one is multiplied).
 //
 // Schedule of one K tile (two 16-deep MFMA k-steps), per wave:
 //   phase A: the k-step-0 MFMAs, interleaved with the LDS reads of k-step 1
-//            and the DMA of K tile kt + 3 into the stage freed by kt - 1;
+//            and the DMA of K tile kt + STAGES - 1 into the stage freed by
+//            kt - 1;
 //   then:    lgkmcnt(0) (this wave is done reading tile kt), vmcnt down to
 //            the tiles younger than kt + 1, barrier (tile kt + 1 is in LDS
 //            for every wave, and nobody reads tile kt any more);
@@ -422,16 +463,34 @@ using bool_tag = std::integral_constant<bool, V>;
 // The MFMA pipe thus always has work queued while LDS reads and DMA issue,
 // and there is one barrier per K tile.  sched_barrier(0) pins the order the
 // source gives (the DMA is inline asm, which the scheduler cannot classify).
-template <bool TA, bool TB, int WM, int WN>
+//
+// BN = 384 (a 384-wide B tile: a sixth fewer L2 -> LDS bytes per FLOP than
+// 256 x 256, and fewer LDS operand bytes per MFMA): the ring's 40 KiB
+// stages fit three deep, the epilogue stages C through LDS in two halves
+// of 128 rows, and N need only be a multiple of 8 -- a tile column that
+// overhangs N re-reads B's last columns (or rows) and stores only n < N.
+template <bool TA, bool TB, int WM, int WN, int BN = 256, int STAGES = 4>
 __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
-  constexpr int BM = 256, BN = 256;
+  constexpr int BM = 256;
   constexpr int NW = WM * WN, NT = 64 * NW;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-  constexpr int LPW = 16 / NW;  // 1 KiB DMA blocks per wave per operand tile
-  constexpr int kStage = 2 * kPipeTile;
+  constexpr int kTileA = BM * kPipeBK * 2, kTileB = BN * kPipeBK * 2;  // bytes per operand tile
+  constexpr int LPA = kTileA / 1024 / NW, LPB = kTileB / 1024 / NW;     // 1 KiB DMA blocks per wave
+  static_assert(LPA * NW * 1024 == kTileA && LPB * NW * 1024 == kTileB, "DMA blocks split evenly over the waves");
+  static_assert(TN % 32 == 0 && TM % 32 == 0 && STAGES >= 2 && STAGES <= 4, "tile shape");
+  constexpr bool kEdgeN = BN != 256;
+  // Lean register use (the 8-wave 384-wide tile holds 192 accumulator
+  // VGPRs): DMA sources as 32-bit offsets from wave-uniform tile origins,
+  // and one set of A operands, each re-read for the next k-step as soon as
+  // its last MFMA of the current one has issued (MFMAs in A-operand order).
+  constexpr bool kLean = BN != 256;
+  constexpr int kStage = kTileA + kTileB;
   constexpr int kCld = BN + 8;
-  constexpr int kRing = kPipeStages * kStage;
-  constexpr int kEpi = BM * kCld * 2;
+  constexpr int kRing = STAGES * kStage;
+  constexpr int kHalves = BM * kCld * 2 + BN * 2 > 163840 ? 2 : 1;  // epilogue passes over the rows
+  static_assert(kHalves == 1 || WM == kHalves, "one wave row per epilogue half");
+  constexpr int kHR = BM / kHalves;  // rows per epilogue half
+  constexpr int kEpi = kHR * kCld * 2;
   constexpr int kBiasOff = kRing > kEpi ? kRing : kEpi;  // bias row (bf16) after both
   __shared__ __attribute__((aligned(1024))) unsigned char smem[kBiasOff + BN * 2];
 
@@ -451,24 +510,40 @@ __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
   const uint16_t *bias_s = reinterpret_cast<const uint16_t *>(smem + kBiasOff);
 
   // Per-lane DMA sources at K = 0, advanced by a fixed step per K tile.
-  const uint16_t *srcA[LPW], *srcB[LPW];
+  const uint16_t *srcA[kLean ? 1 : LPA], *srcB[kLean ? 1 : LPB];
+  uint32_t offA[kLean ? LPA : 1], offB[kLean ? LPB : 1];  // lean: bytes from baseA / baseB
+  const uint16_t *baseA = A + (TA ? (size_t)m0 : (size_t)m0 * a.lda);
+  const uint16_t *baseB = B + (TB ? (size_t)n0 * a.ldb : (size_t)n0);
 #pragma unroll
-  for (int i = 0; i < LPW; ++i) {
-    srcA[i] = tile_src<TA>(A, a.lda, m0, (uint32_t)(wave * LPW + i), lane);
-    srcB[i] = tile_src<!TB>(B, a.ldb, n0, (uint32_t)(wave * LPW + i), lane);
+  for (int i = 0; i < LPA; ++i) {
+    if constexpr (kLean) offA[i] = tile_off<TA, BM>(a.lda, m0, (uint32_t)(wave * LPA + i), lane);
+    else srcA[i] = tile_src<TA, BM>(A, a.lda, m0, (uint32_t)(wave * LPA + i), lane);
+  }
+#pragma unroll
+  for (int i = 0; i < LPB; ++i) {
+    if constexpr (kLean) offB[i] = tile_off<!TB, BN, kEdgeN>(a.ldb, n0, (uint32_t)(wave * LPB + i), lane, a.N);
+    else srcB[i] = tile_src<!TB, BN>(B, a.ldb, n0, (uint32_t)(wave * LPB + i), lane);
   }
   const size_t stepA = TA ? (size_t)kPipeBK * a.lda : (size_t)kPipeBK;
   const size_t stepB = TB ? (size_t)kPipeBK : (size_t)kPipeBK * a.ldb;
-  const uint32_t lds0 =
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)smem + (uint32_t)(wave * LPW) * 1024u;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)smem;
+  const uint32_t ldsA = lds_base + (uint32_t)(wave * LPA) * 1024u;
+  const uint32_t ldsB = lds_base + (uint32_t)kTileA + (uint32_t)(wave * LPB) * 1024u;
 
-  // DMA instruction d (0 .. 2*LPW-1) of K tile kt.
+  // DMA instruction d (0 .. LPA+LPB-1) of K tile kt.
   auto dma = [&](int d, uint32_t kt) {
-    const uint32_t st = lds0 + (kt % kPipeStages) * kStage;
-    if (d < LPW)
-      g2lds16(srcA[d] + kt * stepA, st + (uint32_t)d * 1024u);
-    else
-      g2lds16(srcB[d - LPW] + kt * stepB, st + kPipeTile + (uint32_t)(d - LPW) * 1024u);
+    const uint32_t st = (kt % STAGES) * kStage;
+    if constexpr (kLean) {
+      if (d < LPA)
+        g2lds16_so(baseA + kt * stepA, offA[d], ldsA + st + (uint32_t)d * 1024u);
+      else
+        g2lds16_so(baseB + kt * stepB, offB[d - LPA], ldsB + st + (uint32_t)(d - LPA) * 1024u);
+    } else {
+      if (d < LPA)
+        g2lds16(srcA[d] + kt * stepA, ldsA + st + (uint32_t)d * 1024u);
+      else
+        g2lds16(srcB[d - LPA] + kt * stepB, ldsB + st + (uint32_t)(d - LPA) * 1024u);
+    }
   };
 
   f32x16_t acc[FN][FM];
@@ -479,48 +554,58 @@ __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // fa/fb[0]: operands of k-step 0, [1]: of k-step 1.
-  bf16x8_t fa[2][FM], fb[2][FN];
-  constexpr int kReads = FM + FN, kMfma = FM * FN, kDma = 2 * LPW;
+  // fa/fb[0]: operands of k-step 0, [1]: of k-step 1 (lean: one fa set).
+  bf16x8_t fa[kLean ? 1 : 2][FM], fb[2][FN];
+  constexpr int kReads = FM + FN, kMfma = FM * FN, kDma = LPA + LPB;
   static_assert(kReads <= kMfma && kDma <= kMfma, "interleave needs an MFMA slot per read and DMA");
+  // Wait until at most the y youngest K tiles' DMA are still in flight.
+  auto wait_younger = [&](uint32_t y) {
+    if constexpr (STAGES >= 4) {
+      if (y >= 2) {
+        wait_vmcnt<2 * kDma>();
+        return;
+      }
+    }
+    if (STAGES >= 3 && y >= 1) wait_vmcnt<kDma>();
+    else wait_vmcnt<0>();
+  };
 
-  auto stage_ptr = [&](uint32_t kt) { return smem + (kt % kPipeStages) * kStage; };
+  auto stage_ptr = [&](uint32_t kt) { return smem + (kt % STAGES) * kStage; };
   auto read = [&](auto buf, int r, const unsigned char *As, int ks) {
     constexpr int b = decltype(buf)::value ? 1 : 0;
     if (r < FM)
-      fa[b][r] = read_operand<TA>(As, (uint32_t)(wm * TM + r * 32), ks, lane);
+      fa[kLean ? 0 : b][r] = read_operand<TA, BM>(As, (uint32_t)(wm * TM + r * 32), ks, lane);
     else
-      fb[b][r - FM] = read_operand<!TB>(As + kPipeTile, (uint32_t)(wn * TN + (r - FM) * 32), ks, lane);
+      fb[b][r - FM] = read_operand<!TB, BN>(As + kTileA, (uint32_t)(wn * TN + (r - FM) * 32), ks, lane);
   };
   auto mfma = [&](auto buf, int s) {
     constexpr int b = decltype(buf)::value ? 1 : 0;
-    const int i = s / FM, j = s % FM;
-    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][i], fa[b][j], acc[i][j], 0, 0, 0);
+    const int i = kLean ? s % FN : s / FM, j = kLean ? s / FN : s % FM;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][i], fa[kLean ? 0 : b][j], acc[i][j], 0, 0, 0);
   };
 
-  // The tile's 256 bias values (512 bytes, 16-byte aligned) are copied to
-  // LDS by the first half of wave 0, ahead of its first K tile, so the
-  // prologue wait and barrier publish them and the epilogue never waits on a
-  // global load.
-  if (add && wave == 0 && lane < BN / 8)
-    g2lds16(bias + n0 + 8 * lane,
-            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)smem + (uint32_t)kBiasOff);
+  // The tile's BN bias values (16-byte aligned) are copied to LDS by the
+  // first lanes of wave 0, ahead of its first K tile, so the prologue wait
+  // and barrier publish them and the epilogue never waits on a global load.
+  if (add && wave == 0 && lane < BN / 8) {
+    uint32_t nb = n0 + 8u * (uint32_t)lane;
+    if constexpr (kEdgeN) nb = min(nb, a.N - 8u);
+    g2lds16(bias + nb, lds_base + (uint32_t)kBiasOff);
+  }
 #pragma unroll
-  for (int st = 0; st < kPipeStages - 1; ++st)
+  for (int st = 0; st < STAGES - 1; ++st)
     if ((uint32_t)st < nk) {
 #pragma unroll
       for (int d = 0; d < kDma; ++d) dma(d, (uint32_t)st);
     }
-  if (nk >= 3) wait_vmcnt<2 * kDma>();
-  else if (nk == 2) wait_vmcnt<kDma>();
-  else wait_vmcnt<0>();
+  wait_younger(nk >= (uint32_t)(STAGES - 1) ? (uint32_t)(STAGES - 2) : (nk > 0 ? nk - 1 : 0u));
   __syncthreads();
   if (nk > 0) {
 #pragma unroll
     for (int r = 0; r < kReads; ++r) read(bool_tag<false>{}, r, stage_ptr(0), 0);
   }
 
-  // One K tile; DMA: issue tile kt + 3, NEXT: a tile kt + 1 exists.
+  // One K tile; DMA: issue tile kt + STAGES - 1, NEXT: a tile kt + 1 exists.
   auto ktile = [&](uint32_t kt, auto dma_tag, auto next_tag) {
     constexpr bool kDmaOn = decltype(dma_tag)::value, kNext = decltype(next_tag)::value;
     const unsigned char *cur = stage_ptr(kt);
@@ -529,24 +614,31 @@ __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
     for (int s = 0; s < kMfma; ++s) {
       mfma(bool_tag<false>{}, s);
       __builtin_amdgcn_sched_barrier(0);
-      if (s < kReads) {
+      if constexpr (kLean) {
+        if (s < FN) {
+          read(bool_tag<true>{}, FM + s, cur, 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (s % FN == FN - 1) {  // the last MFMA of fa[s / FN] has issued
+          read(bool_tag<true>{}, s / FN, cur, 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else if (s < kReads) {
         read(bool_tag<true>{}, s, cur, 1);
         __builtin_amdgcn_sched_barrier(0);
       }
       if constexpr (kDmaOn) {
         if (s < kDma) {
-          dma(s, kt + kPipeStages - 1);
+          dma(s, kt + STAGES - 1);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
     if constexpr (kNext) {
       // Tiles issued after kt + 1 may stay in flight.
-      const uint32_t younger = min(nk - 2 - kt, (uint32_t)(kPipeStages - 2));
+      const uint32_t younger = min(nk - 2 - kt, (uint32_t)(STAGES - 2));
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): done reading tile kt
-      if (younger >= 2) wait_vmcnt<2 * kDma>();
-      else if (younger == 1) wait_vmcnt<kDma>();
-      else wait_vmcnt<0>();
+      wait_younger(younger);
       __syncthreads();
     }
     const unsigned char *nxt = stage_ptr(kt + 1);
@@ -555,7 +647,16 @@ __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
     for (int s = 0; s < kMfma; ++s) {
       mfma(bool_tag<true>{}, s);
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (kNext) {
+      if constexpr (kNext && kLean) {
+        if (s < FN) {
+          read(bool_tag<false>{}, FM + s, nxt, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (s % FN == FN - 1) {
+          read(bool_tag<false>{}, s / FN, nxt, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else if constexpr (kNext) {
         if (s < kReads) {
           read(bool_tag<false>{}, s, nxt, 0);
           __builtin_amdgcn_sched_barrier(0);
@@ -565,53 +666,60 @@ __device__ __forceinline__ void gemm_bf16_pipe(const BwppGemmArgs &a) {
   };
 
   uint32_t kt = 0;
-  for (; kt + kPipeStages - 1 < nk; ++kt) ktile(kt, bool_tag<true>{}, bool_tag<true>{});
+  for (; kt + STAGES - 1 < nk; ++kt) ktile(kt, bool_tag<true>{}, bool_tag<true>{});
   for (; kt + 1 < nk; ++kt) ktile(kt, bool_tag<false>{}, bool_tag<true>{});
   if (kt < nk) ktile(kt, bool_tag<false>{}, bool_tag<false>{});
   __syncthreads();
 
-  // Epilogue through LDS (see gemm_bf16).
+  // Epilogue through LDS (see gemm_bf16), in kHalves passes of kHR rows.
   uint16_t *cs = reinterpret_cast<uint16_t *>(smem);
+  uint16_t *C = static_cast<uint16_t *>(a.c);
   const int lrow = lane & 31, lhalf = lane >> 5;
+  constexpr int kRowChunks = BN / 8;
 #pragma unroll
-  for (int i = 0; i < FN; ++i) {
+  for (int hv = 0; hv < kHalves; ++hv) {
+    if (hv > 0) __syncthreads();  // the previous half has left LDS
+    if (kHalves == 1 || wm == hv) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int nl = wn * TN + i * 32 + q * 8 + lhalf * 4;
-      float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (add) {
-        const uint2 raw = *reinterpret_cast<const uint2 *>(bias_s + nl);
-        bv[0] = __uint_as_float(raw.x << 16);
-        bv[1] = __uint_as_float(raw.x & 0xffff0000u);
-        bv[2] = __uint_as_float(raw.y << 16);
-        bv[3] = __uint_as_float(raw.y & 0xffff0000u);
-      }
+      for (int i = 0; i < FN; ++i) {
 #pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        const int ml = wm * TM + j * 32 + lrow;
-        float v[4];
+        for (int q = 0; q < 4; ++q) {
+          const int nl = wn * TN + i * 32 + q * 8 + lhalf * 4;
+          float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          if (add) {
+            const uint2 raw = *reinterpret_cast<const uint2 *>(bias_s + nl);
+            bv[0] = __uint_as_float(raw.x << 16);
+            bv[1] = __uint_as_float(raw.x & 0xffff0000u);
+            bv[2] = __uint_as_float(raw.y << 16);
+            bv[3] = __uint_as_float(raw.y & 0xffff0000u);
+          }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float t = acc[i][j][q * 4 + e] + bv[e];
-          if (act) t = silu(t);
-          v[e] = t;
+          for (int j = 0; j < FM; ++j) {
+            const int ml = wm * TM - hv * kHR + j * 32 + lrow;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float t = acc[i][j][q * 4 + e] + bv[e];
+              if (act) t = silu(t);
+              v[e] = t;
+            }
+            uint2 o;
+            o.x = pack_bf16x2(v[0], v[1]);
+            o.y = pack_bf16x2(v[2], v[3]);
+            *reinterpret_cast<uint2 *>(cs + ml * kCld + nl) = o;
+          }
         }
-        uint2 o;
-        o.x = pack_bf16x2(v[0], v[1]);
-        o.y = pack_bf16x2(v[2], v[3]);
-        *reinterpret_cast<uint2 *>(cs + ml * kCld + nl) = o;
       }
     }
-  }
-  __syncthreads();
-  uint16_t *C = static_cast<uint16_t *>(a.c);
-  constexpr int kRowChunks = BN / 8;
+    __syncthreads();
 #pragma unroll 4
-  for (int it = 0; it < BM * kRowChunks / NT; ++it) {
-    const int q = tid + it * NT;
-    const int row = q / kRowChunks, c = q % kRowChunks;
-    *reinterpret_cast<uint4 *>(C + (size_t)(m0 + row) * a.ldc + n0 + c * 8) =
-        *reinterpret_cast<const uint4 *>(cs + row * kCld + c * 8);
+    for (int it = 0; it < kHR * kRowChunks / NT; ++it) {
+      const int q = tid + it * NT;
+      const int row = q / kRowChunks, c = q % kRowChunks;
+      if (!kEdgeN || n0 + (uint32_t)c * 8u < a.N)
+        *reinterpret_cast<uint4 *>(C + (size_t)(m0 + hv * kHR + row) * a.ldc + n0 + c * 8) =
+            *reinterpret_cast<const uint4 *>(cs + row * kCld + c * 8);
+    }
   }
 }
 
@@ -1192,12 +1300,23 @@ extern "C" __global__ __launch_bounds__(256) void bwpp_gemm_f32_splitk_reduce(co
     else                                                                                  \
       gemm_bf16_pipe<TA, TB, 2, 2>(a);                                                    \
   }
-// 8-wave (2 per SIMD) variant of the pipelined full-tile kernel.
+// 8-wave (2 per SIMD) variant of the pipelined full-tile kernel, with a
+// three-stage ring: 1-1.5 % faster than four stages on C3 (same bits; one
+// tile fewer in flight), two stages 20 % slower.
 #define BWPP_GEMM_BF16_W8(TA, TB)                                                          \
   extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(512, 512),            \
                                        amdgpu_waves_per_eu(2, 2))) void                  \
       bwpp_gemm_bf16w8_t##TA##TB##_f(const BwppGemmArgs a) {                              \
-    gemm_bf16_pipe<TA, TB, 2, 4>(a);                                                      \
+    gemm_bf16_pipe<TA, TB, 2, 4, 256, 3>(a);                                              \
+  }
+// 256 x 384 tiles: 8 waves of 128 x 96 (two per SIMD), three-stage ring.
+// Row-major A only: with a transposed A the compiler spills (40 / 311
+// VGPRs for t10 / t11), so those stay on the 256 x 256 kernels.
+#define BWPP_GEMM_BF16_X384(TA, TB)                                                        \
+  extern "C" __global__ __attribute__((amdgpu_flat_work_group_size(512, 512),            \
+                                       amdgpu_waves_per_eu(2, 2))) void                  \
+      bwpp_gemm_bf16x384w8_t##TA##TB##_f(const BwppGemmArgs a) {                          \
+    gemm_bf16_pipe<TA, TB, 2, 4, 384, 3>(a);                                              \
   }
 #define BWPP_GEMM_F32(TA, TB, EDGE, SUF)                                                   \
   extern "C" __global__ __launch_bounds__(256) void bwpp_gemm_f32_t##TA##TB##_##SUF(     \
@@ -1219,6 +1338,8 @@ BWPP_GEMM_BF16_W8(0, 0)
 BWPP_GEMM_BF16_W8(0, 1)
 BWPP_GEMM_BF16_W8(1, 0)
 BWPP_GEMM_BF16_W8(1, 1)
+BWPP_GEMM_BF16_X384(0, 0)
+BWPP_GEMM_BF16_X384(0, 1)
 BWPP_GEMM_ALL(BWPP_GEMM_F32)
 #define BWPP_GEMM_F32_SPLIT(TA, TB)                                                        \
   extern "C" __global__ __launch_bounds__(256) void bwpp_gemm_f32_t##TA##TB##_s(         \

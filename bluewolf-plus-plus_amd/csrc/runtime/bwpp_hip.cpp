@@ -123,6 +123,9 @@ struct BwppHip {
   std::string scratch_why;
   uint32_t gemm_group_m = 8;  // BWPP_GEMM_GROUP_M
   uint32_t gemm_waves = 8;    // BWPP_GEMM_WAVES: 4 or 8 waves for full bf16 tiles
+  // bf16 256 x 384 tiles (8 waves), row-major A: [trans_b]
+  hipFunction_t gemm_bf16_x384[2] = {};
+  uint32_t gemm_bn = 0;  // BWPP_GEMM_BN: bf16 full-tile width 256 or 384 (0: chosen per shape)
   uint32_t gemm_splitk = 1;   // BWPP_GEMM_SPLITK=0 turns fp32 split-K off
   uint32_t attn_zigzag = 1;  // BWPP_ATTN_ZIGZAG=0: fp32 causal passes always heaviest-first
   uint32_t gemm_f32_pipe = 1;  // BWPP_GEMM_F32_PIPE: fp32 full tiles 0 staged, 1 auto, 2 ring4, 3 ring2
@@ -248,6 +251,10 @@ BwppHipStatus resolve_all(BwppHip *h) {
     for (int tb = 0; tb < 2; ++tb) {
       const std::string n = "bwpp_gemm_bf16w8_t" + std::to_string(ta) + std::to_string(tb) + "_f";
       if ((s = resolve(h, n, &h->gemm_bf16_w8[ta][tb])) != BWPP_HIP_OK) return s;
+      if (ta == 0) {
+        const std::string nx = "bwpp_gemm_bf16x384w8_t0" + std::to_string(tb) + "_f";
+        if ((s = resolve(h, nx, &h->gemm_bf16_x384[tb])) != BWPP_HIP_OK) return s;
+      }
       const std::string ns = std::string("bwpp_gemm_f32_t") + char('0' + ta) + char('0' + tb) + "_s";
       if ((s = resolve(h, ns, &h->gemm_f32_split[ta][tb])) != BWPP_HIP_OK) return s;
       for (int sp = 0; sp < 2; ++sp) {
@@ -424,6 +431,10 @@ BwppHipStatus bwpp_hip_create(BwppHip **out, int device, const char *code_object
   if (const char *cfg = getenv("BWPP_ROW_CFG")) h->row_cfg_override = atoi(cfg);
   if (const char *gc = getenv("BWPP_ROW_GRID")) h->row_grid_cap = (uint32_t)strtoul(gc, nullptr, 10);
   if (const char *gw = getenv("BWPP_GEMM_WAVES")) h->gemm_waves = (uint32_t)strtoul(gw, nullptr, 10) == 4 ? 4 : 8;
+  if (const char *bn = getenv("BWPP_GEMM_BN")) {
+    const uint32_t v = (uint32_t)strtoul(bn, nullptr, 10);
+    h->gemm_bn = v == 256 || v == 384 ? v : 0u;
+  }
   if (const char *sk = getenv("BWPP_GEMM_SPLITK")) h->gemm_splitk = atoi(sk) != 0 ? 1u : 0u;
   if (const char *zz = getenv("BWPP_ATTN_ZIGZAG")) h->attn_zigzag = atoi(zz) != 0 ? 1u : 0u;
   if (const char *fp = getenv("BWPP_GEMM_F32_PIPE")) h->gemm_f32_pipe = (uint32_t)std::min(std::max(atoi(fp), 0), 3);
@@ -840,6 +851,20 @@ BwppHipStatus matmul_impl(BwppHip *h, const void *a, const void *b, void *c, con
   g.ldc2 = ldc2;
   const uint64_t tiles = (uint64_t)g.tiles_m * g.tiles_n;
   if (tiles > 0x7fffffffull) return fail(h, BWPP_HIP_ERR_UNSUPPORTED, "matmul: too many tiles");
+  // bf16 256 x 384 tiles: N a multiple of 8 (a tile column that overhangs
+  // N re-reads B's last columns and stores only n < N); the DMA addresses
+  // are 32-bit offsets from each tile's origin.  On C3 they run even with
+  // the 256 x 256 kernel (a higher clock, less matrix-pipe busy time), so
+  // they are taken where that one cannot run -- N not a multiple of 256,
+  // which would otherwise go to the register-staged edge kernel -- or when
+  // BWPP_GEMM_BN=384 asks.
+  const bool wide_ok = bf16 && !ta && vec && (!use_bias || aligned16(bias)) && p.M % BM == 0 && p.K % BK == 0 &&
+                       p.N % 8 == 0 && h->gemm_waves == 8 && 384ull * 2ull * std::max(lda, ldb) < (1ull << 31);
+  if (wide_ok && (h->gemm_bn == 384 || (h->gemm_bn == 0 && p.N % BN != 0))) {
+    g.tiles_n = (p.N + 383) / 384;
+    const uint64_t wt = (uint64_t)g.tiles_m * g.tiles_n;
+    return launch(h, h->gemm_bf16_x384[tb], (uint32_t)wt, 1, 1, 512, g);
+  }
   if (bf16 && full && h->gemm_waves == 8)
     return launch(h, h->gemm_bf16_w8[ta][tb], (uint32_t)tiles, 1, 1, 512, g);
   // fp32 full tiles: one of three kernels, optionally with K split into S

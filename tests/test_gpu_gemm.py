@@ -225,6 +225,81 @@ def test_full_tile_kernels(oracle, monkeypatch, ta, tb, waves):
         be.close()
 
 
+@pytest.mark.parametrize("tb", [0, 1])
+@pytest.mark.parametrize("M,N,K", [(512, 768, 32 * 7), (256, 1000, 96), (768, 392, 32), (256, 11008, 64),
+                                   (512, 384, 64)])
+def test_wide_tile_kernels(oracle, monkeypatch, M, N, K, tb):
+    """The 256 x 384 full-tile kernels (BWPP_GEMM_BN=384), both B
+    orientations: N not a multiple of 384 (the last tile column overhangs N:
+    B's last columns are re-read and only n < N stored), one and two K tiles
+    (fewer than the ring's stages), and C3's column count.  Against the
+    oracle; bit-identical to the 256 x 256 kernel where that one runs (each
+    output takes the same MFMAs over K in the same order)."""
+    torch = _torch()
+    monkeypatch.setenv("BWPP_GEMM_BN", "384")
+    be = bwpp.HipBackend(0)
+    be.set_stream(torch.cuda.current_stream())
+    ref_be = None
+    try:
+        a = synth.normal((M, K), 23, 0)
+        b = synth.normal((K, N), 23, 1)
+        bias = synth.normal((N,), 23, 2)
+        ad, ah = bf16_dev(a)
+        bd, bh = bf16_dev(stored(b, tb))
+        biasd, biash = bf16_dev(bias)
+        bh = bh.T.copy() if tb else bh
+        c = run(be, bwpp.DType.BF16, ad, bd, biasd, M, N, K, 3, 0, tb)
+        assert be.last_kernel == f"bwpp_gemm_bf16x384w8_t0{tb}_f", be.last_kernel
+        got = bf16_host(c)
+        want = oracle.matmul(ah, bh, biash, apply_silu=True, apply_bias=True)
+        assert rel_max_err(got, want) <= BF16_TOL
+        if N % 256 == 0:
+            monkeypatch.setenv("BWPP_GEMM_BN", "256")
+            ref_be = bwpp.HipBackend(0)
+            ref_be.set_stream(torch.cuda.current_stream())
+            c2 = run(ref_be, bwpp.DType.BF16, ad, bd, biasd, M, N, K, 3, 0, tb)
+            assert ref_be.last_kernel == f"bwpp_gemm_bf16w8_t0{tb}_f", ref_be.last_kernel
+            assert torch.equal(c.view(torch.int16), c2.view(torch.int16))
+    finally:
+        be.close()
+        if ref_be is not None:
+            ref_be.close()
+
+
+@pytest.mark.parametrize("bn,M,N,K,ta,want", [
+    ("", 512, 768, 64, 0, "bwpp_gemm_bf16w8_t00_f"),        # N a multiple of 256
+    ("", 512, 1000, 64, 0, "bwpp_gemm_bf16x384w8_t00_f"),   # N a multiple of 8 only
+    ("256", 512, 1000, 64, 0, "bwpp_gemm_bf16_t00_e"),      # wide tiles refused
+    ("", 512, 1000, 64, 1, "bwpp_gemm_bf16_t10_e"),         # transposed A: no wide kernel
+    ("", 512, 1004, 64, 0, "bwpp_gemm_bf16_t00_e"),         # N not a multiple of 8
+    ("384", 512, 768, 64, 0, "bwpp_gemm_bf16x384w8_t00_f"), # asked for
+])
+def test_bf16_kernel_choice(oracle, monkeypatch, bn, M, N, K, ta, want):
+    """Which bf16 kernel a shape takes (by name), with the result against the
+    oracle."""
+    torch = _torch()
+    if bn:
+        monkeypatch.setenv("BWPP_GEMM_BN", bn)
+    else:
+        monkeypatch.delenv("BWPP_GEMM_BN", raising=False)
+    be = bwpp.HipBackend(0)
+    be.set_stream(torch.cuda.current_stream())
+    try:
+        a = synth.normal((M, K), 29, 0)
+        b = synth.normal((K, N), 29, 1)
+        bias = synth.normal((N,), 29, 2)
+        ad, ah = bf16_dev(stored(a, ta))
+        bd, bh = bf16_dev(b)
+        biasd, biash = bf16_dev(bias)
+        ah = ah.T.copy() if ta else ah
+        c = run(be, bwpp.DType.BF16, ad, bd, biasd, M, N, K, 3, ta, 0)
+        assert be.last_kernel == want, be.last_kernel
+        want_c = oracle.matmul(ah, bh, biash, apply_silu=True, apply_bias=True)
+        assert rel_max_err(bf16_host(c), want_c) <= BF16_TOL
+    finally:
+        be.close()
+
+
 @pytest.mark.parametrize("M,N,K,ta,tb", [(128, 128, 4096, 1, 0), (256, 384, 2048, 0, 0), (128, 256, 4000, 0, 1),
                                          (384, 128, 1056, 1, 1), (1024, 1024, 4096, 1, 0)])
 @pytest.mark.parametrize("epi,silu,add", [(0, False, False), (3, True, True)])
