@@ -56,13 +56,7 @@ C2_BYTES = {
     "reduce_max": ROWS * COLS * F + ROWS * F + ROWS * 4,
     "reduce_max_grad": ROWS * COLS * F + ROWS * F + ROWS * COLS * F,
 }
-C2_KERNEL = {  # kernel symbol each op launches at this shape (rowops.hip)
-    "softmax": "bwpp_row_softmax_v2_w8_f",
-    "layernorm": "bwpp_row_layernorm_v4_w4_f",
-    "rmsnorm": "bwpp_row_rmsnorm_v4_w4_f",
-    "reduce_max": "bwpp_row_max_v4_w4_f",
-    "reduce_max_grad": "bwpp_row_maxgrad_v4_w4_f",
-}
+C2_KERNEL = {}  # kernel symbol each op launched (filled by time_c2_ops from the library)
 
 
 def host_info():
@@ -188,6 +182,7 @@ def time_c2_ops(bench, reps):
     for op in C2_BYTES:
         for i in range(bench.nbuf):
             bench.launch(op, i)
+        C2_KERNEL[op] = bench.be.last_kernel
         t = _launch_times_ms(torch, lambda i: bench.launch(op, i % bench.nbuf), reps, group=10)
         out[op] = (float(np.median(t)), float(np.mean(t)))
     return out
@@ -649,7 +644,10 @@ def _extras_c3f32(be, torch, seed, iters, orc, out):
     us = _events_us(torch, lambda: be.dispatch_matmul(a1, b1, c1, None, p), iters)
     # 4 output tiles: the cost model splits K, so one call is the split-K
     # ring GEMM and the reduce that sums its partials (the last kernel).
-    c1e = {"kernel": be.last_kernel, "us_per_call": round(us, 2),
+    c1k = be.last_kernel
+    if c1k == "bwpp_gemm_f32_splitk_reduce":
+        c1k = be.recent_kernel(1) + " + " + c1k
+    c1e = {"kernel": c1k, "us_per_call": round(us, 2),
            "TFLOP_s": round(2.0 * 256 ** 3 / us / 1e6, 2)}
     if orc is not None:
         ah, bh = a1.cpu().numpy(), b1.cpu().numpy()

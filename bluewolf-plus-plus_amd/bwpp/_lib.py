@@ -126,6 +126,7 @@ SIGNATURES = {
     "bwpp_hip_status_string": (c_char_p, [c_int]),
     "bwpp_hip_device_cus": (c_int, [_P]),
     "bwpp_hip_last_kernel": (c_char_p, [_P]),
+    "bwpp_hip_recent_kernel": (c_char_p, [_P, c_int]),
     "bwpp_hip_arena_init": (c_int, [_P, POINTER(Arena), c_size_t]),
     "bwpp_hip_arena_reset": (None, [POINTER(Arena)]),
     "bwpp_hip_arena_alloc": (_P, [POINTER(Arena), c_size_t, c_size_t]),

@@ -105,6 +105,10 @@ class HipBackend:
         """Symbol of the last kernel this handle launched ('' if none)."""
         return self.lib.bwpp_hip_last_kernel(self._h).decode()
 
+    def recent_kernel(self, back: int) -> str:
+        """Symbol of the launch `back` launches before the last (0..3; '' if none)."""
+        return self.lib.bwpp_hip_recent_kernel(self._h, back).decode()
+
     # --------------------------------------------------------- operators
     def dispatch_matmul(self, a, b, c, bias, params: MatmulParams):
         self._check(self.lib.bwpp_hip_dispatch_matmul(

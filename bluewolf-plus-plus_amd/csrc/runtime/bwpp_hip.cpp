@@ -65,6 +65,7 @@ struct BwppHip {
   std::unordered_map<hipFunction_t, uint32_t> max_threads;  // per resolved kernel
   std::unordered_map<hipFunction_t, std::string> names;     // symbol of each resolved kernel
   const std::string *last_kernel = nullptr;                 // symbol of the last launch
+  const std::string *recent[4] = {};                        // the last four launches, newest first
   std::string err;
   int row_cfg_override = -1;  // BWPP_ROW_CFG: index into kRowCfgs (tuning)
   uint32_t row_grid_cap = 0;  // BWPP_ROW_GRID: max blocks per row launch (0 = per-op default)
@@ -330,6 +331,8 @@ BwppHipStatus launch(BwppHip *h, hipFunction_t f, uint32_t gx, uint32_t gy, uint
   if (e != hipSuccess) return fail(h, BWPP_HIP_ERR_HIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
   const auto nm = h->names.find(f);
   h->last_kernel = nm == h->names.end() ? nullptr : &nm->second;
+  for (int i = 3; i > 0; --i) h->recent[i] = h->recent[i - 1];
+  h->recent[0] = h->last_kernel;
   return BWPP_HIP_OK;
 }
 
@@ -340,11 +343,17 @@ inline uint32_t eff_ld(uint32_t ld, uint32_t cols) { return ld ? ld : cols; }
 // wave each (no cross-wave reduction, no barrier), and so do the norms' and
 // softmax's rows up to 1536; up to 2048 the norms and reduce_max take two
 // waves, and up to 3072 the norms take two waves of 8 chunks.  Longer rows
-// get a block of 4 waves (8 for softmax from 4096 columns, and for every
-// operator above 16384), with the float4 chunks per thread doubled until the
-// row fits (<= 16, i.e. 32768 columns).  These are the fastest layouts
-// measured on MI355X at 768 - 4096 columns (one wave per row: RMSNorm over
-// 4096 x 1024 9.2 -> 6.5 us, LayerNorm over 4096 x 768 15.2 -> 7.0 us).
+// get a block of 4 waves or, where that measured faster, 8 (every operator
+// above 16384 columns; softmax and RMSNorm from 4096, LayerNorm above
+// 4096, the reduce_max gradient from 4096 to 8192; never reduce_max), with
+// the float4 chunks per thread doubled until the row fits (<= 16, i.e.
+// 32768 columns).  These are the fastest layouts measured on MI355X at 768
+// - 16384 columns (one wave per row: RMSNorm over 4096 x 1024 9.2 -> 6.5
+// us, LayerNorm over 4096 x 768 15.2 -> 7.0 us; eight waves instead of
+// four, same bytes: RMSNorm 44.0 -> 43.5 / 46.7 -> 45.5 / 50.7 -> 45.8 us
+// at 4096 / 8192 / 16384 columns, LayerNorm 47.5 -> 46.3 / 51.3 -> 46.3 at
+// 8192 / 16384, the gradient 43.7 -> 43.0 / 45.0 -> 44.6 at 4096 / 8192
+// but 47.5 -> 49.2 at 16384, reduce_max 21.0 -> 24.1 at 4096).
 int pick_row_cfg(const BwppHip *h, RowOpId op, uint32_t cols, bool vec_ok) {
   if (!vec_ok) return -1;
   if (h->row_cfg_override >= 0 && h->row_cfg_override < kRowNCfg &&
@@ -358,7 +367,11 @@ int pick_row_cfg(const BwppHip *h, RowOpId op, uint32_t cols, bool vec_ok) {
   if (cols <= 2048 && op != ROW_SOFTMAX) return find_cfg(4, 2);
   if (cols <= 3072 && norm) return find_cfg(8, 2);
   if (cols > 32768) return -1;
-  const int wpr = (cols > 16384 || (op == ROW_SOFTMAX && cols >= 4096)) ? 8 : 4;
+  bool eight = cols > 16384;
+  if (op == ROW_SOFTMAX || op == ROW_RMSNORM) eight = eight || cols >= 4096;
+  if (op == ROW_LAYERNORM) eight = eight || cols > 4096;
+  if (op == ROW_MAXGRAD) eight = eight || (cols >= 4096 && cols <= 8192);
+  const int wpr = eight ? 8 : 4;
   int vpt = 1;
   while (row_capacity(RowCfg{vpt, wpr}) < cols) vpt *= 2;
   return find_cfg(vpt, wpr);
@@ -518,6 +531,10 @@ int bwpp_hip_device_cus(const BwppHip *h) { return h ? h->cus : 0; }
 
 const char *bwpp_hip_last_kernel(const BwppHip *h) {
   return h && h->last_kernel ? h->last_kernel->c_str() : "";
+}
+
+const char *bwpp_hip_recent_kernel(const BwppHip *h, int back) {
+  return h && back >= 0 && back < 4 && h->recent[back] ? h->recent[back]->c_str() : "";
 }
 
 // ---------------------------------------------------------------- memory

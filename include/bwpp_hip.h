@@ -191,6 +191,11 @@ int bwpp_hip_device_cus(const BwppHip *h);
 /* Symbol of the last kernel this handle launched ("" if none): which
  * variant a dispatch chose.  No reference counterpart (diagnostics). */
 const char *bwpp_hip_last_kernel(const BwppHip *h);
+/* Symbol of the launch `back` launches before the last (0 = the last, at
+ * most 3; "" if none): the kernels of a dispatch that launches several,
+ * e.g. a split-K GEMM and its reduce.  No reference counterpart
+ * (diagnostics). */
+const char *bwpp_hip_recent_kernel(const BwppHip *h, int back);
 
 /* ---- device memory ---- */
 

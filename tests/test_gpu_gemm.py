@@ -485,6 +485,9 @@ def test_f32_kernel_choice_c5_shapes(be, M, N, K, ta, tb, want):
     kern = be.last_kernel
     if be.cus == 256:
         assert kern == ("bwpp_gemm_f32_splitk_reduce" if want == "split" else want), kern
+    if kern == "bwpp_gemm_f32_splitk_reduce":  # the split GEMM itself launched just before
+        first = be.recent_kernel(1)
+        assert first.startswith("bwpp_gemm_f32") and first.endswith(f"_t{ta}{tb}_s"), first
     ad = (a.t() if ta else a).double()
     bd = (b.t() if tb else b).double()
     ref = ad @ bd

@@ -146,13 +146,16 @@ def test_golden_row_vectors(be, golden):
 # (cols, {op: (float4 chunks per thread, waves per row)}) of the default
 # layout choice: one wave per row up to 1024 columns (1536 for the norms
 # and softmax), two up to 2048 (not softmax) and, for the norms, two waves
-# of 8 chunks up to 3072; four beyond, eight for softmax from 4096.
+# of 8 chunks up to 3072; four beyond, eight for softmax and RMSNorm from
+# 4096, LayerNorm above 4096 and the reduce_max gradient from 4096 to 8192.
 LAYOUTS = [
-    (1000, {"rmsnorm": (4, 1), "layernorm": (4, 1), "softmax": (4, 1), "max": (4, 1)}),
-    (1536, {"rmsnorm": (8, 1), "layernorm": (8, 1), "softmax": (8, 1), "max": (4, 2)}),
-    (2048, {"rmsnorm": (4, 2), "layernorm": (4, 2), "softmax": (2, 4), "max": (4, 2)}),
-    (3072, {"rmsnorm": (8, 2), "layernorm": (8, 2), "softmax": (4, 4), "max": (4, 4)}),
-    (4096, {"rmsnorm": (4, 4), "layernorm": (4, 4), "softmax": (2, 8), "max": (4, 4)}),
+    (1000, {"rmsnorm": (4, 1), "layernorm": (4, 1), "softmax": (4, 1), "max": (4, 1), "maxgrad": (4, 1)}),
+    (1536, {"rmsnorm": (8, 1), "layernorm": (8, 1), "softmax": (8, 1), "max": (4, 2), "maxgrad": (4, 2)}),
+    (2048, {"rmsnorm": (4, 2), "layernorm": (4, 2), "softmax": (2, 4), "max": (4, 2), "maxgrad": (4, 2)}),
+    (3072, {"rmsnorm": (8, 2), "layernorm": (8, 2), "softmax": (4, 4), "max": (4, 4), "maxgrad": (4, 4)}),
+    (4096, {"rmsnorm": (2, 8), "layernorm": (4, 4), "softmax": (2, 8), "max": (4, 4), "maxgrad": (2, 8)}),
+    (8192, {"rmsnorm": (4, 8), "layernorm": (4, 8), "softmax": (4, 8), "max": (8, 4), "maxgrad": (4, 8)}),
+    (16384, {"rmsnorm": (8, 8), "layernorm": (8, 8), "softmax": (8, 8), "max": (16, 4), "maxgrad": (16, 4)}),
 ]
 
 
@@ -182,6 +185,10 @@ def test_default_layouts(be, oracle, cols, want):
     wm, wi = oracle.reduce_max(x, 1)
     assert_bits_equal(host(mv), wm)
     assert np.array_equal(host(ix), wi)
+    dy = np.random.default_rng(cols).standard_normal(rows).astype(np.float32)
+    be.dispatch_reduce_max_grad_argmax(xd, None, dev(dy), y, bwpp.ReduceParams(rows, cols, cols, 1))
+    assert be.last_kernel == name("maxgrad", want["maxgrad"])
+    assert_bits_equal(host(y), oracle.reduce_max_grad(dy, x.shape, x=x, axis=1))
 
 
 @pytest.mark.parametrize("idx", range(len(ROW_CFGS)))
