@@ -304,14 +304,17 @@ def pmc_summary(dirs):
     return "\n".join(lines)
 
 
-def stream_ceiling(torch, nbuf=3, reps=20, kind="copy"):
-    """The box's HBM ceiling for the C2 byte pattern: the best GB/s of
-    plain non-temporal 128-bit copies of X[8192 x 4096] fp32 (the bytes one
-    read+write row operator moves; kind "read": the same loads without
-    stores, reduce_max's pattern), over float4-per-thread x block x grid
-    (tests/hip/stream.hip, loaded through HIP's module API), each timed as
-    the median of groups of back-to-back launches over `nbuf` rotating
-    buffer pairs."""
+def stream_ceiling(torch, nbuf=3, reps=20, kind="copy", final_reps=70):
+    """The box's HBM ceiling for the C2 byte pattern: plain non-temporal
+    128-bit copies of X[8192 x 4096] fp32 (the bytes one read+write row
+    operator moves; kind "read": the same loads without stores,
+    reduce_max's pattern) from tests/hip/stream.hip, loaded through HIP's
+    module API.  A sweep over float4-per-thread x block x grid (each shape
+    the median of `reps` launches in groups of 10 over `nbuf` rotating
+    buffer pairs) picks the fastest shape; that shape is then timed again
+    over `final_reps` launches, the same count and statistic as each C2
+    operator, and that median is the ceiling (the sweep's best, a maximum
+    over ~50 noisy medians, is reported beside it as sweep_best_GB_s)."""
     import ctypes
     path = os.path.join(ROOT, "tests", "hip", "bwpp_stream.hsaco")
     if not os.path.exists(path):
@@ -356,7 +359,24 @@ def stream_ceiling(torch, nbuf=3, reps=20, kind="copy"):
                 gbs = (2 if kind == "copy" else 1) * ROWS * COLS * F / us / 1e3
                 if best is None or gbs > best["GB_s"]:
                     best = {"GB_s": round(gbs, 1), "us_per_launch": round(us, 2), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-                            "config": {"float4_per_thread": v, "block": block, "grid": grid}}
+                            "config": {"float4_per_thread": v, "block": block, "grid": grid},
+                            "_fn": fn, "_params": params, "_args": args}  # args: the structs params point at
+    if best is None:
+        return None
+    fn, params, keep, cfg = best.pop("_fn"), best.pop("_params"), best.pop("_args"), best["config"]
+
+    def launch_best(i):
+        rc = hip.hipModuleLaunchKernel(fn, cfg["grid"], 1, 1, cfg["block"], 1, 1, 0, ctypes.c_void_p(stream),
+                                       params[i % nbuf], None)
+        if rc != 0:
+            raise RuntimeError(f"stream launch failed ({rc})")
+
+    t = _launch_times_ms(torch, launch_best, final_reps, group=10)
+    del keep
+    us = float(np.median(t)) * 1e3
+    gbs = (2 if kind == "copy" else 1) * ROWS * COLS * F / us / 1e3
+    best["sweep_best_GB_s"] = best["GB_s"]
+    best.update({"GB_s": round(gbs, 1), "us_per_launch": round(us, 2), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
     torch.cuda.synchronize()
     hip.hipModuleUnload(mod)
     best["kernel"] = f"tests/hip/stream.hip bwpp_stream_{kind}_v*"
@@ -918,8 +938,8 @@ def main():
         "ops": ops,
         "host": host_info(),
     }
-    ceil = stream_ceiling(torch)
-    rceil = stream_ceiling(torch, kind="read")
+    ceil = stream_ceiling(torch, final_reps=args.op_reps)
+    rceil = stream_ceiling(torch, kind="read", final_reps=args.op_reps)
     if ceil:
         out["stream_ceiling"] = ceil
         if rceil:
